@@ -1,0 +1,389 @@
+// Gated-delta-rule verify scan with per-token state tape (gfx950).
+//
+// The recurrence is independent per state row (b, hv, dv): row dv of the
+// [Dv, Dk] state needs only its own Dk values plus the per-token k, q (shared
+// by the head), v[dv], g and beta.  The reference's Metal kernel exploits the
+// same independence (dflash_mlx/custom_qwen35_model.py:33-74: one simdgroup
+// per dv row, simd_sum over dk).
+//
+// CDNA4 mapping:
+//   - 16 lanes (one DPP row) own one state row; lane s holds Dk/16 fp32 of the
+//     row in VGPRs for the whole token loop.  The dk reductions (k.S and q.S)
+//     are 4 DPP adds inside the 16-lane row: no LDS, no barriers.
+//   - Element ownership is interleaved: chunk c of lane s covers
+//     dk = c*16*VEC + s*VEC .. +VEC-1, so one store instruction of a row's 16
+//     lanes writes 16*VEC*4 contiguous bytes (256 B for Dk % 64 == 0).
+//   - A wavefront holds 4 row groups, each carrying R rows; a 256-thread
+//     workgroup covers 16*R consecutive-by-stride rows of one (b, hv) head.
+//   - The tape dominates the bytes (T state copies per head), so it is
+//     written with non-temporal dwordx4 stores as soon as each token is done.
+//   - The inputs of token t+1 are loaded before token t is computed.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dflash_gdn.h"
+#include "device_common.h"
+#include "host_common.h"
+
+namespace dflash {
+namespace {
+
+struct ScanParams {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const float* g;
+  const float* beta;
+  const float* state_in;
+  uint16_t* out;
+  float* final_state;
+  float* tape;
+  const int32_t* lengths;
+  int64_t q_sb, q_st, q_sh;
+  int64_t k_sb, k_st, k_sh;
+  int64_t v_sb, v_st, v_sh;
+  int64_t g_sb, g_st;
+  int64_t b_sb, b_st;
+  int64_t tape_tstride;  // elements between tape[t] and tape[t+1] = B*Hv*Dv*Dk
+  int B, T, Hv, Dv;
+  int rep;         // Hv / Hk
+  int row_blocks;  // Dv / (16 * R)
+  int items;       // B * Hv * row_blocks
+};
+
+template <int VEC>
+struct BF16Vec;
+template <>
+struct BF16Vec<4> {
+  typedef uint2 raw;
+  __device__ static raw load(const uint16_t* p) {
+    return *reinterpret_cast<const uint2*>(p);
+  }
+  __device__ static void unpack(raw r, float* f) {
+    f[0] = bf16_lo(r.x);
+    f[1] = bf16_hi(r.x);
+    f[2] = bf16_lo(r.y);
+    f[3] = bf16_hi(r.y);
+  }
+};
+template <>
+struct BF16Vec<2> {
+  typedef uint32_t raw;
+  __device__ static raw load(const uint16_t* p) {
+    return *reinterpret_cast<const uint32_t*>(p);
+  }
+  __device__ static void unpack(raw r, float* f) {
+    f[0] = bf16_lo(r);
+    f[1] = bf16_hi(r);
+  }
+};
+
+template <int VEC>
+__device__ __forceinline__ void load_f32(const float* p, float* f) {
+  if constexpr (VEC == 4) {
+    f32x4 x = *reinterpret_cast<const f32x4*>(p);
+    f[0] = x.x; f[1] = x.y; f[2] = x.z; f[3] = x.w;
+  } else {
+    f32x2 x = *reinterpret_cast<const f32x2*>(p);
+    f[0] = x.x; f[1] = x.y;
+  }
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_f32(float* p, const float* f) {
+  if constexpr (VEC == 4) {
+    f32x4 x = {f[0], f[1], f[2], f[3]};
+    *reinterpret_cast<f32x4*>(p) = x;
+  } else {
+    f32x2 x = {f[0], f[1]};
+    *reinterpret_cast<f32x2*>(p) = x;
+  }
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_f32_stream(float* p, const float* f) {
+  if constexpr (VEC == 4) {
+    f32x4 x = {f[0], f[1], f[2], f[3]};
+    __builtin_nontemporal_store(x, reinterpret_cast<f32x4*>(p));
+  } else {
+    f32x2 x = {f[0], f[1]};
+    __builtin_nontemporal_store(x, reinterpret_cast<f32x2*>(p));
+  }
+}
+
+template <int DK, int R>
+__global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
+  constexpr int VEC = (DK % 64 == 0) ? 4 : 2;
+  constexpr int NCH = DK / (16 * VEC);
+  constexpr int ROWS_WG = 16 * R;
+  typedef BF16Vec<VEC> LD;
+
+  const int sub = threadIdx.x & 15;  // lane within the 16-lane row group
+  const int gi = threadIdx.x >> 4;   // row group within the workgroup, 0..15
+  const bool has_q = p.q != nullptr;
+  const bool has_tape = p.tape != nullptr;
+
+  for (int item = blockIdx.x; item < p.items; item += gridDim.x) {
+    const int rb = item % p.row_blocks;
+    const int bh = item / p.row_blocks;
+    const int b = bh / p.Hv;
+    const int hv = bh - b * p.Hv;
+    const int hk = hv / p.rep;
+    int n = p.T;
+    if (p.lengths != nullptr) n = min(max(p.lengths[b], 0), p.T);
+
+    int row[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) row[r] = rb * ROWS_WG + r * 16 + gi;
+
+    // Load the state rows.
+    float S[R][NCH][VEC];
+    const int64_t head_base = (int64_t)bh * p.Dv * DK;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+        load_f32<VEC>(p.state_in + head_base + (int64_t)row[r] * DK +
+                          c * 16 * VEC + sub * VEC,
+                      S[r][c]);
+
+    const uint16_t* kp = p.k + b * p.k_sb + hk * p.k_sh + sub * VEC;
+    const uint16_t* qp =
+        has_q ? p.q + b * p.q_sb + hk * p.q_sh + sub * VEC : nullptr;
+    const uint16_t* vp = p.v + b * p.v_sb + hv * p.v_sh;
+    const float* gp = p.g + b * p.g_sb + hv;
+    const float* bp = p.beta + b * p.b_sb + hv;
+    float* tp = has_tape ? p.tape + head_base + sub * VEC : nullptr;
+
+    // Prefetch registers for the next token.
+    typename LD::raw k_raw[NCH], q_raw[NCH];
+    uint16_t v_raw[R];
+    float g_nx = 0.f, b_nx = 0.f;
+    auto fetch = [&](int t) {
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) k_raw[c] = LD::load(kp + t * p.k_st + c * 16 * VEC);
+      if (has_q) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) q_raw[c] = LD::load(qp + t * p.q_st + c * 16 * VEC);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) v_raw[r] = vp[t * p.v_st + row[r]];
+      g_nx = gp[t * p.g_st];
+      b_nx = bp[t * p.b_st];
+    };
+    if (n > 0) fetch(0);
+
+    float okeep[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) okeep[r] = 0.f;
+
+    for (int t = 0; t < n; ++t) {
+      float kf[NCH][VEC], qf[NCH][VEC], vr[R];
+#pragma unroll
+      for (int c = 0; c < NCH; ++c) LD::unpack(k_raw[c], kf[c]);
+      if (has_q) {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) LD::unpack(q_raw[c], qf[c]);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) vr[r] = bf16_bits_to_f32(v_raw[r]);
+      const float gt = g_nx;
+      const float bt = b_nx;
+      fetch(min(t + 1, n - 1));
+
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        // S <- g*S ; kv = S.k
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            S[r][c][e] *= gt;
+            acc = fmaf(S[r][c][e], kf[c][e], acc);
+          }
+        const float kv = row16_sum(acc);
+        const float d = (vr[r] - kv) * bt;
+        // S += k (x) d
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) S[r][c][e] = fmaf(kf[c][e], d, S[r][c][e]);
+        if (has_q) {
+          float o = 0.f;
+#pragma unroll
+          for (int c = 0; c < NCH; ++c)
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) o = fmaf(S[r][c][e], qf[c][e], o);
+          o = row16_sum(o);
+          if (sub == (t & 15)) okeep[r] = o;
+        }
+        if (has_tape) {
+          float* dst = tp + (int64_t)t * p.tape_tstride + (int64_t)row[r] * DK;
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) store_f32_stream<VEC>(dst + c * 16 * VEC, S[r][c]);
+        }
+      }
+
+      // Lane s of each row group holds out for token (t & ~15) + s; flush
+      // every 16 tokens and at the end.
+      if (has_q && (((t & 15) == 15) || (t == n - 1))) {
+        const int t0 = t & ~15;
+        if (sub <= (t & 15)) {
+          uint16_t* op = p.out + (((int64_t)b * p.T + t0 + sub) * p.Hv + hv) * p.Dv;
+#pragma unroll
+          for (int r = 0; r < R; ++r) op[row[r]] = f32_to_bf16_rne(okeep[r]);
+        }
+      }
+    }
+
+    if (p.final_state != nullptr) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+          store_f32<VEC>(p.final_state + head_base + (int64_t)row[r] * DK +
+                             c * 16 * VEC + sub * VEC,
+                         S[r][c]);
+    }
+  }
+}
+
+template <int DK>
+hipError_t launch_dk(const ScanParams& base, int R, int grid, hipStream_t s) {
+  ScanParams p = base;
+  p.row_blocks = p.Dv / (16 * R);
+  p.items = p.B * p.Hv * p.row_blocks;
+  const int blocks = grid > 0 ? min(grid, p.items) : p.items;
+  switch (R) {
+    case 1: hipLaunchKernelGGL((gdn_scan_kernel<DK, 1>), dim3(blocks), dim3(256), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((gdn_scan_kernel<DK, 2>), dim3(blocks), dim3(256), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((gdn_scan_kernel<DK, 4>), dim3(blocks), dim3(256), 0, s, p); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// Rows per lane group.  More rows per group amortise the k/q loads and bf16
+// unpacking over more state; fewer keep more waves in flight.
+int pick_rows(int B, int Hv, int Dv) {
+  const int64_t heads = (int64_t)B * Hv;
+  for (int R : {2, 1}) {
+    if (Dv % (16 * R) != 0) continue;
+    // Keep at least ~4 waves per SIMD worth of workgroups on 256 CUs.
+    if (heads * (Dv / (16 * R)) >= 4096 || R == 1) return R;
+  }
+  return 1;
+}
+
+int scan_impl(const void* q, const void* k, const void* v, const float* g,
+              const float* beta, const float* state_in, void* out,
+              float* final_state, float* tape, const int32_t* lengths, int B,
+              int T, int Hk, int Hv, int Dk, int Dv, const int64_t* strides,
+              void* stream) {
+  if (B < 0 || T < 0 || Hk <= 0 || Hv <= 0 || Dk <= 0 || Dv <= 0) return DFLASH_ERR_SHAPE;
+  if (Hv % Hk != 0) return DFLASH_ERR_SHAPE;
+  if (Dv % 16 != 0) return DFLASH_ERR_UNSUPPORTED;
+  if (!(Dk == 32 || Dk == 64 || Dk == 96 || Dk == 128 || Dk == 192 || Dk == 256))
+    return DFLASH_ERR_UNSUPPORTED;
+  if ((int64_t)B * Hv * (Dv / 16) > INT32_MAX) return DFLASH_ERR_SHAPE;
+  if (B == 0) return DFLASH_OK;
+  if (T == 0) {
+    // Nothing to scan: the final state is the initial state.
+    if (state_in == nullptr) return DFLASH_ERR_NULL;
+    if (final_state != nullptr && final_state != state_in) {
+      hipError_t e = hipMemcpyAsync(final_state, state_in,
+                                    sizeof(float) * (size_t)B * Hv * Dv * Dk,
+                                    hipMemcpyDeviceToDevice, (hipStream_t)stream);
+      return e == hipSuccess ? DFLASH_OK : (int)e;
+    }
+    return DFLASH_OK;
+  }
+  if (k == nullptr || v == nullptr || g == nullptr || beta == nullptr || state_in == nullptr)
+    return DFLASH_ERR_NULL;
+  if ((q == nullptr) != (out == nullptr)) return DFLASH_ERR_NULL;
+  if (out == nullptr && final_state == nullptr && tape == nullptr) return DFLASH_ERR_NULL;
+
+  ScanParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.g = g;
+  p.beta = beta;
+  p.state_in = state_in;
+  p.out = static_cast<uint16_t*>(out);
+  p.final_state = final_state;
+  p.tape = tape;
+  p.lengths = lengths;
+  p.B = B;
+  p.T = T;
+  p.Hv = Hv;
+  p.Dv = Dv;
+  p.rep = Hv / Hk;
+  p.tape_tstride = (int64_t)B * Hv * Dv * Dk;
+  if (strides != nullptr) {
+    p.q_sb = strides[0]; p.q_st = strides[1]; p.q_sh = strides[2];
+    p.k_sb = strides[3]; p.k_st = strides[4]; p.k_sh = strides[5];
+    p.v_sb = strides[6]; p.v_st = strides[7]; p.v_sh = strides[8];
+    p.g_sb = strides[9]; p.g_st = strides[10];
+    p.b_sb = strides[11]; p.b_st = strides[12];
+  } else {
+    p.q_sh = Dk; p.q_st = (int64_t)Hk * Dk; p.q_sb = (int64_t)T * Hk * Dk;
+    p.k_sh = p.q_sh; p.k_st = p.q_st; p.k_sb = p.q_sb;
+    p.v_sh = Dv; p.v_st = (int64_t)Hv * Dv; p.v_sb = (int64_t)T * Hv * Dv;
+    p.g_st = Hv; p.g_sb = (int64_t)T * Hv;
+    p.b_st = Hv; p.b_sb = (int64_t)T * Hv;
+  }
+  // Vector loads of q/k need VEC-element alignment of every row start;
+  // state rows need 16-byte (or 8-byte) alignment.
+  const int vec = (Dk % 64 == 0) ? 4 : 2;
+  const uintptr_t kmask = (uintptr_t)(vec * 2 - 1);
+  if (((uintptr_t)k & kmask) || (p.k_sb % vec) || (p.k_st % vec) || (p.k_sh % vec))
+    return DFLASH_ERR_ALIGN;
+  if (q != nullptr &&
+      (((uintptr_t)q & kmask) || (p.q_sb % vec) || (p.q_st % vec) || (p.q_sh % vec)))
+    return DFLASH_ERR_ALIGN;
+  const uintptr_t smask = (uintptr_t)(vec * 4 - 1);
+  if (((uintptr_t)state_in & smask) || ((uintptr_t)final_state & smask) ||
+      ((uintptr_t)tape & smask))
+    return DFLASH_ERR_ALIGN;
+  if (((uintptr_t)v & 1) || ((uintptr_t)out & 1) || ((uintptr_t)g & 3) || ((uintptr_t)beta & 3))
+    return DFLASH_ERR_ALIGN;
+
+  const int R = pick_rows(B, Hv, Dv);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  switch (Dk) {
+    case 32: e = launch_dk<32>(p, R, 0, s); break;
+    case 64: e = launch_dk<64>(p, R, 0, s); break;
+    case 96: e = launch_dk<96>(p, R, 0, s); break;
+    case 128: e = launch_dk<128>(p, R, 0, s); break;
+    case 192: e = launch_dk<192>(p, R, 0, s); break;
+    default: e = launch_dk<256>(p, R, 0, s); break;
+  }
+  return e == hipSuccess ? DFLASH_OK : (int)e;
+}
+
+}  // namespace
+}  // namespace dflash
+
+extern "C" int dflash_gdn_verify_scan(const void* q, const void* k, const void* v,
+                                      const float* g, const float* beta,
+                                      const float* state_in, void* out,
+                                      float* final_state, float* tape,
+                                      const int32_t* lengths, int B, int T,
+                                      int Hk, int Hv, int Dk, int Dv,
+                                      const int64_t* strides, void* stream) {
+  return dflash::scan_impl(q, k, v, g, beta, state_in, out, final_state, tape,
+                           lengths, B, T, Hk, Hv, Dk, Dv, strides, stream);
+}
+
+extern "C" int dflash_gdn_replay(const void* k, const void* v, const float* g,
+                                 const float* beta, const float* state_in,
+                                 float* state_out, const int32_t* lengths, int B,
+                                 int T, int Hk, int Hv, int Dk, int Dv,
+                                 const int64_t* strides, void* stream) {
+  if (state_out == nullptr) return DFLASH_ERR_NULL;
+  return dflash::scan_impl(nullptr, k, v, g, beta, state_in, nullptr, state_out,
+                           nullptr, lengths, B, T, Hk, Hv, Dk, Dv, strides, stream);
+}

@@ -1,0 +1,241 @@
+// Greedy verify accept: vocabulary argmax + longest agreeing draft prefix.
+//
+// Reference semantics: sample_tokens with temperature 0 is mx.argmax over the
+// last axis (dflash_mlx/runtime.py:22-29); the accept is
+// longest_prefix_match(block[1:], posterior[:-1]) with the bonus token
+// posterior[matched] (runtime.py:41-47, :145-147, :163).
+//
+// Two launches, both HBM-bound on the logits read:
+//   1. argmax_partial: grid (splits, B*N).  Each workgroup reduces one
+//      contiguous slice of one logits row to a 64-bit key
+//      (order-preserving value bits << 32 | ~index), so a plain integer max
+//      gives the largest value and, among equal values, the lowest index.
+//   2. accept_finalize: one wavefront per sequence merges the split keys of
+//      its N rows, writes the posterior tokens, then finds the first draft
+//      mismatch with a 64-lane ballot.
+// Only the small matched/bonus/posterior arrays are written; the host reads
+// them once per verify step.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dflash_gdn.h"
+#include "device_common.h"
+#include "host_common.h"
+
+namespace dflash {
+namespace {
+
+constexpr int kArgmaxThreads = 256;
+
+template <typename T>
+__device__ __forceinline__ float load_logit(const T* p);
+template <>
+__device__ __forceinline__ float load_logit<float>(const float* p) { return *p; }
+template <>
+__device__ __forceinline__ float load_logit<uint16_t>(const uint16_t* p) {
+  return bf16_bits_to_f32(*p);
+}
+struct F16Tag { uint16_t bits; };
+template <>
+__device__ __forceinline__ float load_logit<F16Tag>(const F16Tag* p) {
+  return f16_bits_to_f32(p->bits);
+}
+
+// Scan 16 bytes holding 16/sizeof(T) consecutive logits starting at idx.
+template <typename T>
+__device__ __forceinline__ uint64_t key16(u32x4 raw, int idx, uint64_t best);
+template <>
+__device__ __forceinline__ uint64_t key16<float>(u32x4 raw, int idx, uint64_t best) {
+  best = u64_max(best, argmax_key(__uint_as_float(raw.x), idx + 0));
+  best = u64_max(best, argmax_key(__uint_as_float(raw.y), idx + 1));
+  best = u64_max(best, argmax_key(__uint_as_float(raw.z), idx + 2));
+  best = u64_max(best, argmax_key(__uint_as_float(raw.w), idx + 3));
+  return best;
+}
+template <>
+__device__ __forceinline__ uint64_t key16<uint16_t>(u32x4 raw, int idx, uint64_t best) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    best = u64_max(best, argmax_key(bf16_lo(w[j]), idx + 2 * j));
+    best = u64_max(best, argmax_key(bf16_hi(w[j]), idx + 2 * j + 1));
+  }
+  return best;
+}
+template <>
+__device__ __forceinline__ uint64_t key16<F16Tag>(u32x4 raw, int idx, uint64_t best) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    best = u64_max(best, argmax_key(f16_bits_to_f32((uint16_t)(w[j] & 0xffffu)), idx + 2 * j));
+    best = u64_max(best, argmax_key(f16_bits_to_f32((uint16_t)(w[j] >> 16)), idx + 2 * j + 1));
+  }
+  return best;
+}
+
+template <typename T, bool VECTOR>
+__global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(
+    const T* __restrict__ logits, int64_t bstride, int64_t rstride, int N, int V,
+    int chunk, int splits, uint64_t* __restrict__ part) {
+  const int row = blockIdx.x;
+  const int split = blockIdx.y;
+  const int b = row / N;
+  const int i = row - b * N;
+  const T* base = logits + (int64_t)b * bstride + (int64_t)i * rstride;
+  const int start = split * chunk;
+  const int end = min(V, start + chunk);
+  uint64_t best = 0;
+  if (VECTOR) {
+    constexpr int PER = 16 / sizeof(T);
+    const int nvec = (end - start) / PER;
+    const u32x4* vbase = reinterpret_cast<const u32x4*>(base + start);
+    int j = threadIdx.x;
+    // Four independent 16-byte loads in flight per lane.
+    for (; j + 3 * kArgmaxThreads < nvec; j += 4 * kArgmaxThreads) {
+      u32x4 r0 = __builtin_nontemporal_load(vbase + j);
+      u32x4 r1 = __builtin_nontemporal_load(vbase + j + kArgmaxThreads);
+      u32x4 r2 = __builtin_nontemporal_load(vbase + j + 2 * kArgmaxThreads);
+      u32x4 r3 = __builtin_nontemporal_load(vbase + j + 3 * kArgmaxThreads);
+      best = key16<T>(r0, start + j * PER, best);
+      best = key16<T>(r1, start + (j + kArgmaxThreads) * PER, best);
+      best = key16<T>(r2, start + (j + 2 * kArgmaxThreads) * PER, best);
+      best = key16<T>(r3, start + (j + 3 * kArgmaxThreads) * PER, best);
+    }
+    for (; j < nvec; j += kArgmaxThreads) best = key16<T>(vbase[j], start + j * PER, best);
+    for (int idx = start + nvec * PER + threadIdx.x; idx < end; idx += kArgmaxThreads)
+      best = u64_max(best, argmax_key(load_logit<T>(base + idx), idx));
+  } else {
+    for (int idx = start + threadIdx.x; idx < end; idx += kArgmaxThreads)
+      best = u64_max(best, argmax_key(load_logit<T>(base + idx), idx));
+  }
+  best = wave_max_u64(best);
+  __shared__ uint64_t wbest[kArgmaxThreads / 64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  if (lane == 0) wbest[wave] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint64_t m = wbest[0];
+#pragma unroll
+    for (int w = 1; w < kArgmaxThreads / 64; ++w) m = u64_max(m, wbest[w]);
+    part[(int64_t)row * splits + split] = m;
+  }
+}
+
+__global__ __launch_bounds__(64) void accept_finalize_kernel(
+    const uint64_t* __restrict__ part, int splits, int N,
+    const int32_t* __restrict__ draft, int64_t dstride, int n_draft,
+    int32_t* __restrict__ posterior, int32_t* __restrict__ matched,
+    int32_t* __restrict__ bonus) {
+  extern __shared__ int32_t post[];
+  const int b = blockIdx.x;
+  const int lane = threadIdx.x;
+  for (int i = 0; i < N; ++i) {
+    const uint64_t* pr = part + ((int64_t)b * N + i) * splits;
+    uint64_t best = 0;
+    for (int s = lane; s < splits; s += 64) best = u64_max(best, pr[s]);
+    best = wave_max_u64(best);
+    if (lane == 0) {
+      const int tok = argmax_key_index(best);
+      post[i] = tok;
+      if (posterior != nullptr) posterior[(int64_t)b * N + i] = tok;
+    }
+  }
+  __syncthreads();
+  if (matched == nullptr && bonus == nullptr) return;
+  const int m = min(n_draft, N);
+  int first = m;
+  for (int base = 0; base < m; base += 64) {
+    const int j = base + lane;
+    const bool mismatch = (j < m) && (draft[(int64_t)b * dstride + j] != post[j]);
+    const unsigned long long mask = __ballot(mismatch);
+    if (mask != 0ull) {
+      first = base + __ffsll(mask) - 1;
+      break;
+    }
+  }
+  if (lane == 0) {
+    if (matched != nullptr) matched[b] = first;
+    if (bonus != nullptr) bonus[b] = first < N ? post[first] : -1;
+  }
+}
+
+struct Split {
+  int splits;
+  int chunk;
+};
+
+// Deterministic split of one vocabulary row; the workspace size depends on it.
+Split plan_split(int B, int N, int V) {
+  const int64_t rows = (int64_t)B * N;
+  int64_t splits = ceil_div(2048, rows > 0 ? rows : 1);
+  const int64_t max_by_len = ceil_div(V, 2048);
+  if (splits > max_by_len) splits = max_by_len;
+  if (splits < 1) splits = 1;
+  if (splits > 1024) splits = 1024;
+  int64_t chunk = ceil_div(V, splits);
+  chunk = ceil_div(chunk, 16) * 16;  // keeps 16-byte alignment of each slice
+  splits = ceil_div(V, chunk);
+  return Split{(int)splits, (int)chunk};
+}
+
+template <typename T>
+hipError_t launch_partial(const void* logits, int64_t bs, int64_t rs, int B, int N,
+                          int V, const Split& sp, uint64_t* part, hipStream_t s) {
+  const T* lp = static_cast<const T*>(logits);
+  const int per = 16 / (int)sizeof(T);
+  const bool vec = ((uintptr_t)logits % 16 == 0) && (bs % per == 0) && (rs % per == 0);
+  dim3 grid(B * N, sp.splits);
+  if (vec)
+    hipLaunchKernelGGL((argmax_partial_kernel<T, true>), grid, dim3(kArgmaxThreads), 0, s,
+                       lp, bs, rs, N, V, sp.chunk, sp.splits, part);
+  else
+    hipLaunchKernelGGL((argmax_partial_kernel<T, false>), grid, dim3(kArgmaxThreads), 0, s,
+                       lp, bs, rs, N, V, sp.chunk, sp.splits, part);
+  return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace dflash
+
+extern "C" size_t dflash_greedy_accept_workspace_bytes(int B, int N, int V) {
+  if (B <= 0 || N <= 0 || V <= 0) return 0;
+  const dflash::Split sp = dflash::plan_split(B, N, V);
+  return sizeof(uint64_t) * (size_t)B * N * sp.splits;
+}
+
+extern "C" int dflash_greedy_accept(const void* logits, int logits_dtype,
+                                    int64_t logits_batch_stride,
+                                    int64_t logits_row_stride,
+                                    const int32_t* draft, int64_t draft_stride,
+                                    int n_draft, int32_t* posterior,
+                                    int32_t* matched, int32_t* bonus, int B,
+                                    int N, int V, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  using namespace dflash;
+  if (B < 0 || N <= 0 || V <= 0 || n_draft < 0) return DFLASH_ERR_SHAPE;
+  if (B == 0) return DFLASH_OK;
+  if (logits == nullptr || workspace == nullptr) return DFLASH_ERR_NULL;
+  if (n_draft > 0 && draft == nullptr) return DFLASH_ERR_NULL;
+  if (posterior == nullptr && matched == nullptr && bonus == nullptr) return DFLASH_ERR_NULL;
+  if (N > 16384) return DFLASH_ERR_SHAPE;
+  if (logits_dtype != DFLASH_DTYPE_F32 && logits_dtype != DFLASH_DTYPE_BF16 &&
+      logits_dtype != DFLASH_DTYPE_F16)
+    return DFLASH_ERR_UNSUPPORTED;
+  if (workspace_bytes < dflash_greedy_accept_workspace_bytes(B, N, V)) return DFLASH_ERR_WORKSPACE;
+  if ((uintptr_t)workspace % 8 != 0) return DFLASH_ERR_ALIGN;
+  const Split sp = plan_split(B, N, V);
+  uint64_t* part = static_cast<uint64_t*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (logits_dtype == DFLASH_DTYPE_F32)
+    e = launch_partial<float>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, part, s);
+  else if (logits_dtype == DFLASH_DTYPE_BF16)
+    e = launch_partial<uint16_t>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, part, s);
+  else
+    e = launch_partial<F16Tag>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, part, s);
+  if (e != hipSuccess) return (int)e;
+  hipLaunchKernelGGL(accept_finalize_kernel, dim3(B), dim3(64), sizeof(int32_t) * N, s, part,
+                     sp.splits, N, draft, draft_stride, n_draft, posterior, matched, bonus);
+  return to_status(hipGetLastError());
+}

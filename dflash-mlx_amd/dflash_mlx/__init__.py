@@ -1,0 +1,48 @@
+"""MI355X-native gated-delta verify hot path of DFlash speculative decoding.
+
+Drop-in for the verify step of Aryagm/dflash-mlx's Qwen3.5 target: the
+gated-delta scan with a per-token state tape, the fused greedy accept and the
+tape-gather cache rollback, all on hand-written gfx950 kernels
+(libdflash_gfx950.so, C ABI in include/dflash_gdn.h).  Names follow the
+reference package (dflash_mlx/__init__.py:3-22) where the hot path has them.
+"""
+from .adapters import (
+    Qwen35TargetAdapter,
+    adapter_for_model_type,
+    make_rollback_record,
+    rewind_kv_caches,
+    rollback_linear_caches,
+)
+from .cache import ArraysCache, KVCache
+from .gated_delta import (
+    advance_gated_delta_states,
+    conv_rollback,
+    gated_delta_kernel,
+    gated_delta_verify,
+    tape_select,
+)
+from .runtime import (
+    greedy_accept,
+    longest_prefix_match,
+    sample_tokens,
+    verify_block_parallel_replay,
+)
+
+__all__ = [
+    "ArraysCache",
+    "KVCache",
+    "Qwen35TargetAdapter",
+    "adapter_for_model_type",
+    "advance_gated_delta_states",
+    "conv_rollback",
+    "gated_delta_kernel",
+    "gated_delta_verify",
+    "greedy_accept",
+    "longest_prefix_match",
+    "make_rollback_record",
+    "rewind_kv_caches",
+    "rollback_linear_caches",
+    "sample_tokens",
+    "tape_select",
+    "verify_block_parallel_replay",
+]

@@ -1,0 +1,148 @@
+"""Allocation-free verify step for serving loops.
+
+``VerifyStepRunner`` owns every device buffer of one verify step at fixed
+shapes and drives the C ABI directly (no torch op dispatch, no per-step
+allocation), in the order of the reference's verify_block_parallel_replay
+(dflash_mlx/runtime.py:117-163) with the rollback moved onto the device:
+
+  1. gated-delta scan of all linear layers' inputs, writing out, the final
+     state and the per-token state tape       (dflash_gdn_verify_scan)
+  2. greedy accept on the verify logits       (dflash_greedy_accept)
+  3. recurrent-state rollback by tape gather  (dflash_tape_select)
+  4. conv-window rollback                     (dflash_conv_rollback)
+
+The accepted count produced by step 2 feeds steps 3-4 on the device, so a
+step needs no host synchronisation.  Layers are stacked as batch entries of
+one scan launch (batch index = layer * B + b); layer l's tape is the view
+tape[:, l*B:(l+1)*B] whose token stride is L*B*S.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+
+@dataclass(frozen=True)
+class StepShape:
+    L: int        # gated-delta layers in the step
+    B: int        # sequences
+    T: int        # verify block length
+    Hk: int
+    Hv: int
+    Dk: int
+    Dv: int
+    V: int        # vocabulary of the verify logits
+    conv_dim: int = 0   # 0: no conv-window rollback
+    K1: int = 3         # conv kernel size - 1
+
+    def scan_bytes(self) -> int:
+        Bt, T = self.L * self.B, self.T
+        qkvo = 2 * Bt * T * (2 * self.Hk * self.Dk + 2 * self.Hv * self.Dv)
+        gb = 8 * Bt * T * self.Hv
+        return qkvo + gb + 4 * Bt * self.Hv * self.Dv * self.Dk * (T + 2)
+
+    def accept_bytes(self, logit_bytes: int = 4) -> int:
+        return logit_bytes * self.B * self.T * self.V + 4 * self.B * self.T
+
+    def rollback_bytes(self) -> int:
+        """Upper bound (every sequence accepts >= 1 token): state read + write,
+        conv window read + write."""
+        st = 2 * 4 * self.L * self.B * self.Hv * self.Dv * self.Dk
+        cv = 2 * 2 * self.L * self.B * self.K1 * self.conv_dim
+        return st + cv
+
+
+class VerifyStepRunner:
+    """Holds the step's device buffers; ``run()`` enqueues one verify step on
+    torch's current stream.  Inputs are written into the ``q, k, v, g, beta,
+    state, logits, draft, conv_in, qkv`` buffers by the caller."""
+
+    def __init__(self, shape: StepShape, device: torch.device):
+        s = shape
+        self.shape = s
+        self.device = device
+        Bt = s.L * s.B
+        bf, f32, i32 = torch.bfloat16, torch.float32, torch.int32
+        z = lambda *shp, dt: torch.zeros(shp, dtype=dt, device=device)
+        self.q = z(Bt, s.T, s.Hk, s.Dk, dt=bf)
+        self.k = z(Bt, s.T, s.Hk, s.Dk, dt=bf)
+        self.v = z(Bt, s.T, s.Hv, s.Dv, dt=bf)
+        self.g = z(Bt, s.T, s.Hv, dt=f32)
+        self.beta = z(Bt, s.T, s.Hv, dt=f32)
+        self.state = z(Bt, s.Hv, s.Dv, s.Dk, dt=f32)
+        self.out = z(Bt, s.T, s.Hv, s.Dv, dt=bf)
+        self.final = z(Bt, s.Hv, s.Dv, s.Dk, dt=f32)
+        self.tape = z(s.T, Bt, s.Hv, s.Dv, s.Dk, dt=f32)
+        self.new_state = z(Bt, s.Hv, s.Dv, s.Dk, dt=f32)
+        self.logits = z(s.B, s.T, s.V, dt=f32)
+        self.draft = z(s.B, s.T, dt=i32)
+        self.posterior = z(s.B, s.T, dt=i32)
+        self.matched = z(s.B, dt=i32)
+        self.bonus = z(s.B, dt=i32)
+        lib = _lib.load()
+        ws = int(lib.dflash_greedy_accept_workspace_bytes(s.B, s.T, s.V))
+        self.workspace = z(max(ws, 8), dt=torch.uint8)
+        if s.conv_dim:
+            self.conv_in = [z(s.B, s.K1, s.conv_dim, dt=bf) for _ in range(s.L)]
+            self.qkv = [z(s.B, s.T, s.conv_dim, dt=bf) for _ in range(s.L)]
+            self.conv_out = [z(s.B, s.K1, s.conv_dim, dt=bf) for _ in range(s.L)]
+        self._build_args()
+
+    def _build_args(self) -> None:
+        s = self.shape
+        Bt = s.L * s.B
+        S = s.Hv * s.Dv * s.Dk
+        self._scan_args = (
+            self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.g.data_ptr(),
+            self.beta.data_ptr(), self.state.data_ptr(), self.out.data_ptr(),
+            self.final.data_ptr(), self.tape.data_ptr(), None,
+            Bt, s.T, s.Hk, s.Hv, s.Dk, s.Dv, None,
+        )
+        self._accept_args = (
+            self.logits.data_ptr(), _lib.DFLASH_DTYPE_F32, s.T * s.V, s.V,
+            self.draft.data_ptr(), s.T, s.T, self.posterior.data_ptr(),
+            self.matched.data_ptr(), self.bonus.data_ptr(), s.B, s.T, s.V,
+            self.workspace.data_ptr(), self.workspace.numel(),
+        )
+        esz = 4
+        tapes = (ctypes.c_void_p * s.L)(*[self.tape.data_ptr() + l * s.B * S * esz for l in range(s.L)])
+        sins = (ctypes.c_void_p * s.L)(*[self.state.data_ptr() + l * s.B * S * esz for l in range(s.L)])
+        souts = (ctypes.c_void_p * s.L)(*[self.new_state.data_ptr() + l * s.B * S * esz
+                                          for l in range(s.L)])
+        self._tape_args = (tapes, sins, souts, self.matched.data_ptr(), s.L, s.B, s.T, S, Bt * S)
+        if s.conv_dim:
+            cins = _lib.ptr_array(self.conv_in)
+            qkvs = _lib.ptr_array(self.qkv)
+            couts = _lib.ptr_array(self.conv_out)
+            self._conv_args = (cins, qkvs, couts, self.matched.data_ptr(), s.L, s.B, s.T, s.K1,
+                               s.conv_dim, s.T * s.conv_dim, s.conv_dim, 2)
+        lib = _lib.load()
+        self._scan = lib.dflash_gdn_verify_scan
+        self._accept = lib.dflash_greedy_accept
+        self._tsel = lib.dflash_tape_select
+        self._conv = lib.dflash_conv_rollback
+
+    def _stream(self) -> int:
+        return torch.cuda.current_stream(self.device).cuda_stream
+
+    def scan(self, stream: int | None = None) -> None:
+        _lib.check("dflash_gdn_verify_scan", self._scan(*self._scan_args, stream or self._stream()))
+
+    def accept(self, stream: int | None = None) -> None:
+        _lib.check("dflash_greedy_accept", self._accept(*self._accept_args, stream or self._stream()))
+
+    def rollback(self, stream: int | None = None) -> None:
+        st = stream or self._stream()
+        _lib.check("dflash_tape_select", self._tsel(*self._tape_args, st))
+        if self.shape.conv_dim:
+            _lib.check("dflash_conv_rollback", self._conv(*self._conv_args, st))
+
+    def run(self) -> None:
+        st = self._stream()
+        self.scan(st)
+        self.accept(st)
+        self.rollback(st)

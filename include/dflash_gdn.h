@@ -1,0 +1,188 @@
+/*
+ * dflash_gdn.h — C ABI of the MI355X (gfx950) gated-delta verify hot path.
+ *
+ * One shared library, libdflash_gfx950.so, exports these entry points.  They
+ * take plain device pointers, sizes and element strides; no C++ or framework
+ * types cross the boundary.  Every entry point:
+ *   - returns 0 on success, a negative DFLASH_ERR_* code when the arguments are
+ *     rejected before any launch, or a positive hipError_t when the launch
+ *     itself fails;
+ *   - allocates nothing, synchronises nothing and keeps no state between calls
+ *     (so it is reentrant and ordered only by the stream it is given);
+ *   - enqueues its kernels on `stream` (a hipStream_t; NULL = the null stream).
+ *
+ * Tensor conventions (row-major, innermost index last):
+ *   q, k    [B, T, Hk, Dk]  bf16, Dk contiguous, other dims strided
+ *   v       [B, T, Hv, Dv]  bf16, Dv contiguous, other dims strided
+ *   g, beta [B, T, Hv]      fp32, Hv contiguous, other dims strided
+ *   state   [B, Hv, Dv, Dk] fp32, contiguous (the reference's recurrent-state
+ *                           orientation: dk fastest)
+ *   out     [B, T, Hv, Dv]  bf16, contiguous
+ *   tape    [T, B, Hv, Dv, Dk] fp32, contiguous; tape[t] is the state after
+ *                           token t, so tape[T-1] equals the final state.
+ * GQA: value head hv reads key head hv / (Hv / Hk).
+ */
+#ifndef DFLASH_GDN_H
+#define DFLASH_GDN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DFLASH_ABI_VERSION 1
+
+/* Argument-validation codes (negative).  Positive values are hipError_t. */
+#define DFLASH_OK 0
+#define DFLASH_ERR_NULL (-1)        /* a required pointer is NULL              */
+#define DFLASH_ERR_SHAPE (-2)       /* a size is out of range or inconsistent  */
+#define DFLASH_ERR_UNSUPPORTED (-3) /* head dim / dtype not compiled in        */
+#define DFLASH_ERR_ALIGN (-4)       /* pointer or stride breaks vector access  */
+#define DFLASH_ERR_WORKSPACE (-5)   /* workspace smaller than required         */
+
+/* dtype tags used where an entry point accepts more than one element type. */
+#define DFLASH_DTYPE_F32 0
+#define DFLASH_DTYPE_BF16 1
+#define DFLASH_DTYPE_F16 2
+
+/* Returns DFLASH_ABI_VERSION.  No reference counterpart (ABI handshake). */
+int dflash_abi_version(void);
+
+/* Human-readable text for a return code (static storage). */
+const char* dflash_strerror(int code);
+
+/*
+ * Gated-delta-rule scan over a verify block, emitting the per-token state tape.
+ *
+ * Replaces the forward scan the reference calls per linear-attention layer,
+ * mlx_lm gated_delta_kernel(q, k, v, g, beta, state) -> (out, state)
+ * (call sites dflash_mlx/custom_qwen35_model.py:457-466 and :365-374,
+ * dflash_mlx/adapters.py:202-211), and adds the tape that the reference
+ * rebuilds by replay on rollback (custom_qwen35_model.py:1029-1074).
+ *
+ * Per (b, hv) with S = state_in[b, hv] and for t = 0 .. n_b - 1:
+ *   S      <- g[b,t,hv] * S
+ *   kv[dv]  = sum_dk S[dv,dk] * k[b,t,hk,dk]
+ *   d[dv]   = (v[b,t,hv,dv] - kv[dv]) * beta[b,t,hv]
+ *   S[dv,dk] += k[b,t,hk,dk] * d[dv]
+ *   out[b,t,hv,dv] = bf16(sum_dk S[dv,dk] * q[b,t,hk,dk])   (if q and out)
+ *   tape[t,b,hv] = S                                          (if tape)
+ * and final_state[b,hv] = S after n_b tokens (if final_state), where
+ * n_b = lengths ? clamp(lengths[b], 0, T) : T.  Entries of out and tape at
+ * t >= n_b are left untouched.
+ *
+ * q and out are optional together (both NULL gives the state-only replay);
+ * tape, final_state and lengths are each optional.  At least one of out,
+ * tape, final_state must be given.
+ *
+ * strides: NULL for contiguous inputs, else 13 int64 element strides:
+ *   { q_b, q_t, q_h,  k_b, k_t, k_h,  v_b, v_t, v_h,  g_b, g_t,  beta_b, beta_t }
+ *
+ * Supported: Dk in {32, 64, 96, 128, 192, 256}; Dv % 16 == 0; Hv % Hk == 0.
+ * final_state may alias state_in (each state row is read before it is
+ * written by the same lanes); tape and out must not alias any input.
+ */
+int dflash_gdn_verify_scan(const void* q, const void* k, const void* v,
+                           const float* g, const float* beta,
+                           const float* state_in, void* out,
+                           float* final_state, float* tape,
+                           const int32_t* lengths, int B, int T, int Hk,
+                           int Hv, int Dk, int Dv, const int64_t* strides,
+                           void* stream);
+
+/*
+ * State-only replay of the first n_b tokens: the same recurrence without q,
+ * out or tape.  Replaces advance_gated_delta_states(initial_states, keys,
+ * values, g, beta) (dflash_mlx/custom_qwen35_model.py:97-139, duplicate at
+ * dflash_mlx/adapters.py:93-135) and its Metal kernel
+ * gated_delta_state_update (custom_qwen35_model.py:29-89).  The reference
+ * passes keys already repeated to Hv heads; pass Hk == Hv for that layout,
+ * or Hk < Hv to read un-repeated keys.  strides as for the scan (q entries
+ * ignored).  state_out may alias state_in.
+ */
+int dflash_gdn_replay(const void* k, const void* v, const float* g,
+                      const float* beta, const float* state_in,
+                      float* state_out, const int32_t* lengths, int B, int T,
+                      int Hk, int Hv, int Dk, int Dv, const int64_t* strides,
+                      void* stream);
+
+/*
+ * Greedy verify accept: argmax over the vocabulary, then the longest prefix of
+ * the draft that agrees with it.
+ *
+ * Replaces sample_tokens(logits, temperature=0) (dflash_mlx/runtime.py:22-29)
+ * followed by longest_prefix_match(block[1:], posterior[:-1]) and the bonus
+ * pick posterior[matched] (runtime.py:41-47, :145-147, :163).
+ *
+ *   posterior[b,i] = argmax_v logits[b,i,v]   (lowest index wins ties; NaN
+ *                    counts as larger than every number, first NaN wins)
+ *   matched[b]     = largest m <= min(n_draft, N) with
+ *                    draft[b,j] == posterior[b,j] for all j < m
+ *   bonus[b]       = posterior[b, matched[b]] if matched[b] < N, else -1
+ * The reference wiring is draft = block[1:] (n_draft = T-1) against N = T
+ * logit rows; accepted_inputs = matched + 1.  n_draft = 0 gives the plain
+ * greedy sample (matched = 0, bonus = posterior[b,0]).
+ *
+ * logits: [B, N, V] of logits_dtype (DFLASH_DTYPE_F32 / _BF16 / _F16),
+ * innermost contiguous, batch and row strides in elements.  draft: int32
+ * [B, n_draft] with batch stride draft_stride.  posterior (int32 [B, N],
+ * contiguous; may be NULL), matched and bonus (int32 [B]) are outputs.
+ * matched and bonus may be NULL when only posterior is wanted.
+ * workspace: device memory of at least
+ * dflash_greedy_accept_workspace_bytes(B, N, V) bytes.
+ */
+size_t dflash_greedy_accept_workspace_bytes(int B, int N, int V);
+int dflash_greedy_accept(const void* logits, int logits_dtype,
+                         int64_t logits_batch_stride, int64_t logits_row_stride,
+                         const int32_t* draft, int64_t draft_stride,
+                         int n_draft, int32_t* posterior, int32_t* matched,
+                         int32_t* bonus, int B, int N, int V, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/*
+ * Recurrent-state rollback by tape gather, for L layers in one launch.
+ *
+ * Replaces the replay in Qwen3_5TextModel.rollback_linear_caches
+ * (dflash_mlx/custom_qwen35_model.py:1053-1074; adapter copy
+ * dflash_mlx/adapters.py:537-560), which re-runs the accepted prefix; with
+ * the tape the state after a accepted tokens is already stored.
+ *
+ * For layer l < L and sequence b < B with a = clamp(accepted[b], 0, T):
+ *   states_out[l][b] = a >= 1 ? tapes[l][a-1, b] : states_in[l][b]
+ * tapes[l] is [T, B, S] fp32 whose token index has stride tape_token_stride
+ * elements (0 means B*S, a contiguous per-layer tape; layers stacked as batch
+ * entries of one scan pass L*B*S), states_in[l] / states_out[l] are [B, S]
+ * fp32 with S = state_elems (= Hv*Dv*Dk).  The three arguments are host
+ * arrays of L device pointers.  states_out[l] may alias states_in[l].
+ */
+int dflash_tape_select(const float* const* tapes,
+                       const float* const* states_in, float* const* states_out,
+                       const int32_t* accepted, int L, int B, int T,
+                       int64_t state_elems, int64_t tape_token_stride,
+                       void* stream);
+
+/*
+ * Convolution-window rollback for L layers in one launch.
+ *
+ * Replaces the conv-state half of rollback_linear_caches
+ * (dflash_mlx/custom_qwen35_model.py:1044-1051; adapters.py:530-536):
+ *   conv_out[l][b] = concat(conv_in[l][b], qkv[l][b, :a], axis=0)[-K1:]
+ * with a = clamp(accepted[b], 0, T) and K1 = conv kernel size - 1, i.e. row r
+ * of the window is conv_in row a+r when a+r < K1, else qkv row a+r-K1.
+ * conv_in[l] / conv_out[l]: [B, K1, C] contiguous; qkv[l]: [B, T, C] with
+ * batch / row strides in elements and C contiguous.  elem_bytes is 2 or 4.
+ * conv_out[l] may alias conv_in[l].  Host arrays of L device pointers.
+ */
+int dflash_conv_rollback(const void* const* conv_in, const void* const* qkv,
+                         void* const* conv_out, const int32_t* accepted, int L,
+                         int B, int T, int K1, int64_t C,
+                         int64_t qkv_batch_stride, int64_t qkv_row_stride,
+                         int elem_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DFLASH_GDN_H */

@@ -1,0 +1,263 @@
+"""CPU oracle for the gated-delta verify hot path.
+
+TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg may import this module, and only as the checker (or the timed
+CPU baseline); the product package never imports it and has no CPU fallback.
+
+What is here, each restating a piece of the reference (Aryagm/dflash-mlx):
+
+* ``scan_c``: ctypes binding of gdn_oracle.c — the recurrence in the op order
+  of dflash_mlx/custom_qwen35_model.py:129-139 (fp32, or fp64 accumulation),
+  with ``out`` and the per-token state tape.
+* ``scan_oploop``: numpy restatement of the same pure-op loop, vectorised over
+  (B, Hv, Dv, Dk) the way the reference's MLX op loop is
+  (custom_qwen35_model.py:129-139; mlx_lm gated_delta_ops is the same maths).
+* ``scan_matrix_form``: an algebraically different statement of the same
+  recurrence, S_t = S_{t-1} (g_t (I - beta_t k_t k_t^T)) + beta_t v_t k_t^T,
+  computed with fp64 matrix products.  It shares no code with the loops, so a
+  dropped term, a wrong sign or a transposed operand in either one fails the
+  comparison.
+* ``advance_gated_delta_states``: the replay contract of
+  custom_qwen35_model.py:97-139 (keys already repeated to Hv heads).
+* ``tape_select`` / ``conv_rollback``: the rollback gathers that replace the
+  replay (custom_qwen35_model.py:1044-1051 for the conv window).
+* ``longest_prefix_match`` (runtime.py:41-47) and ``greedy_accept``
+  (runtime.py:22-29 argmax + :145-147 wiring).
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+LIB_PATH = ORACLE_DIR / "liboracle_gdn.so"
+
+_lib = None
+
+
+def build(force: bool = True) -> Path:
+    """Compile gdn_oracle.c with gcc via oracle/Makefile."""
+    cmd = ["make", "-C", str(ORACLE_DIR)] + (["-B"] if force else []) + ["liboracle_gdn.so"]
+    res = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"oracle build failed:\n{res.stdout}")
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build(force=False)
+        L = ctypes.CDLL(str(LIB_PATH))
+        fp = ctypes.POINTER(ctypes.c_float)
+        dp = ctypes.POINTER(ctypes.c_double)
+        ip = ctypes.POINTER(ctypes.c_int32)
+        i = ctypes.c_int
+        L.oracle_gdn_scan_f32.argtypes = [fp, fp, fp, fp, fp, fp, fp, fp, fp, ip, i, i, i, i, i, i]
+        L.oracle_gdn_scan_f32.restype = i
+        L.oracle_gdn_scan_f64.argtypes = [fp, fp, fp, fp, fp, fp, dp, dp, dp, ip, i, i, i, i, i, i]
+        L.oracle_gdn_scan_f64.restype = i
+        L.oracle_greedy_accept_f32.argtypes = [fp, ip, i, ip, ip, ip, i, i, i]
+        L.oracle_greedy_accept_f32.restype = i
+        L.oracle_num_threads.restype = i
+        L.oracle_set_num_threads.argtypes = [i]
+        _lib = L
+    return _lib
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _ptr(a: np.ndarray | None, ctype):
+    if a is None:
+        return None
+    return a.ctypes.data_as(ctypes.POINTER(ctype))
+
+
+def scan_c(q, k, v, g, beta, state, lengths=None, acc64: bool = False, with_out=True,
+           with_tape=True, threads: int | None = None):
+    """Scan via the C oracle.  Shapes: q,k [B,T,Hk,Dk]; v [B,T,Hv,Dv];
+    g,beta [B,T,Hv]; state [B,Hv,Dv,Dk].  Returns (out [B,T,Hv,Dv] or None,
+    final_state [B,Hv,Dv,Dk], tape [T,B,Hv,Dv,Dk] or None)."""
+    k = _f32(k)
+    v = _f32(v)
+    g = _f32(g)
+    beta = _f32(beta)
+    state = _f32(state)
+    B, T, Hk, Dk = k.shape
+    Hv, Dv = v.shape[2], v.shape[3]
+    qa = _f32(q) if (with_out and q is not None) else None
+    dt = np.float64 if acc64 else np.float32
+    out = np.zeros((B, T, Hv, Dv), dt) if qa is not None else None
+    final = np.zeros((B, Hv, Dv, Dk), dt)
+    tape = np.zeros((T, B, Hv, Dv, Dk), dt) if with_tape else None
+    lens = None if lengths is None else np.ascontiguousarray(lengths, dtype=np.int32)
+    L = lib()
+    if threads is not None:
+        L.oracle_set_num_threads(int(threads))
+    fn = L.oracle_gdn_scan_f64 if acc64 else L.oracle_gdn_scan_f32
+    ot = ctypes.c_double if acc64 else ctypes.c_float
+    rc = fn(_ptr(qa, ctypes.c_float), _ptr(k, ctypes.c_float), _ptr(v, ctypes.c_float),
+            _ptr(g, ctypes.c_float), _ptr(beta, ctypes.c_float), _ptr(state, ctypes.c_float),
+            _ptr(out, ot), _ptr(final, ot), _ptr(tape, ot), _ptr(lens, ctypes.c_int32),
+            B, T, Hk, Hv, Dk, Dv)
+    if rc != 0:
+        raise ValueError(f"oracle_gdn_scan rejected the shapes (rc={rc})")
+    return out, final, tape
+
+
+def _repeat_heads(x: np.ndarray, Hv: int) -> np.ndarray:
+    """[B,T,Hk,D] -> [B,T,Hv,D] with value head hv reading key head hv // (Hv/Hk)
+    (the mx.repeat(..., repeat_factor, axis=2) of custom_qwen35_model.py:1054-1057)."""
+    Hk = x.shape[2]
+    return np.repeat(x, Hv // Hk, axis=2)
+
+
+def scan_oploop(q, k, v, g, beta, state, dtype=np.float64):
+    """Vectorised op loop (custom_qwen35_model.py:129-139) plus out = S.q."""
+    Hv = v.shape[2]
+    kf = _repeat_heads(np.asarray(k, dtype), Hv)
+    qf = _repeat_heads(np.asarray(q, dtype), Hv) if q is not None else None
+    vf = np.asarray(v, dtype)
+    gf = np.asarray(g, dtype)
+    bf = np.asarray(beta, dtype)
+    S = np.array(state, dtype=dtype, copy=True)
+    B, T = kf.shape[:2]
+    outs, tape = [], []
+    for t in range(T):
+        S = S * gf[:, t, :, None, None]
+        kv_mem = np.sum(S * kf[:, t, :, None, :], axis=-1)
+        delta = (vf[:, t] - kv_mem) * bf[:, t, :, None]
+        S = S + delta[..., None] * kf[:, t, :, None, :]
+        if qf is not None:
+            outs.append(np.sum(S * qf[:, t, :, None, :], axis=-1))
+        tape.append(S.copy())
+    out = np.stack(outs, axis=1) if qf is not None else None
+    tape_arr = np.stack(tape, axis=0) if T else np.zeros((0,) + S.shape, dtype)
+    return out, S, tape_arr
+
+
+def scan_matrix_form(q, k, v, g, beta, state):
+    """fp64 matrix statement: S_t = S_{t-1} A_t + beta_t v_t k_t^T with
+    A_t = g_t (I - beta_t k_t k_t^T); out_t = S_t q_t."""
+    Hv = v.shape[2]
+    kf = _repeat_heads(np.asarray(k, np.float64), Hv)
+    qf = _repeat_heads(np.asarray(q, np.float64), Hv) if q is not None else None
+    vf = np.asarray(v, np.float64)
+    gf = np.asarray(g, np.float64)
+    bf = np.asarray(beta, np.float64)
+    S = np.array(state, dtype=np.float64, copy=True)  # [B,Hv,Dv,Dk]
+    B, T, _, Dk = kf.shape
+    eye = np.eye(Dk)
+    outs, tape = [], []
+    for t in range(T):
+        kt = kf[:, t]                                   # [B,Hv,Dk]
+        outer_kk = kt[..., :, None] * kt[..., None, :]  # [B,Hv,Dk,Dk]
+        A = gf[:, t, :, None, None] * (eye - bf[:, t, :, None, None] * outer_kk)
+        S = S @ A + bf[:, t, :, None, None] * (vf[:, t][..., :, None] * kt[..., None, :])
+        if qf is not None:
+            outs.append((S @ qf[:, t][..., :, None])[..., 0])
+        tape.append(S.copy())
+    out = np.stack(outs, axis=1) if qf is not None else None
+    return out, S, (np.stack(tape, axis=0) if T else None)
+
+
+def advance_gated_delta_states(initial_states, keys, values, g, beta):
+    """Replay contract of custom_qwen35_model.py:97-139: keys are already
+    repeated to Hv heads; returns the state after all keys.shape[1] tokens
+    (fp32 compute, cast back to the state dtype as at :139)."""
+    _, S, _ = scan_oploop(None, keys, values, g, beta, initial_states, dtype=np.float32)
+    return S.astype(np.asarray(initial_states).dtype)
+
+
+def tape_select(tape, state_in, accepted):
+    """state after a_b tokens: tape[a_b-1, b] for a_b >= 1, else state_in[b]."""
+    tape = np.asarray(tape)
+    state_in = np.asarray(state_in)
+    T = tape.shape[0]
+    out = np.empty_like(state_in)
+    for b, a in enumerate(np.asarray(accepted).tolist()):
+        a = min(max(int(a), 0), T)
+        out[b] = tape[a - 1, b] if a >= 1 else state_in[b]
+    return out
+
+
+def conv_rollback(conv_in, qkv, accepted):
+    """concat(conv_in[b], qkv[b, :a], axis=0)[-K1:] per sequence
+    (custom_qwen35_model.py:1044-1051)."""
+    conv_in = np.asarray(conv_in)
+    qkv = np.asarray(qkv)
+    K1 = conv_in.shape[1]
+    T = qkv.shape[1]
+    out = np.empty_like(conv_in)
+    for b, a in enumerate(np.asarray(accepted).tolist()):
+        a = min(max(int(a), 0), T)
+        out[b] = np.concatenate([conv_in[b], qkv[b, :a]], axis=0)[-K1:] if K1 else conv_in[b]
+    return out
+
+
+def longest_prefix_match(draft_tokens, verifier_tokens) -> int:
+    """runtime.py:41-47: count of leading positions where the lists agree."""
+    matched = 0
+    for d, p in zip(draft_tokens, verifier_tokens):
+        if d != p:
+            break
+        matched += 1
+    return matched
+
+
+def argmax_rows(logits) -> np.ndarray:
+    """numpy argmax over the last axis: first maximum, NaN wins (first NaN)."""
+    x = np.asarray(logits, dtype=np.float32)
+    return np.argmax(x, axis=-1).astype(np.int32)
+
+
+def greedy_accept(logits, draft):
+    """logits [B,N,V], draft [B,n] -> (posterior [B,N], matched [B], bonus [B])."""
+    post = argmax_rows(logits)
+    draft = np.asarray(draft)
+    B, N = post.shape
+    matched = np.zeros(B, np.int32)
+    bonus = np.zeros(B, np.int32)
+    for b in range(B):
+        m = longest_prefix_match(draft[b].tolist(), post[b].tolist())
+        matched[b] = m
+        bonus[b] = post[b, m] if m < N else -1
+    return post, matched, bonus
+
+
+def greedy_accept_c(logits, draft):
+    """C oracle of greedy_accept (fp32 logits)."""
+    lg = _f32(logits)
+    B, N, V = lg.shape
+    dr = np.ascontiguousarray(draft, dtype=np.int32).reshape(B, -1)
+    n = dr.shape[1]
+    post = np.zeros((B, N), np.int32)
+    matched = np.zeros(B, np.int32)
+    bonus = np.zeros(B, np.int32)
+    rc = lib().oracle_greedy_accept_f32(_ptr(lg, ctypes.c_float), _ptr(dr, ctypes.c_int32), n,
+                                        _ptr(post, ctypes.c_int32), _ptr(matched, ctypes.c_int32),
+                                        _ptr(bonus, ctypes.c_int32), B, N, V)
+    if rc != 0:
+        raise ValueError(f"oracle_greedy_accept rejected the shapes (rc={rc})")
+    return post, matched, bonus
+
+
+def num_threads() -> int:
+    return int(lib().oracle_num_threads())
+
+
+def bf16_round(x) -> np.ndarray:
+    """Round fp32 to the nearest bf16 (ties to even), returned as fp32."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    nan = np.isnan(a)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    out = r.astype(np.uint32).view(np.float32).copy()
+    out[nan] = np.nan
+    return out

@@ -1,0 +1,127 @@
+"""The C-ABI library: loads, exports every declared entry point, and rejects
+bad arguments before any launch (runs without a GPU: nothing here computes)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "dflash_gdn.h"
+
+
+def _declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dflash_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from dflash_mlx import _lib
+
+    if not _lib.LIB_PATH.exists():
+        pytest.fail("libdflash_gfx950.so is not built; run __graft_entry__.build()")
+    return _lib.load()
+
+
+def test_header_declares_expected_entry_points():
+    names = _declared_functions()
+    assert names == sorted([
+        "dflash_abi_version", "dflash_strerror", "dflash_gdn_verify_scan", "dflash_gdn_replay",
+        "dflash_greedy_accept_workspace_bytes", "dflash_greedy_accept", "dflash_tape_select",
+        "dflash_conv_rollback",
+    ])
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from dflash_mlx import _lib
+
+    for name in _declared_functions():
+        assert hasattr(lib, name), f"{name} declared in {HEADER.name} but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_library_targets_gfx950_only():
+    from dflash_mlx import _lib
+
+    blob = _lib.LIB_PATH.read_bytes()
+    assert b"gfx950" in blob
+    for other in (b"gfx942", b"gfx90a", b"gfx1100"):
+        assert other not in blob
+
+
+def test_abi_version_and_strerror(lib):
+    assert lib.dflash_abi_version() == 1
+    assert lib.dflash_strerror(0) == b"ok"
+    assert b"NULL" in lib.dflash_strerror(-1)
+    assert lib.dflash_strerror(-999) == b"unknown dflash error"
+
+
+def test_scan_validation_codes(lib):
+    f = lib.dflash_gdn_verify_scan
+    dummy = ctypes.c_void_p(0x1000)
+    # missing k
+    assert f(None, None, dummy, dummy, dummy, dummy, None, dummy, None, None,
+             1, 16, 4, 4, 64, 64, None, None) == -1
+    # q without out
+    assert f(dummy, dummy, dummy, dummy, dummy, dummy, None, dummy, None, None,
+             1, 16, 4, 4, 64, 64, None, None) == -1
+    # Hv not a multiple of Hk
+    assert f(dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, None, None,
+             1, 16, 3, 4, 64, 64, None, None) == -2
+    # unsupported Dk
+    assert f(dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, None, None,
+             1, 16, 4, 4, 80, 64, None, None) == -3
+    # Dv not a multiple of 16
+    assert f(dummy, dummy, dummy, dummy, dummy, dummy, dummy, dummy, None, None,
+             1, 16, 4, 4, 64, 40, None, None) == -3
+    # misaligned k pointer
+    odd = ctypes.c_void_p(0x1002)
+    assert f(dummy, odd, dummy, dummy, dummy, dummy, dummy, dummy, None, None,
+             1, 16, 4, 4, 64, 64, None, None) == -4
+
+
+def test_accept_workspace_and_validation(lib):
+    ws = lib.dflash_greedy_accept_workspace_bytes(1, 16, 151936)
+    assert ws > 0 and ws % 8 == 0
+    assert lib.dflash_greedy_accept_workspace_bytes(0, 16, 10) == 0
+    dummy = ctypes.c_void_p(0x1000)
+    f = lib.dflash_greedy_accept
+    # too-small workspace
+    assert f(dummy, 0, 16 * 1024, 1024, None, 0, 0, dummy, dummy, dummy,
+             1, 16, 1024, dummy, 8, None) == -5
+    # bad dtype
+    assert f(dummy, 7, 16 * 1024, 1024, None, 0, 0, dummy, dummy, dummy,
+             1, 16, 1024, dummy, 1 << 20, None) == -3
+    # draft missing while n_draft > 0
+    assert f(dummy, 0, 16 * 1024, 1024, None, 16, 16, dummy, dummy, dummy,
+             1, 16, 1024, dummy, 1 << 20, None) == -1
+
+
+def test_rollback_validation(lib):
+    f = lib.dflash_tape_select
+    assert f(None, None, None, None, 0, 1, 16, 10, 0, None) == 0  # nothing to do
+    assert f(None, None, None, None, 1, 1, 16, 10, 0, None) == -1
+    assert f(None, None, None, None, 1, 1, 16, 10, -4, None) == -2
+    g = lib.dflash_conv_rollback
+    assert g(None, None, None, None, 1, 1, 16, 9, 8192, 0, 0, 2, None) == -3  # K1 > 8
+    assert g(None, None, None, None, 1, 1, 16, 3, 8192, 0, 0, 3, None) == -3  # elem size
+
+
+def test_ops_refuse_cpu_tensors():
+    """No CPU fallback: host tensors are rejected, not computed."""
+    import torch
+
+    from dflash_mlx import gated_delta_verify, greedy_accept
+
+    q = torch.zeros(1, 2, 1, 64, dtype=torch.bfloat16)
+    v = torch.zeros(1, 2, 1, 64, dtype=torch.bfloat16)
+    g = torch.zeros(1, 2, 1)
+    s = torch.zeros(1, 1, 64, 64)
+    with pytest.raises(ValueError, match="ROCm device"):
+        gated_delta_verify(q, q, v, g, g, s)
+    with pytest.raises(ValueError, match="ROCm device"):
+        greedy_accept(torch.zeros(1, 2, 8), None)

@@ -1,0 +1,83 @@
+"""Host-side logic of the hot path: accept wiring, KV trim, cache layout and
+the benchmark workloads (CPU only)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+from hypothesis import given, settings
+from hypothesis import strategies as st
+
+from dflash_mlx import KVCache, Qwen35TargetAdapter, longest_prefix_match, rewind_kv_caches
+from dflash_mlx.workloads import CONFIGS, make_accept_inputs, make_scan_inputs
+
+
+@settings(max_examples=200, deadline=None)
+@given(st.lists(st.integers(0, 5), max_size=20), st.lists(st.integers(0, 5), max_size=20))
+def test_longest_prefix_match_matches_oracle(a, b):
+    from oracle import oracle as orc
+
+    assert longest_prefix_match(a, b) == orc.longest_prefix_match(a, b)
+    m = longest_prefix_match(a, b)
+    assert a[:m] == b[:m]
+    assert m == min(len(a), len(b)) or a[m] != b[m]
+
+
+def test_public_names_follow_reference():
+    """dflash_mlx/__init__.py:3-22 exports longest_prefix_match and
+    sample_tokens; the hot-path ops keep the reference's names."""
+    import dflash_mlx
+
+    for name in ("longest_prefix_match", "sample_tokens", "advance_gated_delta_states",
+                 "gated_delta_kernel", "rollback_linear_caches", "rewind_kv_caches",
+                 "verify_block_parallel_replay"):
+        assert name in dflash_mlx.__all__ and hasattr(dflash_mlx, name)
+
+
+def test_kv_trim_is_offset_arithmetic():
+    import torch
+
+    c = KVCache()
+    c.update_and_fetch(torch.zeros(1, 2, 20, 4), torch.zeros(1, 2, 20, 4))
+    c.update_and_fetch(torch.ones(1, 2, 16, 4), torch.ones(1, 2, 16, 4))
+    assert c.offset == 36
+    accepted_inputs = 6
+    rewind_kv_caches([c, object()], 16 - accepted_inputs)  # runtime.py:155
+    assert c.offset == 26
+    assert c.trim(100) == 26 and c.offset == 0
+
+
+def test_make_cache_pattern_is_3_to_1():
+    """custom_qwen35_model.py:818: layer i is linear unless (i+1) % 4 == 0."""
+    cache = Qwen35TargetAdapter().make_cache(32)
+    kinds = ["kv" if isinstance(c, KVCache) else "ssm" for c in cache]
+    assert kinds.count("ssm") == 24 and kinds.count("kv") == 8
+    assert [i for i, k in enumerate(kinds) if k == "kv"] == [3, 7, 11, 15, 19, 23, 27, 31]
+
+
+def test_scan_bytes_match_baseline_table():
+    """Algorithmic bytes per scan launch, as tabulated for the benchmark."""
+    assert CONFIGS[0].scan_bytes() == 1_212_928
+    assert CONFIGS[1].scan_bytes() == 915_505_152
+    assert CONFIGS[2].scan_bytes() == 1_220_673_536
+
+
+def test_workload_inputs_follow_the_recipe():
+    x = make_scan_inputs(CONFIGS[0])
+    import torch
+
+    assert x["q"].dtype == torch.bfloat16 and x["state"].abs().max() == 0
+    norms = torch.linalg.vector_norm(x["k"].float(), dim=-1)
+    assert torch.allclose(norms, torch.ones_like(norms), atol=1e-2)
+    assert bool(((x["g"] > 0) & (x["g"] < 1)).all()) and bool(((x["beta"] > 0) & (x["beta"] < 1)).all())
+
+
+@pytest.mark.parametrize("cfg_id", [0, 1])
+def test_accept_inputs_have_the_drawn_accept_length(cfg_id):
+    from oracle import oracle as orc
+
+    cfg = CONFIGS[cfg_id]
+    if cfg_id == 1:
+        cfg = type(cfg)(**{**cfg.__dict__, "layers": 1, "state_std": 0.0})
+    acc = make_accept_inputs(cfg)
+    post, matched, _ = orc.greedy_accept(acc["logits"].numpy(), acc["draft"].numpy())
+    np.testing.assert_array_equal(matched, acc["accept"].numpy())
