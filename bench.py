@@ -1,14 +1,20 @@
 #!/usr/bin/env python
 """Benchmark of the gated-delta verify hot path on one MI355X.
 
-One step = one verify pass over the Qwen3.5-4B-shaped block (B=1, T=16,
-Hk=16, Hv=32, Dk=Dv=128) for all 24 gated-delta layers:
-  scan with out + final state + per-token tape (one launch, layers stacked)
-  -> fused greedy accept over [16, 151936] fp32 logits
-  -> rollback: tape gather of all 24 layers' states + conv-window rebuild
-     (conv_dim 8192, kernel 4), driven by the device-side accepted count.
-Inputs are resident in HBM before timing; the step runs through the C ABI
-with preallocated buffers.  Prints one JSON line (see DESIGN.md for fields).
+Workload (config c1): Qwen3.5-4B-shaped verify block, B=1, T=16, Hk=16, Hv=32,
+Dk=Dv=128, for all 24 gated-delta layers (stacked as batch entries of one scan
+launch), greedy accept over [16, 151936] fp32 logits, and the cache rollback
+to the accepted length (recurrent state + conv window, conv_dim 8192).
+
+Two step forms are timed, both through the C ABI with preallocated buffers and
+inputs resident in HBM:
+  fused    (headline)  scan whose state load performs the previous step's
+                       rollback (state read from the previous tape at the
+                       device-side accepted count) -> greedy accept -> conv
+                       rollback.  3 launches, no host sync.
+  explicit             scan (+ final state) -> greedy accept -> tape gather of
+                       all 24 layers' states -> conv rollback.  4 launches.
+Prints one JSON line.
 
 python bench.py [--steps K] [--warmup W] [--config 1|2] [--cpu-seconds S]
 """
@@ -33,14 +39,39 @@ CONV_DIM = 8192  # 2*Hk*Dk + Hv*Dv at the Qwen3.5-4B shape
 
 
 def parse_args():
-    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap = argparse.ArgumentParser(description=__doc__,
+                                 formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=1, choices=(1, 2))
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="bounded CPU-baseline sample (0 disables it)")
+    ap.add_argument("--probe", action="store_true",
+                    help="for rocprofv3 --pmc runs: 3 explicit scans, 3 fused scans and 3 "
+                         "calibration copies of 256 MiB, then exit without timing")
     return ap.parse_args()
+
+
+PROBE_COPY_BYTES = 256 << 20
+
+
+def probe(torch, fused, explicit) -> int:
+    """Launch sequence for the HBM-traffic counters.  The calibration copy
+    (torch's elementwise copy of a 256 MiB fp32 buffer) reads and writes
+    exactly PROBE_COPY_BYTES, which scales FETCH_SIZE / WRITE_SIZE."""
+    src = torch.ones(PROBE_COPY_BYTES // 4, device=fused.device)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(3):
+        explicit.scan()
+    for _ in range(3):
+        fused.scan_rolled()
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(f"[bench] probe done: copy bytes {PROBE_COPY_BYTES}", file=sys.stderr, flush=True)
+    return 0
 
 
 def host_cores() -> int:
@@ -54,16 +85,37 @@ def host_cores() -> int:
 def traffic_from_profiles(workload: str):
     """HBM bytes per scan launch from the committed rocprofv3 --pmc summary
     (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration)."""
-    path = ROOT / "profiles" / f"gdn_verify_scan_{workload}_pmc.md"
+    path = ROOT / "profiles" / f"gdn_scan_{workload}_pmc.md"
     if not path.exists():
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", path.read_text())
     return int(m.group(1)) if m else None
 
 
+def time_steps(torch, K: int, phases):
+    """Run K steps of `phases` [(name, fn)], HIP events between phases on the
+    launch stream; returns wall ms/step and per-phase / whole-step GPU µs."""
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(len(phases) + 1)] for _ in range(K)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(K):
+        e = ev[i]
+        e[0].record()
+        for j, (_, fn) in enumerate(phases):
+            fn()
+            e[j + 1].record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    res = {"ms_per_step": wall * 1e3 / K}
+    for j, (name, _) in enumerate(phases):
+        res[name] = sum(e[j].elapsed_time(e[j + 1]) for e in ev) * 1e3 / K
+    res["gpu_step"] = sum(e[0].elapsed_time(e[-1]) for e in ev) * 1e3 / K
+    return res
+
+
 def cpu_baseline(cfg, x, acc, conv, seconds: float):
     """The CPU oracle (C restatement, OpenMP over heads) running the same step
-    on a bounded sample: whole 24-layer steps repeated for ~`seconds`."""
+    on a bounded sample: whole steps repeated for ~`seconds`."""
     import numpy as np
 
     from oracle import oracle as orc
@@ -81,8 +133,7 @@ def cpu_baseline(cfg, x, acc, conv, seconds: float):
     while True:
         _, _, tape = orc.scan_c(*ins, threads=cores)
         _, matched, _ = orc.greedy_accept_c(logits, draft)
-        a = np.tile(matched, L)
-        orc.tape_select(tape, ins[5], a)
+        orc.tape_select(tape, ins[5], np.tile(matched, L))
         for l in range(L):
             orc.conv_rollback(conv_in_np[l], qkv_np[l], matched)
         steps += 1
@@ -96,7 +147,7 @@ def cpu_baseline(cfg, x, acc, conv, seconds: float):
         "cores": cores,
         "kind": "port",
         "sample": f"{steps} full steps of {cfg.name} (scan+tape over {L} layers, accept over "
-                  f"[{B},{cfg.T},{cfg.V}] fp32, tape + conv rollback) in {el:.1f} s; "
+                  f"[{B},{cfg.T},{cfg.V}] fp32, state gather + conv rollback) in {el:.1f} s; "
                   "oracle/gdn_oracle.c fp32, OpenMP over heads",
     }
 
@@ -105,8 +156,9 @@ def main() -> int:
     args = parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, WORLD_SIZE={world}); "
-              "the verify scan shards with no communication, see DESIGN.md", file=sys.stderr)
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, "
+              f"WORLD_SIZE={world}); this build runs on a single MI355X and the verify scan "
+              "would shard across GPUs with no communication (see DESIGN.md)", file=sys.stderr)
         return 2
 
     import torch
@@ -119,102 +171,114 @@ def main() -> int:
         return 1
     dev = torch.device("cuda", 0)
     cfg = CONFIGS[args.config]
-    L = cfg.layers
-    shape = StepShape(L=L, B=cfg.B, T=cfg.T, Hk=cfg.Hk, Hv=cfg.Hv, Dk=cfg.Dk, Dv=cfg.Dv,
+    L, B, T = cfg.layers, cfg.B, cfg.T
+    shape = StepShape(L=L, B=B, T=T, Hk=cfg.Hk, Hv=cfg.Hv, Dk=cfg.Dk, Dv=cfg.Dv,
                       V=cfg.V, conv_dim=CONV_DIM, K1=3)
     print(f"[bench] {cfg.name}: building inputs", file=sys.stderr, flush=True)
     x = make_scan_inputs(cfg)
-    acc_cfg = ScanConfig(**{**cfg.__dict__, "layers": 1})
-    acc = make_accept_inputs(acc_cfg, gen=x["_gen"])
+    acc = make_accept_inputs(ScanConfig(**{**cfg.__dict__, "layers": 1}), gen=x["_gen"])
     gen = x["_gen"]
-    conv_in = [torch.randn(cfg.B, 3, CONV_DIM, generator=gen).to(torch.bfloat16) for _ in range(L)]
-    qkv = [torch.randn(cfg.B, cfg.T, CONV_DIM, generator=gen).to(torch.bfloat16) for _ in range(L)]
+    conv_in = [torch.randn(B, 3, CONV_DIM, generator=gen).to(torch.bfloat16) for _ in range(L)]
+    qkv = [torch.randn(B, T, CONV_DIM, generator=gen).to(torch.bfloat16) for _ in range(L)]
 
-    run = VerifyStepRunner(shape, dev)
-    for name in ("q", "k", "v", "g", "beta", "state"):
-        getattr(run, name).copy_(x[name])
-    run.logits.copy_(acc["logits"])
-    run.draft.copy_(acc["draft"])
-    for l in range(L):
-        run.conv_in[l].copy_(conv_in[l])
-        run.qkv[l].copy_(qkv[l])
+    runners = {}
+    for form in ("fused", "explicit"):
+        run = VerifyStepRunner(shape, dev)
+        for name in ("q", "k", "v", "g", "beta", "state"):
+            getattr(run, name).copy_(x[name])
+        run.logits.copy_(acc["logits"])
+        run.draft.copy_(acc["draft"])
+        for l in range(L):
+            run.conv_in[l].copy_(conv_in[l])
+            run.qkv[l].copy_(qkv[l])
+        runners[form] = run
     torch.cuda.synchronize()
 
+    fused, explicit = runners["fused"], runners["explicit"]
     print(f"[bench] warmup {args.warmup}", file=sys.stderr, flush=True)
     for _ in range(args.warmup):
-        run.run()
+        fused.run_fused()
+        explicit.run()
     torch.cuda.synchronize()
-    # The accept result is checked once: the draft agrees with the argmax on
-    # exactly the drawn accept length.
-    if run.matched.cpu().tolist() != acc["accept"].tolist():
-        print("[bench] accept mismatch", file=sys.stderr)
-        return 1
+    for form, r in runners.items():
+        # The draft agrees with the argmax on exactly the drawn accept length.
+        if r.matched.cpu().tolist() != acc["accept"].tolist():
+            print(f"[bench] {form}: accept mismatch", file=sys.stderr)
+            return 1
+    accepted = acc["accept"].tolist()
+    if args.probe:
+        return probe(torch, fused, explicit)
 
     K = args.steps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(K)]
-    print(f"[bench] timing {K} steps", file=sys.stderr, flush=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(K):
-        e = ev[i]
-        e[0].record()
-        run.scan()
-        e[1].record()
-        run.accept()
-        e[2].record()
-        run.rollback()
-        e[3].record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    scan_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / K
-    accept_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / K
-    roll_ms = sum(e[2].elapsed_time(e[3]) for e in ev) / K
-    gpu_step_ms = sum(e[0].elapsed_time(e[3]) for e in ev) / K
-    ms_per_step = wall * 1e3 / K
-    tokens = cfg.B * cfg.T
-    value = tokens / (ms_per_step / 1e3)
+    print(f"[bench] timing {K} fused + {K} explicit steps", file=sys.stderr, flush=True)
+    tf = time_steps(torch, K, [("scan", fused.scan_rolled), ("accept", fused.accept),
+                               ("rollback", fused.conv_rollback)])
+    te = time_steps(torch, K, [("scan", explicit.scan), ("accept", explicit.accept),
+                               ("rollback", explicit.rollback)])
 
-    scan_bytes = shape.scan_bytes()
-    step_bytes = scan_bytes + shape.accept_bytes() + shape.rollback_bytes()
-    achieved = scan_bytes / (scan_ms / 1e3) / 1e9
+    # Algorithmic HBM bytes.  Scan: bf16 q,k,v,out + fp32 g,beta + fp32 state
+    # read + tape (16 states per head).  The fused scan also writes the
+    # rolled-back state for sequences that accepted >= 1 token; the explicit
+    # scan writes the final state instead.
+    S_bytes = 4 * cfg.Hv * cfg.Dv * cfg.Dk
+    io = 2 * L * B * T * (2 * cfg.Hk * cfg.Dk + 2 * cfg.Hv * cfg.Dv) + 8 * L * B * T * cfg.Hv
+    n_wb = L * sum(1 for a in accepted if a >= 1)
+    scan_fused_bytes = io + S_bytes * (L * B * (1 + T) + n_wb)
+    scan_expl_bytes = shape.scan_bytes()
+    accept_bytes = shape.accept_bytes()
+    conv_bytes = 2 * 2 * L * B * 3 * CONV_DIM
+    gather_bytes = 2 * S_bytes * L * B
+    tokens = B * T
+
+    achieved = scan_fused_bytes / (tf["scan"] / 1e6) / 1e9
     roof = {
         "bound": "hbm",
-        "kernel": "gdn_scan_kernel (dflash_gdn_verify_scan)",
+        "kernel": "gdn_scan_kernel<128,R> via dflash_gdn_verify_scan_rollback",
         "achieved": round(achieved, 1),
         "peak": PEAK_HBM_GBPS,
         "unit": "GB/s",
         "frac": round(achieved / PEAK_HBM_GBPS, 4),
         "traffic": traffic_from_profiles(cfg.name),
-        "bytes_alg_per_launch": scan_bytes,
-        "avg_launch_us": round(scan_ms * 1e3, 2),
+        "bytes_alg_per_launch": scan_fused_bytes,
+        "avg_launch_us": round(tf["scan"], 2),
     }
-
+    r2 = lambda d: {k: round(v, 2) for k, v in d.items() if k != "ms_per_step"}
+    expl_scan_gbps = scan_expl_bytes / (te["scan"] / 1e6) / 1e9
     line = {
         "metric": METRIC,
-        "value": round(value, 1),
+        "value": round(tokens / (tf["ms_per_step"] / 1e3), 1),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": K,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(tf["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": cfg.name, "B": cfg.B, "T": cfg.T, "Hk": cfg.Hk, "Hv": cfg.Hv,
+            "workload": cfg.name, "B": B, "T": T, "Hk": cfg.Hk, "Hv": cfg.Hv,
             "Dk": cfg.Dk, "Dv": cfg.Dv, "layers": L, "vocab": cfg.V, "conv_dim": CONV_DIM,
+            "accepted": accepted,
             "io": "bf16 q/k/v/out, fp32 g/beta/state/tape, fp32 logits",
-            "step": "scan+tape (1 launch) -> greedy accept (2) -> tape gather (1) + conv rollback (1)",
+            "step": "fused: scan+tape with the previous step's state rollback in its load "
+                    "(1 launch) -> greedy accept (1) -> conv-window rollback (1)",
         },
         "roofline": roof,
-        "breakdown_us": {
-            "scan": round(scan_ms * 1e3, 2), "accept": round(accept_ms * 1e3, 2),
-            "rollback": round(roll_ms * 1e3, 2), "gpu_step": round(gpu_step_ms * 1e3, 2),
+        "breakdown_us": r2(tf),
+        "step_hbm_gbps": round((scan_fused_bytes + accept_bytes + conv_bytes)
+                               / (tf["gpu_step"] / 1e6) / 1e9, 1),
+        "explicit_step": {
+            "value": round(tokens / (te["ms_per_step"] / 1e3), 1),
+            "ms_per_step": round(te["ms_per_step"], 4),
+            "breakdown_us": r2(te),
+            "scan_gbps": round(expl_scan_gbps, 1),
+            "scan_frac": round(expl_scan_gbps / PEAK_HBM_GBPS, 4),
+            "scan_bytes_alg": scan_expl_bytes,
+            "step_hbm_gbps": round((scan_expl_bytes + accept_bytes + gather_bytes + conv_bytes)
+                                   / (te["gpu_step"] / 1e6) / 1e9, 1),
         },
-        "step_hbm_gbps": round(step_bytes / (gpu_step_ms / 1e3) / 1e9, 1),
-        "scan_tokens_per_s": round(tokens / (scan_ms / 1e3), 1),
     }
     if args.cpu_seconds > 0:
         print(f"[bench] cpu baseline (~{args.cpu_seconds:.0f} s)", file=sys.stderr, flush=True)

@@ -39,6 +39,14 @@ struct ScanParams {
   float* final_state;
   float* tape;
   const int32_t* lengths;
+  // Fused rollback of the previous verify (null sel_tape: off).  Sequence b
+  // starts from sel_tape[a-1, b] with a = clamp(sel_accepted[b % sel_period],
+  // 0, sel_T); for a >= 1 that state is also written to state_wb (= the
+  // state buffer), so the buffer always ends holding the block's initial state.
+  const float* sel_tape;
+  const int32_t* sel_accepted;
+  float* state_wb;
+  int sel_period, sel_T;
   int64_t q_sb, q_st, q_sh;
   int64_t k_sb, k_st, k_sh;
   int64_t v_sb, v_st, v_sh;
@@ -49,6 +57,11 @@ struct ScanParams {
   int rep;         // Hv / Hk
   int row_blocks;  // Dv / (16 * R)
   int items;       // B * Hv * row_blocks
+  // XCD-aware walk (gridDim % 8 == 0, items % 8 == 0): workgroups are
+  // dispatched round-robin over the 8 XCDs, so workgroup w runs on XCD w % 8;
+  // that XCD walks the contiguous item range [x*items/8, (x+1)*items/8), which
+  // keeps all row blocks of a head (and its k/q/v) in one XCD's L2.
+  int xcd_items;  // items / 8, or 0 for the plain grid-stride walk
 };
 
 template <int VEC>
@@ -123,7 +136,14 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
   const bool has_q = p.q != nullptr;
   const bool has_tape = p.tape != nullptr;
 
-  for (int item = blockIdx.x; item < p.items; item += gridDim.x) {
+  int item_begin = blockIdx.x, item_end = p.items, item_step = gridDim.x;
+  if (p.xcd_items > 0) {
+    const int x = blockIdx.x & 7;
+    item_begin = x * p.xcd_items + (blockIdx.x >> 3);
+    item_end = (x + 1) * p.xcd_items;
+    item_step = gridDim.x >> 3;
+  }
+  for (int item = item_begin; item < item_end; item += item_step) {
     const int rb = item % p.row_blocks;
     const int bh = item / p.row_blocks;
     const int b = bh / p.Hv;
@@ -136,16 +156,31 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
 #pragma unroll
     for (int r = 0; r < R; ++r) row[r] = rb * ROWS_WG + r * 16 + gi;
 
-    // Load the state rows.
+    // Load the state rows (from the previous tape when the rollback is fused).
     float S[R][NCH][VEC];
     const int64_t head_base = (int64_t)bh * p.Dv * DK;
+    const float* s_src = p.state_in + head_base;
+    bool writeback = false;
+    if (p.sel_tape != nullptr) {
+      const int a = min(max(p.sel_accepted[b % p.sel_period], 0), p.sel_T);
+      if (a >= 1) {
+        s_src = p.sel_tape + (int64_t)(a - 1) * p.tape_tstride + head_base;
+        writeback = true;
+      }
+    }
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
-        load_f32<VEC>(p.state_in + head_base + (int64_t)row[r] * DK +
-                          c * 16 * VEC + sub * VEC,
-                      S[r][c]);
+        load_f32<VEC>(s_src + (int64_t)row[r] * DK + c * 16 * VEC + sub * VEC, S[r][c]);
+    if (writeback) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int c = 0; c < NCH; ++c)
+          store_f32<VEC>(p.state_wb + head_base + (int64_t)row[r] * DK + c * 16 * VEC + sub * VEC,
+                         S[r][c]);
+    }
 
     const uint16_t* kp = p.k + b * p.k_sb + hk * p.k_sh + sub * VEC;
     const uint16_t* qp =
@@ -249,12 +284,18 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
   }
 }
 
+int scan_grid(int items);
+
 template <int DK>
-hipError_t launch_dk(const ScanParams& base, int R, int grid, hipStream_t s) {
+hipError_t launch_dk(const ScanParams& base, int R, int grid, int xcd, hipStream_t s) {
   ScanParams p = base;
   p.row_blocks = p.Dv / (16 * R);
   p.items = p.B * p.Hv * p.row_blocks;
-  const int blocks = grid > 0 ? min(grid, p.items) : p.items;
+  // grid < 0: the tuned default; 0: one workgroup per item; > 0: that many.
+  const int blocks = grid < 0 ? scan_grid(p.items) : (grid > 0 ? min(grid, p.items) : p.items);
+  // xcd < 0: XCD-aware walk whenever the shapes allow it; 0: off; > 0: on if allowed.
+  const bool xcd_ok = blocks % 8 == 0 && p.items % 8 == 0 && blocks < p.items;
+  p.xcd_items = (xcd != 0 && xcd_ok) ? p.items / 8 : 0;
   switch (R) {
     case 1: hipLaunchKernelGGL((gdn_scan_kernel<DK, 1>), dim3(blocks), dim3(256), 0, s, p); break;
     case 2: hipLaunchKernelGGL((gdn_scan_kernel<DK, 2>), dim3(blocks), dim3(256), 0, s, p); break;
@@ -264,33 +305,58 @@ hipError_t launch_dk(const ScanParams& base, int R, int grid, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Rows per lane group.  More rows per group amortise the k/q loads and bf16
-// unpacking over more state; fewer keep more waves in flight.
-int pick_rows(int B, int Hv, int Dv) {
-  const int64_t heads = (int64_t)B * Hv;
-  for (int R : {2, 1}) {
-    if (Dv % (16 * R) != 0) continue;
-    // Keep at least ~4 waves per SIMD worth of workgroups on 256 CUs.
-    if (heads * (Dv / (16 * R)) >= 4096 || R == 1) return R;
-  }
+// Rows per lane group (1, 2 or 4 are compiled).  Measured on MI355X at the
+// Qwen3.5-4B verify shapes with the capped grid below, one row per group was
+// fastest (R = 2 within 2 %, R = 4 slower: fewer waves in flight).
+int pick_rows(int Dv) {
+  (void)Dv;
   return 1;
 }
+
+// Workgroups launched: at most 3 per CU, each walking several (head, row
+// block) items.  On MI355X this beat one workgroup per item by ~12 % on the
+// tape-write-bound verify shapes (fewer concurrent write streams).
+int scan_grid(int items) {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return items;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      return items;
+    cus[dev] = n;
+  }
+  const int cap = 3 * cus[dev];
+  return items < cap ? items : cap;
+}
+
+// Fused-rollback source of the initial states (see ScanParams::sel_tape).
+struct Select {
+  const float* prev_tape;
+  const int32_t* prev_accepted;
+  float* state;  // the state buffer: read for a == 0, written for a >= 1
+  int prev_T;
+  int period;
+};
 
 int scan_impl(const void* q, const void* k, const void* v, const float* g,
               const float* beta, const float* state_in, void* out,
               float* final_state, float* tape, const int32_t* lengths, int B,
               int T, int Hk, int Hv, int Dk, int Dv, const int64_t* strides,
-              void* stream) {
+              const Select* sel, void* stream) {
   if (B < 0 || T < 0 || Hk <= 0 || Hv <= 0 || Dk <= 0 || Dv <= 0) return DFLASH_ERR_SHAPE;
   if (Hv % Hk != 0) return DFLASH_ERR_SHAPE;
   if (Dv % 16 != 0) return DFLASH_ERR_UNSUPPORTED;
   if (!(Dk == 32 || Dk == 64 || Dk == 96 || Dk == 128 || Dk == 192 || Dk == 256))
     return DFLASH_ERR_UNSUPPORTED;
   if ((int64_t)B * Hv * (Dv / 16) > INT32_MAX) return DFLASH_ERR_SHAPE;
+  if (sel != nullptr && (sel->prev_T < 0 || sel->period <= 0)) return DFLASH_ERR_SHAPE;
   if (B == 0) return DFLASH_OK;
-  if (T == 0) {
+  if (state_in == nullptr) return DFLASH_ERR_NULL;
+  if (sel != nullptr && sel->prev_T > 0 && (sel->prev_tape == nullptr || sel->prev_accepted == nullptr))
+    return DFLASH_ERR_NULL;
+  if (T == 0 && sel == nullptr) {
     // Nothing to scan: the final state is the initial state.
-    if (state_in == nullptr) return DFLASH_ERR_NULL;
     if (final_state != nullptr && final_state != state_in) {
       hipError_t e = hipMemcpyAsync(final_state, state_in,
                                     sizeof(float) * (size_t)B * Hv * Dv * Dk,
@@ -299,12 +365,20 @@ int scan_impl(const void* q, const void* k, const void* v, const float* g,
     }
     return DFLASH_OK;
   }
-  if (k == nullptr || v == nullptr || g == nullptr || beta == nullptr || state_in == nullptr)
+  if (T > 0 && (k == nullptr || v == nullptr || g == nullptr || beta == nullptr))
     return DFLASH_ERR_NULL;
   if ((q == nullptr) != (out == nullptr)) return DFLASH_ERR_NULL;
-  if (out == nullptr && final_state == nullptr && tape == nullptr) return DFLASH_ERR_NULL;
+  if (sel == nullptr && out == nullptr && final_state == nullptr && tape == nullptr)
+    return DFLASH_ERR_NULL;
 
   ScanParams p{};
+  if (sel != nullptr && sel->prev_T > 0) {
+    p.sel_tape = sel->prev_tape;
+    p.sel_accepted = sel->prev_accepted;
+    p.state_wb = sel->state;
+    p.sel_period = sel->period;
+    p.sel_T = sel->prev_T;
+  }
   p.q = static_cast<const uint16_t*>(q);
   p.k = static_cast<const uint16_t*>(k);
   p.v = static_cast<const uint16_t*>(v);
@@ -345,21 +419,21 @@ int scan_impl(const void* q, const void* k, const void* v, const float* g,
     return DFLASH_ERR_ALIGN;
   const uintptr_t smask = (uintptr_t)(vec * 4 - 1);
   if (((uintptr_t)state_in & smask) || ((uintptr_t)final_state & smask) ||
-      ((uintptr_t)tape & smask))
+      ((uintptr_t)tape & smask) || ((uintptr_t)p.sel_tape & smask) || ((uintptr_t)p.state_wb & smask))
     return DFLASH_ERR_ALIGN;
   if (((uintptr_t)v & 1) || ((uintptr_t)out & 1) || ((uintptr_t)g & 3) || ((uintptr_t)beta & 3))
     return DFLASH_ERR_ALIGN;
 
-  const int R = pick_rows(B, Hv, Dv);
+  const int R = pick_rows(Dv);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
   switch (Dk) {
-    case 32: e = launch_dk<32>(p, R, 0, s); break;
-    case 64: e = launch_dk<64>(p, R, 0, s); break;
-    case 96: e = launch_dk<96>(p, R, 0, s); break;
-    case 128: e = launch_dk<128>(p, R, 0, s); break;
-    case 192: e = launch_dk<192>(p, R, 0, s); break;
-    default: e = launch_dk<256>(p, R, 0, s); break;
+    case 32: e = launch_dk<32>(p, R, -1, -1, s); break;
+    case 64: e = launch_dk<64>(p, R, -1, -1, s); break;
+    case 96: e = launch_dk<96>(p, R, -1, -1, s); break;
+    case 128: e = launch_dk<128>(p, R, -1, -1, s); break;
+    case 192: e = launch_dk<192>(p, R, -1, -1, s); break;
+    default: e = launch_dk<256>(p, R, -1, -1, s); break;
   }
   return e == hipSuccess ? DFLASH_OK : (int)e;
 }
@@ -375,7 +449,19 @@ extern "C" int dflash_gdn_verify_scan(const void* q, const void* k, const void* 
                                       int Hk, int Hv, int Dk, int Dv,
                                       const int64_t* strides, void* stream) {
   return dflash::scan_impl(q, k, v, g, beta, state_in, out, final_state, tape,
-                           lengths, B, T, Hk, Hv, Dk, Dv, strides, stream);
+                           lengths, B, T, Hk, Hv, Dk, Dv, strides, nullptr, stream);
+}
+
+extern "C" int dflash_gdn_verify_scan_rollback(
+    const void* q, const void* k, const void* v, const float* g, const float* beta,
+    float* state, const float* prev_tape, const int32_t* prev_accepted, int prev_T,
+    int accepted_period, void* out, float* final_state, float* tape, int B, int T, int Hk,
+    int Hv, int Dk, int Dv, const int64_t* strides, void* stream) {
+  if (state == nullptr) return DFLASH_ERR_NULL;
+  if (final_state != nullptr && final_state == state) return DFLASH_ERR_SHAPE;
+  const dflash::Select sel{prev_tape, prev_accepted, state, prev_T, accepted_period};
+  return dflash::scan_impl(q, k, v, g, beta, state, out, final_state, tape, nullptr, B, T, Hk,
+                           Hv, Dk, Dv, strides, &sel, stream);
 }
 
 extern "C" int dflash_gdn_replay(const void* k, const void* v, const float* g,
@@ -385,5 +471,5 @@ extern "C" int dflash_gdn_replay(const void* k, const void* v, const float* g,
                                  const int64_t* strides, void* stream) {
   if (state_out == nullptr) return DFLASH_ERR_NULL;
   return dflash::scan_impl(nullptr, k, v, g, beta, state_in, nullptr, state_out,
-                           nullptr, lengths, B, T, Hk, Hv, Dk, Dv, strides, stream);
+                           nullptr, lengths, B, T, Hk, Hv, Dk, Dv, strides, nullptr, stream);
 }

@@ -5,16 +5,17 @@
 // longest_prefix_match(block[1:], posterior[:-1]) with the bonus token
 // posterior[matched] (runtime.py:41-47, :145-147, :163).
 //
-// Two launches, both HBM-bound on the logits read:
-//   1. argmax_partial: grid (splits, B*N).  Each workgroup reduces one
+// Two launches, HBM-bound on the logits read:
+//   1. argmax_partial: grid (B*N rows, splits).  Each workgroup reduces one
 //      contiguous slice of one logits row to a 64-bit key
-//      (order-preserving value bits << 32 | ~index), so a plain integer max
-//      gives the largest value and, among equal values, the lowest index.
-//   2. accept_finalize: one wavefront per sequence merges the split keys of
-//      its N rows, writes the posterior tokens, then finds the first draft
-//      mismatch with a 64-lane ballot.
-// Only the small matched/bonus/posterior arrays are written; the host reads
-// them once per verify step.
+//      (order-preserving value bits << 32 | ~index), so an integer max gives
+//      the largest value and, among equal values, the lowest index.
+//   2. accept_finalize: one workgroup per sequence, one wavefront per logits
+//      row, merges the split keys of all rows at once, writes the posterior
+//      tokens, then finds the first draft mismatch with a 64-lane ballot.
+// The kernel boundary orders the two phases; no cross-workgroup atomics or
+// cache write-backs are needed.  Only the small matched/bonus/posterior arrays
+// leave the device.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -26,6 +27,8 @@ namespace dflash {
 namespace {
 
 constexpr int kArgmaxThreads = 256;
+constexpr int kMaxAcceptRows = 16384;
+constexpr int kFinalizeWaves = 16;
 
 template <typename T>
 __device__ __forceinline__ float load_logit(const T* p);
@@ -41,7 +44,7 @@ __device__ __forceinline__ float load_logit<F16Tag>(const F16Tag* p) {
   return f16_bits_to_f32(p->bits);
 }
 
-// Scan 16 bytes holding 16/sizeof(T) consecutive logits starting at idx.
+// Keys of 16 bytes holding 16/sizeof(T) consecutive logits starting at idx.
 template <typename T>
 __device__ __forceinline__ uint64_t key16(u32x4 raw, int idx, uint64_t best);
 template <>
@@ -75,8 +78,8 @@ __device__ __forceinline__ uint64_t key16<F16Tag>(u32x4 raw, int idx, uint64_t b
 
 template <typename T, bool VECTOR>
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(
-    const T* __restrict__ logits, int64_t bstride, int64_t rstride, int N, int V,
-    int chunk, int splits, uint64_t* __restrict__ part) {
+    const T* __restrict__ logits, int64_t bstride, int64_t rstride, int N, int V, int chunk,
+    int splits, uint64_t* __restrict__ keys) {
   const int row = blockIdx.x;
   const int split = blockIdx.y;
   const int b = row / N;
@@ -92,10 +95,10 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(
     int j = threadIdx.x;
     // Four independent 16-byte loads in flight per lane.
     for (; j + 3 * kArgmaxThreads < nvec; j += 4 * kArgmaxThreads) {
-      u32x4 r0 = __builtin_nontemporal_load(vbase + j);
-      u32x4 r1 = __builtin_nontemporal_load(vbase + j + kArgmaxThreads);
-      u32x4 r2 = __builtin_nontemporal_load(vbase + j + 2 * kArgmaxThreads);
-      u32x4 r3 = __builtin_nontemporal_load(vbase + j + 3 * kArgmaxThreads);
+      const u32x4 r0 = __builtin_nontemporal_load(vbase + j);
+      const u32x4 r1 = __builtin_nontemporal_load(vbase + j + kArgmaxThreads);
+      const u32x4 r2 = __builtin_nontemporal_load(vbase + j + 2 * kArgmaxThreads);
+      const u32x4 r3 = __builtin_nontemporal_load(vbase + j + 3 * kArgmaxThreads);
       best = key16<T>(r0, start + j * PER, best);
       best = key16<T>(r1, start + (j + kArgmaxThreads) * PER, best);
       best = key16<T>(r2, start + (j + 2 * kArgmaxThreads) * PER, best);
@@ -118,39 +121,41 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(
     uint64_t m = wbest[0];
 #pragma unroll
     for (int w = 1; w < kArgmaxThreads / 64; ++w) m = u64_max(m, wbest[w]);
-    part[(int64_t)row * splits + split] = m;
+    keys[(int64_t)row * splits + split] = m;
   }
 }
 
-__global__ __launch_bounds__(64) void accept_finalize_kernel(
-    const uint64_t* __restrict__ part, int splits, int N,
-    const int32_t* __restrict__ draft, int64_t dstride, int n_draft,
-    int32_t* __restrict__ posterior, int32_t* __restrict__ matched,
-    int32_t* __restrict__ bonus) {
+// grid: B workgroups of kFinalizeWaves wavefronts; wave w merges rows w,
+// w + kFinalizeWaves, ... of its sequence.
+__global__ __launch_bounds__(64 * kFinalizeWaves) void accept_finalize_kernel(
+    const uint64_t* __restrict__ keys, int splits, int N, const int32_t* __restrict__ draft,
+    int64_t dstride, int n_draft, int32_t* __restrict__ posterior,
+    int32_t* __restrict__ matched, int32_t* __restrict__ bonus) {
   extern __shared__ int32_t post[];
   const int b = blockIdx.x;
-  const int lane = threadIdx.x;
-  for (int i = 0; i < N; ++i) {
-    const uint64_t* pr = part + ((int64_t)b * N + i) * splits;
-    uint64_t best = 0;
-    for (int s = lane; s < splits; s += 64) best = u64_max(best, pr[s]);
-    best = wave_max_u64(best);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  for (int r = wave; r < N; r += kFinalizeWaves) {
+    const uint64_t* kr = keys + ((int64_t)b * N + r) * splits;
+    uint64_t m = 0;
+    for (int s = lane; s < splits; s += 64) m = u64_max(m, kr[s]);
+    m = wave_max_u64(m);
     if (lane == 0) {
-      const int tok = argmax_key_index(best);
-      post[i] = tok;
-      if (posterior != nullptr) posterior[(int64_t)b * N + i] = tok;
+      const int tok = argmax_key_index(m);
+      post[r] = tok;
+      if (posterior != nullptr) posterior[(int64_t)b * N + r] = tok;
     }
   }
   __syncthreads();
-  if (matched == nullptr && bonus == nullptr) return;
-  const int m = min(n_draft, N);
-  int first = m;
-  for (int base = 0; base < m; base += 64) {
-    const int j = base + lane;
-    const bool mismatch = (j < m) && (draft[(int64_t)b * dstride + j] != post[j]);
+  if (wave != 0 || (matched == nullptr && bonus == nullptr)) return;
+  const int mlen = min(n_draft, N);
+  int first = mlen;
+  for (int base0 = 0; base0 < mlen; base0 += 64) {
+    const int j = base0 + lane;
+    const bool mismatch = (j < mlen) && (draft[(int64_t)b * dstride + j] != post[j]);
     const unsigned long long mask = __ballot(mismatch);
     if (mask != 0ull) {
-      first = base + __ffsll(mask) - 1;
+      first = base0 + __ffsll(mask) - 1;
       break;
     }
   }
@@ -180,18 +185,18 @@ Split plan_split(int B, int N, int V) {
 }
 
 template <typename T>
-hipError_t launch_partial(const void* logits, int64_t bs, int64_t rs, int B, int N,
-                          int V, const Split& sp, uint64_t* part, hipStream_t s) {
+hipError_t launch_partial(const void* logits, int64_t bs, int64_t rs, int B, int N, int V,
+                          const Split& sp, uint64_t* keys, hipStream_t s) {
   const T* lp = static_cast<const T*>(logits);
   const int per = 16 / (int)sizeof(T);
   const bool vec = ((uintptr_t)logits % 16 == 0) && (bs % per == 0) && (rs % per == 0);
-  dim3 grid(B * N, sp.splits);
+  const dim3 grid(B * N, sp.splits);
   if (vec)
-    hipLaunchKernelGGL((argmax_partial_kernel<T, true>), grid, dim3(kArgmaxThreads), 0, s,
-                       lp, bs, rs, N, V, sp.chunk, sp.splits, part);
+    hipLaunchKernelGGL((argmax_partial_kernel<T, true>), grid, dim3(kArgmaxThreads), 0, s, lp, bs,
+                       rs, N, V, sp.chunk, sp.splits, keys);
   else
-    hipLaunchKernelGGL((argmax_partial_kernel<T, false>), grid, dim3(kArgmaxThreads), 0, s,
-                       lp, bs, rs, N, V, sp.chunk, sp.splits, part);
+    hipLaunchKernelGGL((argmax_partial_kernel<T, false>), grid, dim3(kArgmaxThreads), 0, s, lp, bs,
+                       rs, N, V, sp.chunk, sp.splits, keys);
   return hipGetLastError();
 }
 
@@ -214,28 +219,29 @@ extern "C" int dflash_greedy_accept(const void* logits, int logits_dtype,
                                     size_t workspace_bytes, void* stream) {
   using namespace dflash;
   if (B < 0 || N <= 0 || V <= 0 || n_draft < 0) return DFLASH_ERR_SHAPE;
+  if (N > kMaxAcceptRows || (int64_t)B * N > INT32_MAX) return DFLASH_ERR_SHAPE;
   if (B == 0) return DFLASH_OK;
   if (logits == nullptr || workspace == nullptr) return DFLASH_ERR_NULL;
   if (n_draft > 0 && draft == nullptr) return DFLASH_ERR_NULL;
   if (posterior == nullptr && matched == nullptr && bonus == nullptr) return DFLASH_ERR_NULL;
-  if (N > 16384) return DFLASH_ERR_SHAPE;
   if (logits_dtype != DFLASH_DTYPE_F32 && logits_dtype != DFLASH_DTYPE_BF16 &&
       logits_dtype != DFLASH_DTYPE_F16)
     return DFLASH_ERR_UNSUPPORTED;
   if (workspace_bytes < dflash_greedy_accept_workspace_bytes(B, N, V)) return DFLASH_ERR_WORKSPACE;
   if ((uintptr_t)workspace % 8 != 0) return DFLASH_ERR_ALIGN;
   const Split sp = plan_split(B, N, V);
-  uint64_t* part = static_cast<uint64_t*>(workspace);
+  uint64_t* keys = static_cast<uint64_t*>(workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (logits_dtype == DFLASH_DTYPE_F32)
-    e = launch_partial<float>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, part, s);
+    e = launch_partial<float>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, keys, s);
   else if (logits_dtype == DFLASH_DTYPE_BF16)
-    e = launch_partial<uint16_t>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, part, s);
+    e = launch_partial<uint16_t>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, keys, s);
   else
-    e = launch_partial<F16Tag>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, part, s);
+    e = launch_partial<F16Tag>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, keys, s);
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(accept_finalize_kernel, dim3(B), dim3(64), sizeof(int32_t) * N, s, part,
-                     sp.splits, N, draft, draft_stride, n_draft, posterior, matched, bonus);
+  hipLaunchKernelGGL(accept_finalize_kernel, dim3(B), dim3(64 * kFinalizeWaves),
+                     sizeof(int32_t) * (size_t)N, s, keys, sp.splits, N, draft, draft_stride,
+                     n_draft, posterior, matched, bonus);
   return to_status(hipGetLastError());
 }

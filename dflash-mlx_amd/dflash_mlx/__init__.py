@@ -19,6 +19,7 @@ from .gated_delta import (
     conv_rollback,
     gated_delta_kernel,
     gated_delta_verify,
+    gated_delta_verify_rollback,
     tape_select,
 )
 from .runtime import (
@@ -37,6 +38,7 @@ __all__ = [
     "conv_rollback",
     "gated_delta_kernel",
     "gated_delta_verify",
+    "gated_delta_verify_rollback",
     "greedy_accept",
     "longest_prefix_match",
     "make_rollback_record",

@@ -33,6 +33,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP, _VP],
     ),
+    "dflash_gdn_verify_scan_rollback": (
+        _I,
+        [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I,
+         _VP, _VP],
+    ),
     "dflash_gdn_replay": (
         _I,
         [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP, _VP],

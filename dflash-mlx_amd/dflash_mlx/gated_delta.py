@@ -143,6 +143,46 @@ def gated_delta_kernel(q, k, v, g, beta, state, mask=None):
     return out, final
 
 
+def gated_delta_verify_rollback(q, k, v, g, beta, state, prev_tape, prev_accepted,
+                                accepted_period: int | None = None, tape_out=None):
+    """Verify scan with the previous step's rollback fused into the state load.
+
+    For sequence b with a = prev_accepted[b % accepted_period] (device int32),
+    the block starts from prev_tape[a-1, b] (a >= 1) or state[b] (a == 0);
+    ``state`` is updated in place to that rolled-back initial state.  Returns
+    (out, tape).  ``tape_out`` may be ``prev_tape`` itself (in-place reuse).
+    The device-side counterpart of rollback_linear_caches + the next scan
+    (custom_qwen35_model.py:1029-1074, :457-466), with no host sync."""
+    B, T, Hk, Hv, Dk, Dv = _check_scan_inputs(q, k, v, g, beta, state)
+    if state.dtype != _STATE_DTYPE or not state.is_contiguous():
+        raise ValueError("state must be a contiguous float32 buffer (it is updated in place)")
+    q, k, v, g, beta, _, strides = _prep(q, k, v, g, beta, state)
+    dev = k.device
+    _require_device("prev_tape", prev_tape, dev)
+    _require_device("prev_accepted", prev_accepted, dev)
+    if prev_tape.dtype != _STATE_DTYPE or not prev_tape.is_contiguous():
+        raise ValueError("prev_tape must be a contiguous float32 tape")
+    if tuple(prev_tape.shape[1:]) != (B, Hv, Dv, Dk):
+        raise ValueError(f"prev_tape must be [T', B, Hv, Dv, Dk], got {tuple(prev_tape.shape)}")
+    acc = prev_accepted.to(torch.int32).reshape(-1).contiguous()
+    period = acc.numel() if accepted_period is None else int(accepted_period)
+    if period <= 0 or acc.numel() < period or B % period != 0:
+        raise ValueError(f"accepted_period {period} must divide the batch {B} and fit prev_accepted")
+    out = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
+    if tape_out is None:
+        tape_out = torch.empty((T, B, Hv, Dv, Dk), dtype=_STATE_DTYPE, device=dev)
+    elif tuple(tape_out.shape) != (T, B, Hv, Dv, Dk) or not tape_out.is_contiguous():
+        raise ValueError("tape_out must be a contiguous [T, B, Hv, Dv, Dk] float32 tensor")
+    _lib.call(
+        "dflash_gdn_verify_scan_rollback",
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta), state.data_ptr(),
+        prev_tape.data_ptr(), acc.data_ptr(), prev_tape.shape[0], period,
+        out.data_ptr(), None, tape_out.data_ptr(), B, T, Hk, Hv, Dk, Dv, strides,
+        _lib.stream_handle(dev),
+    )
+    return out, tape_out
+
+
 def advance_gated_delta_states(initial_states, keys, values, g, beta, lengths=None):
     """State after replaying keys.shape[1] tokens (or lengths[b] per sequence).
 

@@ -67,7 +67,10 @@ class VerifyStepRunner:
         self.device = device
         Bt = s.L * s.B
         bf, f32, i32 = torch.bfloat16, torch.float32, torch.int32
-        z = lambda *shp, dt: torch.zeros(shp, dtype=dt, device=device)
+        # Inputs are written by the caller and outputs by the kernels, so the
+        # buffers start uninitialised; only `matched` must start at zero (the
+        # first fused step then starts every sequence from `state`).
+        z = lambda *shp, dt: torch.empty(shp, dtype=dt, device=device)
         self.q = z(Bt, s.T, s.Hk, s.Dk, dt=bf)
         self.k = z(Bt, s.T, s.Hk, s.Dk, dt=bf)
         self.v = z(Bt, s.T, s.Hv, s.Dv, dt=bf)
@@ -81,7 +84,7 @@ class VerifyStepRunner:
         self.logits = z(s.B, s.T, s.V, dt=f32)
         self.draft = z(s.B, s.T, dt=i32)
         self.posterior = z(s.B, s.T, dt=i32)
-        self.matched = z(s.B, dt=i32)
+        self.matched = torch.zeros(s.B, dtype=i32, device=device)
         self.bonus = z(s.B, dt=i32)
         lib = _lib.load()
         ws = int(lib.dflash_greedy_accept_workspace_bytes(s.B, s.T, s.V))
@@ -101,6 +104,15 @@ class VerifyStepRunner:
             self.beta.data_ptr(), self.state.data_ptr(), self.out.data_ptr(),
             self.final.data_ptr(), self.tape.data_ptr(), None,
             Bt, s.T, s.Hk, s.Hv, s.Dk, s.Dv, None,
+        )
+        # Fused form: the scan starts each sequence from the previous step's
+        # tape at its accepted count (self.matched), updating self.state in
+        # place, and rewrites the same tape buffer; the final state is tape[T-1].
+        self._scan_rb_args = (
+            self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.g.data_ptr(),
+            self.beta.data_ptr(), self.state.data_ptr(), self.tape.data_ptr(),
+            self.matched.data_ptr(), s.T, s.B, self.out.data_ptr(), None,
+            self.tape.data_ptr(), Bt, s.T, s.Hk, s.Hv, s.Dk, s.Dv, None,
         )
         self._accept_args = (
             self.logits.data_ptr(), _lib.DFLASH_DTYPE_F32, s.T * s.V, s.V,
@@ -122,6 +134,7 @@ class VerifyStepRunner:
                                s.conv_dim, s.T * s.conv_dim, s.conv_dim, 2)
         lib = _lib.load()
         self._scan = lib.dflash_gdn_verify_scan
+        self._scan_rb = lib.dflash_gdn_verify_scan_rollback
         self._accept = lib.dflash_greedy_accept
         self._tsel = lib.dflash_tape_select
         self._conv = lib.dflash_conv_rollback
@@ -141,8 +154,36 @@ class VerifyStepRunner:
         if self.shape.conv_dim:
             _lib.check("dflash_conv_rollback", self._conv(*self._conv_args, st))
 
+    def scan_rolled(self, stream: int | None = None) -> None:
+        _lib.check("dflash_gdn_verify_scan_rollback",
+                   self._scan_rb(*self._scan_rb_args, stream or self._stream()))
+
+    def conv_rollback(self, stream: int | None = None) -> None:
+        if self.shape.conv_dim:
+            _lib.check("dflash_conv_rollback", self._conv(*self._conv_args, stream or self._stream()))
+
     def run(self) -> None:
+        """Explicit form: scan (with final state) -> accept -> gather rollback."""
         st = self._stream()
         self.scan(st)
         self.accept(st)
         self.rollback(st)
+
+    def run_fused(self) -> None:
+        """Steady-state serving form: scan with the previous step's state
+        rollback fused into its load -> accept -> conv-window rollback.  After
+        the call, the state after accepting matched[b] tokens of this block is
+        tape[matched[b]-1, b] (or state[b] when matched[b] == 0), which the next
+        run_fused() picks up on the device.  Start with matched zeroed."""
+        st = self._stream()
+        self.scan_rolled(st)
+        self.accept(st)
+        self.conv_rollback(st)
+
+    def rolled_back_state(self) -> torch.Tensor:
+        """Materialise the state the next fused step starts from (test helper;
+        reads matched on the host)."""
+        s = self.shape
+        a = self.matched.cpu().repeat(s.L).tolist()
+        outs = [self.tape[ai - 1, i] if ai >= 1 else self.state[i] for i, ai in enumerate(a)]
+        return torch.stack(outs)

@@ -93,6 +93,39 @@ int dflash_gdn_verify_scan(const void* q, const void* k, const void* v,
                            void* stream);
 
 /*
+ * The scan above with the previous verify step's rollback fused into its
+ * state load, for device-driven serving loops (no host sync, no separate
+ * gather launch).
+ *
+ * Replaces the pair rollback_linear_caches(..., accepted_inputs)
+ * (dflash_mlx/custom_qwen35_model.py:1029-1074) + next verify scan
+ * (custom_qwen35_model.py:457-466): the reference replays the accepted prefix
+ * and then scans the next block from the rebuilt state; here the next scan
+ * reads that state straight from the previous tape.
+ *
+ * For sequence b, with a = clamp(prev_accepted[b % accepted_period], 0, prev_T):
+ *   S0[b] = a >= 1 ? prev_tape[a-1, b] : state[b]
+ * and when a >= 1, S0[b] is also written to state[b], so on return `state`
+ * holds every sequence's rolled-back initial state (the state an accept of
+ * zero tokens in this block would roll back to).  The scan then runs from S0
+ * exactly as dflash_gdn_verify_scan (out, final_state, tape optional; no
+ * lengths).  prev_tape is [prev_T, B, Hv, Dv, Dk] fp32 and may be the same
+ * buffer as tape (each state row is read before the same lanes write it).
+ * prev_T = 0 disables the selection (prev_tape and prev_accepted unused).
+ * final_state must not alias state.  accepted_period lets layers stacked as
+ * batch entries (index l*B + b) share one accepted count per sequence
+ * (accepted_period = B).
+ */
+int dflash_gdn_verify_scan_rollback(const void* q, const void* k, const void* v,
+                                    const float* g, const float* beta,
+                                    float* state, const float* prev_tape,
+                                    const int32_t* prev_accepted, int prev_T,
+                                    int accepted_period, void* out,
+                                    float* final_state, float* tape, int B,
+                                    int T, int Hk, int Hv, int Dk, int Dv,
+                                    const int64_t* strides, void* stream);
+
+/*
  * State-only replay of the first n_b tokens: the same recurrence without q,
  * out or tape.  Replaces advance_gated_delta_states(initial_states, keys,
  * values, g, beta) (dflash_mlx/custom_qwen35_model.py:97-139, duplicate at
@@ -131,7 +164,9 @@ int dflash_gdn_replay(const void* k, const void* v, const float* g,
  * contiguous; may be NULL), matched and bonus (int32 [B]) are outputs.
  * matched and bonus may be NULL when only posterior is wanted.
  * workspace: device memory of at least
- * dflash_greedy_accept_workspace_bytes(B, N, V) bytes.
+ * dflash_greedy_accept_workspace_bytes(B, N, V) bytes, 8-byte aligned, no
+ * initial contents needed (it holds the per-slice partial maxima between the
+ * two launches).  Calls that overlap in time must use different workspaces.
  */
 size_t dflash_greedy_accept_workspace_bytes(int B, int N, int V);
 int dflash_greedy_accept(const void* logits, int logits_dtype,

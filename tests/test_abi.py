@@ -30,7 +30,8 @@ def lib():
 def test_header_declares_expected_entry_points():
     names = _declared_functions()
     assert names == sorted([
-        "dflash_abi_version", "dflash_strerror", "dflash_gdn_verify_scan", "dflash_gdn_replay",
+        "dflash_abi_version", "dflash_strerror", "dflash_gdn_verify_scan",
+        "dflash_gdn_verify_scan_rollback", "dflash_gdn_replay",
         "dflash_greedy_accept_workspace_bytes", "dflash_greedy_accept", "dflash_tape_select",
         "dflash_conv_rollback",
     ])

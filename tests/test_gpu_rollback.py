@@ -188,3 +188,76 @@ def test_device_side_accept_rollback_batched(oracle, device):
         assert torch.equal(cache[0][1][b], want)
     ref_conv = oracle.conv_rollback(conv0.float().cpu().numpy(), qkv.float().cpu().numpy(), [0, 3, 11, 16])
     np.testing.assert_array_equal(cache[0][0].float().cpu().numpy(), ref_conv)
+
+
+def _step_inputs(gen, Bt, T, Hk, Hv, D, device):
+    q = torch.nn.functional.normalize(torch.randn(Bt, T, Hk, D, generator=gen), dim=-1).bfloat16()
+    k = torch.nn.functional.normalize(torch.randn(Bt, T, Hk, D, generator=gen), dim=-1).bfloat16()
+    v = torch.randn(Bt, T, Hv, D, generator=gen).bfloat16()
+    g = torch.exp(-torch.nn.functional.softplus(torch.randn(Bt, T, Hv, generator=gen)))
+    be = torch.sigmoid(torch.randn(Bt, T, Hv, generator=gen))
+    return [t.to(device) for t in (q, k, v, g, be)]
+
+
+@pytest.mark.parametrize("in_place", [False, True])
+def test_fused_rollback_scan_equals_gather_then_scan(device, in_place):
+    """Three verify steps of 2 stacked layers x 3 sequences: the fused scan
+    (state read from the previous tape at the device-side accepted count) gives
+    bit-identical out and tape to tape_select followed by the plain scan."""
+    from dflash_mlx import gated_delta_verify_rollback
+
+    gen = torch.Generator().manual_seed(11)
+    L, B, T, Hk, Hv, D = 2, 3, 16, 2, 4, 128
+    Bt = L * B
+    s0 = (0.05 * torch.randn(Bt, Hv, D, D, generator=gen)).to(device)
+    accepts = [[0, 5, 16], [16, 1, 0], [7, 7, 2]]
+    # explicit
+    st_e = s0.clone()
+    tape_e = torch.zeros(T, Bt, Hv, D, D, device=device)
+    # fused
+    st_f = s0.clone()
+    tape_f = torch.zeros(T, Bt, Hv, D, D, device=device)
+    acc_f = torch.zeros(B, dtype=torch.int32, device=device)
+    for step, acc in enumerate(accepts):
+        print(f"[fused step {step} in_place={in_place}]", flush=True)
+        q, k, v, g, be = _step_inputs(gen, Bt, T, Hk, Hv, D, device)
+        out_e, _, tape_new = gated_delta_verify(q, k, v, g, be, st_e)
+        out_f, tape_out = gated_delta_verify_rollback(
+            q, k, v, g, be, st_f, tape_f, acc_f, accepted_period=B,
+            tape_out=tape_f if in_place else None)
+        assert torch.equal(st_f, st_e), f"rolled-back state differs at step {step}"
+        assert torch.equal(out_f, out_e) and torch.equal(tape_out, tape_new)
+        tape_f = tape_out
+        # rollback for the next step
+        acc_t = torch.tensor(acc, dtype=torch.int32, device=device)
+        st_e = tape_select([tape_new], [st_e], acc_t.repeat(L))[0]
+        acc_f = acc_t
+        tape_e = tape_new
+    del tape_e
+
+
+def test_step_runner_fused_matches_explicit(device):
+    """VerifyStepRunner: run_fused (rollback folded into the next scan) and run
+    (explicit gather) leave the same rolled-back state and the same tape."""
+    from dflash_mlx.step import StepShape, VerifyStepRunner
+    from dflash_mlx.workloads import CONFIGS, ScanConfig, make_accept_inputs, make_scan_inputs
+
+    cfg = ScanConfig(**{**CONFIGS[2].__dict__, "B": 4, "V": 5000})
+    x = make_scan_inputs(cfg)
+    acc = make_accept_inputs(cfg, gen=x["_gen"])
+    shape = StepShape(L=1, B=4, T=16, Hk=16, Hv=32, Dk=128, Dv=128, V=5000, conv_dim=512)
+    runs = []
+    for fused in (False, True):
+        r = VerifyStepRunner(shape, device)
+        for n in ("q", "k", "v", "g", "beta", "state"):
+            getattr(r, n).copy_(x[n])
+        r.logits.copy_(acc["logits"])
+        r.draft.copy_(acc["draft"])
+        (r.run_fused if fused else r.run)()
+        torch.cuda.synchronize()
+        assert r.matched.cpu().tolist() == acc["accept"].tolist()
+        runs.append(r)
+    explicit, fused = runs
+    assert torch.equal(explicit.tape, fused.tape)
+    assert torch.equal(explicit.out, fused.out)
+    assert torch.equal(fused.rolled_back_state(), explicit.new_state)
