@@ -47,6 +47,8 @@ def parse_args():
     ap.add_argument("--config", type=int, default=1, choices=(1, 2))
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="bounded CPU-baseline sample (0 disables it)")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the measurements of the next-row kernels (fused LM head)")
     ap.add_argument("--probe", action="store_true",
                     help="for rocprofv3 --pmc runs: 3 explicit scans, 3 fused scans and 3 "
                          "calibration copies of 256 MiB, then exit without timing")
@@ -111,6 +113,50 @@ def time_steps(torch, K: int, phases):
         res[name] = sum(e[j].elapsed_time(e[j + 1]) for e in ev) * 1e3 / K
     res["gpu_step"] = sum(e[0].elapsed_time(e[-1]) for e in ev) * 1e3 / K
     return res
+
+
+def measure_lm_head(torch, dev, M=16, H=2560, V=151936, n=50):
+    """§8(f) row 1: fused greedy LM head + accept (MFMA, no logits) at the
+    Qwen3.5-4B shape vs the unfused path (hipBLASLt bf16 logits via a 2-D
+    F.linear, then the greedy-accept kernel).  HBM-bound on the weight."""
+    from dflash_mlx.runtime import greedy_accept, lm_head_greedy_accept
+
+    gen = torch.Generator(device=dev).manual_seed(0)
+    hidden = (torch.randn(M, H, generator=gen, device=dev) / H ** 0.25).to(torch.bfloat16)
+    weight = (torch.randn(V, H, generator=gen, device=dev) / H ** 0.25).to(torch.bfloat16)
+    draft = torch.zeros(1, M, dtype=torch.int32, device=dev)
+
+    def fused():
+        lm_head_greedy_accept(hidden[None], weight, draft, want_posterior=False)
+
+    def unfused():
+        logits = torch.nn.functional.linear(hidden, weight)
+        greedy_accept(logits[None], draft, want_posterior=False)
+
+    out = {}
+    for name, fn in (("fused", fused), ("unfused", unfused)):
+        for _ in range(5):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = e0.elapsed_time(e1) * 1e3 / n
+    bytes_alg = 2 * V * H + 2 * M * H
+    gbps = bytes_alg / (out["fused"] / 1e6) / 1e9
+    return {
+        "shape": {"M": M, "H": H, "V": V},
+        "fused_us": round(out["fused"], 2),
+        "unfused_us": round(out["unfused"], 2),
+        "bytes_alg": bytes_alg,
+        "fused_gbps": round(gbps, 1),
+        "fused_frac": round(gbps / PEAK_HBM_GBPS, 4),
+        "note": "per call, back-to-back launches incl. Python dispatch (fused: 2 kernels; "
+                "unfused: GEMM + 2 kernels)",
+    }
 
 
 def cpu_baseline(cfg, x, acc, conv, seconds: float):
@@ -280,6 +326,10 @@ def main() -> int:
                                    / (te["gpu_step"] / 1e6) / 1e9, 1),
         },
     }
+    if not args.no_extras:
+        print("[bench] next rows: fused LM head", file=sys.stderr, flush=True)
+        del runners, fused, explicit
+        line["next_rows"] = {"lm_head_greedy_accept": measure_lm_head(torch, dev)}
     if args.cpu_seconds > 0:
         print(f"[bench] cpu baseline (~{args.cpu_seconds:.0f} s)", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(cfg, x, acc, (conv_in, qkv), args.cpu_seconds)

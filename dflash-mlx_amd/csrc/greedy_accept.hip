@@ -19,6 +19,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "accept_common.h"
 #include "dflash_gdn.h"
 #include "device_common.h"
 #include "host_common.h"
@@ -28,7 +29,6 @@ namespace {
 
 constexpr int kArgmaxThreads = 256;
 constexpr int kMaxAcceptRows = 16384;
-constexpr int kFinalizeWaves = 16;
 
 template <typename T>
 __device__ __forceinline__ float load_logit(const T* p);
@@ -125,46 +125,6 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(
   }
 }
 
-// grid: B workgroups of kFinalizeWaves wavefronts; wave w merges rows w,
-// w + kFinalizeWaves, ... of its sequence.
-__global__ __launch_bounds__(64 * kFinalizeWaves) void accept_finalize_kernel(
-    const uint64_t* __restrict__ keys, int splits, int N, const int32_t* __restrict__ draft,
-    int64_t dstride, int n_draft, int32_t* __restrict__ posterior,
-    int32_t* __restrict__ matched, int32_t* __restrict__ bonus) {
-  extern __shared__ int32_t post[];
-  const int b = blockIdx.x;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  for (int r = wave; r < N; r += kFinalizeWaves) {
-    const uint64_t* kr = keys + ((int64_t)b * N + r) * splits;
-    uint64_t m = 0;
-    for (int s = lane; s < splits; s += 64) m = u64_max(m, kr[s]);
-    m = wave_max_u64(m);
-    if (lane == 0) {
-      const int tok = argmax_key_index(m);
-      post[r] = tok;
-      if (posterior != nullptr) posterior[(int64_t)b * N + r] = tok;
-    }
-  }
-  __syncthreads();
-  if (wave != 0 || (matched == nullptr && bonus == nullptr)) return;
-  const int mlen = min(n_draft, N);
-  int first = mlen;
-  for (int base0 = 0; base0 < mlen; base0 += 64) {
-    const int j = base0 + lane;
-    const bool mismatch = (j < mlen) && (draft[(int64_t)b * dstride + j] != post[j]);
-    const unsigned long long mask = __ballot(mismatch);
-    if (mask != 0ull) {
-      first = base0 + __ffsll(mask) - 1;
-      break;
-    }
-  }
-  if (lane == 0) {
-    if (matched != nullptr) matched[b] = first;
-    if (bonus != nullptr) bonus[b] = first < N ? post[first] : -1;
-  }
-}
-
 struct Split {
   int splits;
   int chunk;
@@ -240,8 +200,6 @@ extern "C" int dflash_greedy_accept(const void* logits, int logits_dtype,
   else
     e = launch_partial<F16Tag>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, keys, s);
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(accept_finalize_kernel, dim3(B), dim3(64 * kFinalizeWaves),
-                     sizeof(int32_t) * (size_t)N, s, keys, sp.splits, N, draft, draft_stride,
-                     n_draft, posterior, matched, bonus);
-  return to_status(hipGetLastError());
+  return to_status(launch_accept_finalize(keys, sp.splits, B, N, draft, draft_stride, n_draft,
+                                          posterior, matched, bonus, s));
 }

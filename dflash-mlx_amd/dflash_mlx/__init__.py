@@ -24,6 +24,8 @@ from .gated_delta import (
 )
 from .runtime import (
     greedy_accept,
+    lm_head_argmax,
+    lm_head_greedy_accept,
     longest_prefix_match,
     sample_tokens,
     verify_block_parallel_replay,
@@ -40,6 +42,8 @@ __all__ = [
     "gated_delta_verify",
     "gated_delta_verify_rollback",
     "greedy_accept",
+    "lm_head_argmax",
+    "lm_head_greedy_accept",
     "longest_prefix_match",
     "make_rollback_record",
     "rewind_kv_caches",

@@ -90,6 +90,70 @@ def greedy_accept(
     return post, matched, bonus
 
 
+def lm_head_greedy_accept(
+    hidden: torch.Tensor,
+    weight: torch.Tensor,
+    draft: torch.Tensor | Sequence[int] | Sequence[Sequence[int]] | None = None,
+    *,
+    want_posterior: bool = True,
+) -> tuple[torch.Tensor | None, torch.Tensor, torch.Tensor]:
+    """greedy_accept(hidden @ weight.T, draft) without materialising logits.
+
+    hidden: [B,N,H] (or [N,H]) bf16; weight: [V,H] bf16 (LM head or tied
+    embedding).  B*N <= 64 (verify-sized), H % 64 == 0.  Fuses the reference's
+    lm_head_argmax hook (dflash_mlx/adapters.py:267-271) with the accept."""
+    _require_device("hidden", hidden, None)
+    dev = hidden.device
+    _require_device("weight", weight, dev)
+    h = hidden.unsqueeze(0) if hidden.dim() == 2 else hidden
+    if h.dim() != 3 or weight.dim() != 2 or h.shape[-1] != weight.shape[1]:
+        raise ValueError(f"hidden [B,N,H] and weight [V,H] disagree: {tuple(hidden.shape)}, "
+                         f"{tuple(weight.shape)}")
+    if h.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("hidden and weight must be bfloat16")
+    B, N, H = h.shape
+    V = weight.shape[0]
+    h2 = h.reshape(B * N, H)
+    if h2.stride(-1) != 1 or h2.stride(0) % 8 or h2.data_ptr() % 16:
+        h2 = h2.contiguous()
+    w = weight if (weight.stride(-1) == 1 and weight.stride(0) % 8 == 0) else weight.contiguous()
+    d, n = None, 0
+    if draft is not None:
+        d = draft.to(torch.int32) if isinstance(draft, torch.Tensor) else \
+            torch.tensor(draft, dtype=torch.int32).to(dev)
+        if isinstance(draft, torch.Tensor):
+            _require_device("draft", draft, dev)
+        if d.dim() == 1:
+            d = d.unsqueeze(0)
+        d = d.contiguous()
+        if d.shape[0] != B:
+            raise ValueError(f"draft batch {d.shape[0]} != hidden batch {B}")
+        n = d.shape[1]
+    post = torch.empty((B, N), dtype=torch.int32, device=dev) if want_posterior else None
+    matched = torch.empty((B,), dtype=torch.int32, device=dev)
+    bonus = torch.empty((B,), dtype=torch.int32, device=dev)
+    if B == 0:
+        return post, matched, bonus
+    lib = _lib.load()
+    ws = torch.empty((max(int(lib.dflash_lm_head_accept_workspace_bytes(B, N, V)), 8),),
+                     dtype=torch.uint8, device=dev)
+    _lib.call(
+        "dflash_lm_head_greedy_accept",
+        h2.data_ptr(), h2.stride(0), w.data_ptr(), w.stride(0), H, V,
+        _lib.ptr(d), d.stride(0) if d is not None else 0, n,
+        _lib.ptr(post), matched.data_ptr(), bonus.data_ptr(), B, N,
+        ws.data_ptr(), ws.numel(), _lib.stream_handle(dev),
+    )
+    return post, matched, bonus
+
+
+def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """The reference's lm_head_argmax hook (adapters.py:267-271):
+    argmax(hidden @ weight.T, -1) as int32 [..., N], fused (no logits)."""
+    post, _, _ = lm_head_greedy_accept(hidden, weight, None)
+    return post.reshape(hidden.shape[:-1])
+
+
 def sample_tokens(logits: torch.Tensor, temperature: float) -> torch.Tensor:
     """runtime.py:22-29: greedy argmax over the last axis when temperature is
     ~0 (gfx950 kernel), else a categorical draw (torch on the device; outside

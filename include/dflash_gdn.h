@@ -177,6 +177,32 @@ int dflash_greedy_accept(const void* logits, int logits_dtype,
                          size_t workspace_bytes, void* stream);
 
 /*
+ * Fused greedy LM head + accept: the same outputs as dflash_greedy_accept on
+ * logits = hidden . weight^T, without materialising the logits.
+ *
+ * Replaces MLXTargetAdapter.lm_head_argmax(model, hidden_states)
+ * (dflash_mlx/adapters.py:267-271) and the prefix compare that follows it in
+ * verify_block_parallel_greedy_argmax (dflash_mlx/runtime.py:246-292).
+ *
+ * hidden: bf16 [B*N, H] (row b*N + i is sequence b, position i), row stride
+ * hidden_row_stride; weight: bf16 [V, H] (the LM head / tied embedding
+ * matrix), row stride weight_row_stride.  Logits are accumulated in fp32 from
+ * bf16 products (MFMA); posterior/matched/bonus and the draft follow
+ * dflash_greedy_accept.  Supported: B*N <= 64, H % 64 == 0, 16-byte aligned
+ * rows.  workspace: dflash_lm_head_accept_workspace_bytes(B, N, V) bytes,
+ * 8-byte aligned, no initial contents needed.
+ */
+size_t dflash_lm_head_accept_workspace_bytes(int B, int N, int V);
+int dflash_lm_head_greedy_accept(const void* hidden, int64_t hidden_row_stride,
+                                 const void* weight, int64_t weight_row_stride,
+                                 int H, int V, const int32_t* draft,
+                                 int64_t draft_stride, int n_draft,
+                                 int32_t* posterior, int32_t* matched,
+                                 int32_t* bonus, int B, int N,
+                                 void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
+/*
  * Recurrent-state rollback by tape gather, for L layers in one launch.
  *
  * Replaces the replay in Qwen3_5TextModel.rollback_linear_caches
