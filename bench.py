@@ -159,6 +159,109 @@ def measure_lm_head(torch, dev, M=16, H=2560, V=151936, n=50):
     }
 
 
+def _graph_time_us(torch, fn, n=20):
+    """Average replay time of a HIP graph capturing fn (µs)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / n
+
+
+def measure_layer(torch, dev, L=24, B=1, T=16):
+    """§8(f) row 2: the gated-delta layer between its projections (prologue ->
+    scan -> gated-norm epilogue) for L layers of the Qwen3.5-4B shape, each
+    phase captured as one HIP graph of L launches, against the same prologue
+    and epilogue written as torch op chains."""
+    from dflash_mlx.gated_delta import gated_delta_verify
+    from dflash_mlx.gdn_layer import (GatedDeltaConfig, GatedDeltaWeights, gated_rmsnorm,
+                                      gdn_layer_verify, gdn_prologue)
+
+    cfg = GatedDeltaConfig()
+    gen = torch.Generator().manual_seed(0)
+    C, K, Hk, Hv = cfg.conv_dim, cfg.linear_conv_kernel_dim, cfg.linear_num_key_heads, cfg.linear_num_value_heads
+    Dk, Dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
+    layers = []
+    for _ in range(L):
+        layers.append(dict(
+            qkv=torch.randn(B, T, C, generator=gen).bfloat16().to(dev),
+            z=torch.randn(B, T, Hv * Dv, generator=gen).bfloat16().to(dev),
+            a=torch.randn(B, T, Hv, generator=gen).bfloat16().to(dev),
+            b=torch.randn(B, T, Hv, generator=gen).bfloat16().to(dev),
+            conv=torch.randn(B, K - 1, C, generator=gen).bfloat16().to(dev),
+            state=(0.05 * torch.randn(B, Hv, Dv, Dk, generator=gen)).to(dev),
+            w=GatedDeltaWeights.random(cfg, dev, gen)))
+    pro = [gdn_prologue(l["qkv"], l["conv"], l["a"], l["b"], l["w"], cfg) for l in layers]
+    outs = [gated_delta_verify(*p[:5], l["state"])[0] for p, l in zip(pro, layers)]
+    zs = [l["z"].reshape(B, T, Hv, Dv) for l in layers]
+
+    def t_prologue():
+        for l in layers:
+            gdn_prologue(l["qkv"], l["conv"], l["a"], l["b"], l["w"], cfg)
+
+    def t_scan():
+        for p, l in zip(pro, layers):
+            gated_delta_verify(*p[:5], l["state"])
+
+    def t_epilogue():
+        for o, z, l in zip(outs, zs, layers):
+            gated_rmsnorm(o, z, l["w"].norm_weight, cfg.rms_norm_eps)
+
+    def t_layer():
+        for l in layers:
+            gdn_layer_verify(l["qkv"], l["z"], l["a"], l["b"], l["conv"], l["state"], l["w"], cfg)
+
+    F = torch.nn.functional
+
+    def torch_prologue(l):
+        x = torch.cat([l["conv"], l["qkv"]], dim=1).float()
+        wc = l["w"].conv_weight.float()
+        conv = sum(wc[:, j] * x[:, j:j + T] for j in range(K))
+        act = F.silu(conv)
+        q = act[..., :Hk * Dk].unflatten(-1, (Hk, Dk))
+        k = act[..., Hk * Dk:2 * Hk * Dk].unflatten(-1, (Hk, Dk))
+        v = act[..., 2 * Hk * Dk:].unflatten(-1, (Hv, Dv))
+        q = (Dk ** -1.0) * q * torch.rsqrt(q.pow(2).mean(-1, keepdim=True) + 1e-6)
+        k = (Dk ** -0.5) * k * torch.rsqrt(k.pow(2).mean(-1, keepdim=True) + 1e-6)
+        g = torch.exp(-torch.exp(l["w"].A_log) * F.softplus(l["a"].float() + l["w"].dt_bias.float()))
+        beta = torch.sigmoid(l["b"].float())
+        return q.bfloat16(), k.bfloat16(), v.bfloat16(), g, beta, x[:, -(K - 1):].bfloat16()
+
+    def torch_epilogue(o, z, w):
+        of = o.float()
+        y = of * torch.rsqrt(of.pow(2).mean(-1, keepdim=True) + 1e-6) * w.float() * F.silu(z.float())
+        return y.bfloat16()
+
+    def t_torch_pe():
+        for o, z, l in zip(outs, zs, layers):
+            torch_prologue(l)
+            torch_epilogue(o, z, l["w"].norm_weight)
+
+    res = {name: _graph_time_us(torch, fn) for name, fn in (
+        ("prologue", t_prologue), ("scan", t_scan), ("epilogue", t_epilogue),
+        ("layer", t_layer), ("torch_prologue_epilogue", t_torch_pe))}
+    return {
+        "shape": {"layers": L, "B": B, "T": T, "Hk": Hk, "Hv": Hv, "Dk": Dk, "Dv": Dv, "conv_dim": C},
+        "per_step_us": {k: round(v, 2) for k, v in res.items()},
+        "per_layer_us": {k: round(v / L, 2) for k, v in res.items()},
+        "note": f"each phase = one HIP graph of {L} per-layer launches; torch_prologue_epilogue "
+                "= the same prologue + epilogue maths as torch op chains",
+    }
+
+
 def cpu_baseline(cfg, x, acc, conv, seconds: float):
     """The CPU oracle (C restatement, OpenMP over heads) running the same step
     on a bounded sample: whole steps repeated for ~`seconds`."""
@@ -330,6 +433,8 @@ def main() -> int:
         print("[bench] next rows: fused LM head", file=sys.stderr, flush=True)
         del runners, fused, explicit
         line["next_rows"] = {"lm_head_greedy_accept": measure_lm_head(torch, dev)}
+        print("[bench] next rows: gated-delta layer prologue/epilogue", file=sys.stderr, flush=True)
+        line["next_rows"]["gdn_layer"] = measure_layer(torch, dev)
     if args.cpu_seconds > 0:
         print(f"[bench] cpu baseline (~{args.cpu_seconds:.0f} s)", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(cfg, x, acc, (conv_in, qkv), args.cpu_seconds)

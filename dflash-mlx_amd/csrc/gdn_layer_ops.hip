@@ -1,0 +1,300 @@
+// Prologue and epilogue of a gated-delta layer around the verify scan.
+//
+// Reference layer body (dflash_mlx/custom_qwen35_model.py:409-484):
+//   conv_input = concat(conv_state, qkv)              (:431-433)
+//   new_conv_state = conv_input[:, -(K-1):]            (:434)
+//   conv_out = silu(depthwise conv1d(conv_input))      (:435; weight [C, K, 1], :718-725)
+//   q, k, v = split(conv_out) per head                 (:437-444)
+//   q = Dk^-1 * rms_norm(q, eps=1e-6); k = Dk^-0.5 * rms_norm(k)   (:446-448)
+//   beta = sigmoid(b); g = compute_g(A_log, a, dt_bias)            (:449-450)
+//   ... scan ...
+//   out = RMSNormGated(out, z)                         (:478)
+// compute_g and RMSNormGated live in the un-vendored mlx-lm 0.31.2; they are
+// the published Qwen3-Next forms: g = exp(-exp(A_log) * softplus(a + dt_bias))
+// and y = weight * rms_norm(x) * silu(z).
+//
+// Both kernels are small and HBM/launch-bound; all arithmetic is fp32 and
+// only the outputs are rounded (q/k/v to bf16, the scan's input type).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "dflash_gdn.h"
+#include "device_common.h"
+#include "host_common.h"
+
+namespace dflash {
+namespace {
+
+constexpr int kMaxConvTaps = 8;
+
+__device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); }
+__device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
+// softplus(x) = log(1 + exp(x)), evaluated without overflow.
+__device__ __forceinline__ float softplus(float x) {
+  return x > 20.f ? x : log1pf(__expf(x));
+}
+
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+struct ProParams {
+  const uint16_t* qkv;  // [B, T, C] bf16, C contiguous
+  int64_t qkv_sb, qkv_st;
+  const uint16_t* conv_state;  // [B, K1, C] bf16 contiguous
+  const uint16_t* conv_w;      // [C, K] bf16 (the MLX [C, K, 1] layout)
+  const uint16_t* a;           // [B, T, Hv] bf16
+  const uint16_t* b;           // [B, T, Hv] bf16
+  int64_t a_sb, a_st, b_sb, b_st;
+  const float* A_log;       // [Hv] fp32
+  const uint16_t* dt_bias;  // [Hv] bf16
+  uint16_t* act;            // [B, T, C] bf16: q | k (normalised, scaled) | v
+  float* g;                 // [B, T, Hv]
+  float* beta;              // [B, T, Hv]
+  uint16_t* new_conv_state; // [B, K1, C]
+  int T, C, K, Hk, Hv, Dk;
+  float eps, q_scale, k_scale;
+};
+
+__device__ __forceinline__ float ldbf(const uint16_t* p) { return bf16_bits_to_f32(*p); }
+
+// silu(conv1d) of NC consecutive channels c0 .. c0+NC-1 at token t of
+// sequence b.  All K taps of every channel are loaded before any is used.
+template <int NC>
+__device__ __forceinline__ void conv_silu(const ProParams& p, int b, int t, int c0, float* out) {
+  const int K1 = p.K - 1;
+  float x[kMaxConvTaps][NC];
+  float w[NC][kMaxConvTaps];
+#pragma unroll
+  for (int j = 0; j < kMaxConvTaps; ++j) {
+    if (j < p.K) {
+      const int s = t + j;  // row of concat(conv_state, qkv)
+      const uint16_t* src = s < K1 ? p.conv_state + ((int64_t)b * K1 + s) * p.C + c0
+                                   : p.qkv + b * p.qkv_sb + (int64_t)(s - K1) * p.qkv_st + c0;
+#pragma unroll
+      for (int i = 0; i < NC; ++i) x[j][i] = ldbf(src + i);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NC; ++i)
+#pragma unroll
+    for (int j = 0; j < kMaxConvTaps; ++j)
+      if (j < p.K) w[i][j] = ldbf(p.conv_w + (int64_t)(c0 + i) * p.K + j);
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxConvTaps; ++j)
+      if (j < p.K) acc = fmaf(w[i][j], x[j][i], acc);
+    out[i] = silu(acc);
+  }
+}
+
+// Work units of one (sequence, token): 2*Hk q/k heads (one wavefront each,
+// with the head's rms-norm), then value chunks of 256 channels (one
+// wavefront each, 4 channels per lane), then one unit for g / beta and the
+// new conv window.  grid: (B*T, ceil(units / 4)), 256 threads.
+template <int PER>  // Dk / 64 channels per lane
+__global__ __launch_bounds__(256) void gdn_prologue_kernel(const ProParams p) {
+  const int bt = blockIdx.x;
+  const int b = bt / p.T;
+  const int t = bt - b * p.T;
+  const int lane = threadIdx.x & 63;
+  const int unit = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int n_qk = 2 * p.Hk;
+  const int v0 = 2 * p.Hk * p.Dk;
+  const int n_v = (p.C - v0 + 255) / 256;
+  uint16_t* act = p.act + (int64_t)bt * p.C;
+
+  if (unit < n_qk) {
+    // q heads first, then k heads (the split order); lane owns PER channels.
+    const int c0 = unit * p.Dk + lane * PER;
+    float vals[PER];
+    conv_silu<PER>(p, b, t, c0, vals);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) ss = fmaf(vals[i], vals[i], ss);
+    ss = wave_sum(ss);
+    const float r = rsqrtf(ss / (float)p.Dk + p.eps) * (unit < p.Hk ? p.q_scale : p.k_scale);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) act[c0 + i] = f32_to_bf16_rne(vals[i] * r);
+  } else if (unit < n_qk + n_v) {
+    const int c0 = v0 + (unit - n_qk) * 256 + lane * 4;
+    if (c0 + 4 <= p.C) {
+      float vals[4];
+      conv_silu<4>(p, b, t, c0, vals);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) act[c0 + i] = f32_to_bf16_rne(vals[i]);
+    } else {
+      for (int c = c0; c < p.C; ++c) {
+        float v1[1];
+        conv_silu<1>(p, b, t, c, v1);
+        act[c] = f32_to_bf16_rne(v1[0]);
+      }
+    }
+  } else if (unit == n_qk + n_v) {
+    // Per-head decay and write strength.
+    for (int h = lane; h < p.Hv; h += 64) {
+      const float av = ldbf(p.a + b * p.a_sb + (int64_t)t * p.a_st + h);
+      const float bv = ldbf(p.b + b * p.b_sb + (int64_t)t * p.b_st + h);
+      const float gv = __expf(-__expf(p.A_log[h]) * softplus(av + ldbf(p.dt_bias + h)));
+      p.g[(int64_t)bt * p.Hv + h] = gv;
+      p.beta[(int64_t)bt * p.Hv + h] = sigmoid(bv);
+    }
+  } else {
+    // New conv window = the last K-1 rows of concat(conv_state, qkv): row r
+    // is stream row T + r.  Token t writes the rows that are qkv[t]; token 0
+    // also writes rows still coming from the old state (when T < K-1).  This
+    // unit copies channels [c0, c0 + 512) of those rows, 8 per lane.
+    const int c0 = (unit - n_qk - n_v - 1) * 512 + lane * 8;
+    const int K1 = p.K - 1;
+    for (int r = 0; r < K1; ++r) {
+      const int s = p.T + r;
+      const bool mine = (s >= K1) ? (s - K1 == t) : (t == 0);
+      if (!mine) continue;
+      uint16_t* dst = p.new_conv_state + ((int64_t)b * K1 + r) * p.C;
+      const uint16_t* src = s >= K1 ? p.qkv + b * p.qkv_sb + (int64_t)(s - K1) * p.qkv_st
+                                    : p.conv_state + ((int64_t)b * K1 + s) * p.C;
+      uint16_t tmp[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (c0 + i < p.C) tmp[i] = src[c0 + i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (c0 + i < p.C) dst[c0 + i] = tmp[i];
+    }
+  }
+}
+
+struct NormParams {
+  const uint16_t* x;  // [rows, D] bf16 contiguous (scan out [B,T,Hv,Dv])
+  const uint16_t* z;  // gate, [B, T, Hv, D] with strides
+  int64_t z_sb, z_st, z_sh;
+  const uint16_t* w;  // [D] bf16
+  uint16_t* y;        // [rows, D] bf16
+  int T, H, D, rows;
+  float eps;
+};
+
+// One wavefront per (b, t, h) row of D channels; 4 rows per workgroup.
+__global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const NormParams p) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= p.rows) return;
+  const int h = row % p.H;
+  const int bt = row / p.H;
+  const int t = bt % p.T;
+  const int b = bt / p.T;
+  const uint16_t* x = p.x + (int64_t)row * p.D;
+  const uint16_t* z = p.z + b * p.z_sb + (int64_t)t * p.z_st + (int64_t)h * p.z_sh;
+  const int per = p.D / 64;
+  float xv[4];
+  float ss = 0.f;
+  for (int i = 0; i < per; ++i) {
+    xv[i] = ldbf(x + i * 64 + lane);
+    ss = fmaf(xv[i], xv[i], ss);
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / (float)p.D + p.eps);
+  for (int i = 0; i < per; ++i) {
+    const int c = i * 64 + lane;
+    p.y[(int64_t)row * p.D + c] = f32_to_bf16_rne(xv[i] * r * ldbf(p.w + c) * silu(ldbf(z + c)));
+  }
+}
+
+}  // namespace
+}  // namespace dflash
+
+extern "C" int dflash_gdn_prologue(const void* qkv, int64_t qkv_batch_stride,
+                                   int64_t qkv_row_stride, const void* conv_state,
+                                   const void* conv_weight, const void* a, const void* b,
+                                   const int64_t* ab_strides, const float* A_log,
+                                   const void* dt_bias, void* act, float* g, float* beta,
+                                   void* new_conv_state, int B, int T, int K, int Hk, int Hv,
+                                   int Dk, int Dv, float eps, void* stream) {
+  using namespace dflash;
+  if (B < 0 || T < 0 || K < 1 || K > kMaxConvTaps || Hk <= 0 || Hv <= 0 || Dk <= 0 || Dv <= 0)
+    return DFLASH_ERR_SHAPE;
+  if (Hv % Hk != 0) return DFLASH_ERR_SHAPE;
+  if (Dk % 64 != 0 || Dk > 256) return DFLASH_ERR_UNSUPPORTED;
+  if (B == 0 || T == 0) return DFLASH_OK;
+  if (qkv == nullptr || (K > 1 && conv_state == nullptr) || conv_weight == nullptr ||
+      a == nullptr || b == nullptr || A_log == nullptr || dt_bias == nullptr || act == nullptr ||
+      g == nullptr || beta == nullptr || (K > 1 && new_conv_state == nullptr))
+    return DFLASH_ERR_NULL;
+  if (K > 1 && new_conv_state == conv_state) return DFLASH_ERR_SHAPE;  // see the header
+  if (((uintptr_t)qkv | (uintptr_t)conv_state | (uintptr_t)conv_weight | (uintptr_t)a |
+       (uintptr_t)b | (uintptr_t)dt_bias | (uintptr_t)act | (uintptr_t)new_conv_state) & 1)
+    return DFLASH_ERR_ALIGN;
+  ProParams p{};
+  p.qkv = static_cast<const uint16_t*>(qkv);
+  p.qkv_sb = qkv_batch_stride;
+  p.qkv_st = qkv_row_stride;
+  p.conv_state = static_cast<const uint16_t*>(conv_state);
+  p.conv_w = static_cast<const uint16_t*>(conv_weight);
+  p.a = static_cast<const uint16_t*>(a);
+  p.b = static_cast<const uint16_t*>(b);
+  const int64_t C = 2LL * Hk * Dk + (int64_t)Hv * Dv;
+  if (ab_strides != nullptr) {
+    p.a_sb = ab_strides[0]; p.a_st = ab_strides[1]; p.b_sb = ab_strides[2]; p.b_st = ab_strides[3];
+  } else {
+    p.a_st = p.b_st = Hv;
+    p.a_sb = p.b_sb = (int64_t)T * Hv;
+  }
+  p.A_log = A_log;
+  p.dt_bias = static_cast<const uint16_t*>(dt_bias);
+  p.act = static_cast<uint16_t*>(act);
+  p.g = g;
+  p.beta = beta;
+  p.new_conv_state = static_cast<uint16_t*>(new_conv_state);
+  p.T = T;
+  p.C = (int)C;
+  p.K = K;
+  p.Hk = Hk;
+  p.Hv = Hv;
+  p.Dk = Dk;
+  p.eps = eps;
+  p.k_scale = 1.0f / sqrtf((float)Dk);
+  p.q_scale = p.k_scale * p.k_scale;
+  const int64_t units = 2LL * Hk + ceil_div(C - 2LL * Hk * Dk, 256) + 1 + ceil_div(C, 512);
+  const dim3 grid(B * T, (unsigned)ceil_div(units, 4));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (Dk / 64) {
+    case 1: hipLaunchKernelGGL(gdn_prologue_kernel<1>, grid, dim3(256), 0, s, p); break;
+    case 2: hipLaunchKernelGGL(gdn_prologue_kernel<2>, grid, dim3(256), 0, s, p); break;
+    case 3: hipLaunchKernelGGL(gdn_prologue_kernel<3>, grid, dim3(256), 0, s, p); break;
+    default: hipLaunchKernelGGL(gdn_prologue_kernel<4>, grid, dim3(256), 0, s, p); break;
+  }
+  return to_status(hipGetLastError());
+}
+
+extern "C" int dflash_gdn_gated_rmsnorm(const void* x, const void* z, const int64_t* z_strides,
+                                        const void* weight, void* y, int B, int T, int H, int D,
+                                        float eps, void* stream) {
+  using namespace dflash;
+  if (B < 0 || T < 0 || H <= 0 || D <= 0) return DFLASH_ERR_SHAPE;
+  if (D % 64 != 0 || D > 256) return DFLASH_ERR_UNSUPPORTED;
+  if (B == 0 || T == 0) return DFLASH_OK;
+  if (x == nullptr || z == nullptr || weight == nullptr || y == nullptr) return DFLASH_ERR_NULL;
+  if (((uintptr_t)x | (uintptr_t)z | (uintptr_t)weight | (uintptr_t)y) & 1) return DFLASH_ERR_ALIGN;
+  NormParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.z = static_cast<const uint16_t*>(z);
+  if (z_strides != nullptr) {
+    p.z_sb = z_strides[0]; p.z_st = z_strides[1]; p.z_sh = z_strides[2];
+  } else {
+    p.z_sh = D; p.z_st = (int64_t)H * D; p.z_sb = (int64_t)T * H * D;
+  }
+  p.w = static_cast<const uint16_t*>(weight);
+  p.y = static_cast<uint16_t*>(y);
+  p.T = T;
+  p.H = H;
+  p.D = D;
+  p.rows = B * T * H;
+  p.eps = eps;
+  hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3((unsigned)ceil_div(p.rows, 4)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), p);
+  return to_status(hipGetLastError());
+}

@@ -47,6 +47,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_VP, _I, _I64, _I64, _VP, _I64, _I, _VP, _VP, _VP, _I, _I, _I, _VP, _SZ, _VP],
     ),
+    "dflash_gdn_prologue": (
+        _I,
+        [_VP, _I64, _I64, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
+         _I, _I, _I, _I, _I, _I, _I, ctypes.c_float, _VP],
+    ),
+    "dflash_gdn_gated_rmsnorm": (
+        _I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, ctypes.c_float, _VP]),
     "dflash_lm_head_accept_workspace_bytes": (_SZ, [_I, _I, _I]),
     "dflash_lm_head_greedy_accept": (
         _I,

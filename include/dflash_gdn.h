@@ -177,6 +177,50 @@ int dflash_greedy_accept(const void* logits, int logits_dtype,
                          size_t workspace_bytes, void* stream);
 
 /*
+ * Gated-delta layer prologue: everything between the input projections and
+ * the scan, in one launch.
+ *
+ * Replaces the layer body at dflash_mlx/custom_qwen35_model.py:431-450:
+ * conv_input = concat(conv_state, qkv); causal depthwise conv1d (weight
+ * [C, K, 1], :718-725) + silu; split into q | k | v heads; q <- Dk^-1 *
+ * rms_norm(q, eps), k <- Dk^-1/2 * rms_norm(k, eps); beta = sigmoid(b);
+ * g = compute_g(A_log, a, dt_bias) = exp(-exp(A_log) * softplus(a + dt_bias))
+ * (mlx-lm 0.31.2, the published Qwen3-Next decay); new conv window
+ * conv_input[:, -(K-1):] (:434).
+ *
+ * qkv: bf16 [B, T, C], C = 2*Hk*Dk + Hv*Dv contiguous, batch/row strides in
+ * elements; conv_state bf16 [B, K-1, C] contiguous; conv_weight bf16 [C, K];
+ * a, b bf16 [B, T, Hv] with strides {a_b, a_t, b_b, b_t} (NULL: contiguous);
+ * A_log fp32 [Hv]; dt_bias bf16 [Hv].  Outputs: act bf16 [B, T, C] holding
+ * q | k | v (the scan reads them as strided views), g and beta fp32
+ * [B, T, Hv], new_conv_state bf16 [B, K-1, C], which must not alias
+ * conv_state.  All arithmetic is fp32; only act is rounded (to bf16).
+ * Supported: Dk % 64 == 0, Dk <= 256, 1 <= K <= 8.
+ */
+int dflash_gdn_prologue(const void* qkv, int64_t qkv_batch_stride,
+                        int64_t qkv_row_stride, const void* conv_state,
+                        const void* conv_weight, const void* a, const void* b,
+                        const int64_t* ab_strides, const float* A_log,
+                        const void* dt_bias, void* act, float* g, float* beta,
+                        void* new_conv_state, int B, int T, int K, int Hk,
+                        int Hv, int Dk, int Dv, float eps, void* stream);
+
+/*
+ * Gated-delta layer epilogue: y = weight * x * rsqrt(mean(x^2) + eps) *
+ * silu(z) over each (b, t, h) row of D channels.
+ *
+ * Replaces RMSNormGated(out, z) (dflash_mlx/custom_qwen35_model.py:478;
+ * mlx-lm qwen3_next, the published Qwen3-Next gated norm).
+ * x bf16 [B, T, H, D] contiguous (the scan's out); z bf16 [B, T, H, D] with
+ * element strides {b, t, h} (NULL: contiguous), D contiguous; weight bf16
+ * [D]; y bf16 [B, T, H, D] contiguous.  Supported: D % 64 == 0, D <= 256.
+ */
+int dflash_gdn_gated_rmsnorm(const void* x, const void* z,
+                             const int64_t* z_strides, const void* weight,
+                             void* y, int B, int T, int H, int D, float eps,
+                             void* stream);
+
+/*
  * Fused greedy LM head + accept: the same outputs as dflash_greedy_accept on
  * logits = hidden . weight^T, without materialising the logits.
  *

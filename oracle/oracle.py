@@ -261,3 +261,61 @@ def bf16_round(x) -> np.ndarray:
     out = r.astype(np.uint32).view(np.float32).copy()
     out[nan] = np.nan
     return out
+
+
+# ------------------------------------------------ gated-delta layer prologue
+
+def silu(x):
+    return x / (1.0 + np.exp(-x))
+
+
+def softplus(x):
+    return np.logaddexp(0.0, x)
+
+
+def rms_norm(x, eps):
+    """mx.fast.rms_norm(x, None, eps): x / sqrt(mean(x^2, -1) + eps)."""
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps)
+
+
+def compute_g(A_log, a, dt_bias):
+    """mlx-lm compute_g (not vendored; the published Qwen3-Next decay):
+    exp(-exp(A_log) * softplus(a + dt_bias))."""
+    return np.exp(-np.exp(np.asarray(A_log, np.float64)) *
+                  softplus(np.asarray(a, np.float64) + np.asarray(dt_bias, np.float64)))
+
+
+def gdn_prologue(qkv, conv_state, conv_w, a, b, A_log, dt_bias, Hk, Hv, Dk, Dv, eps=1e-6):
+    """fp64 restatement of custom_qwen35_model.py:431-450.
+
+    qkv [B,T,C], conv_state [B,K-1,C], conv_w [C,K] (MLX [C,K,1] layout),
+    a, b [B,T,Hv], A_log, dt_bias [Hv].  Returns (q [B,T,Hk,Dk],
+    k [B,T,Hk,Dk], v [B,T,Hv,Dv], g, beta [B,T,Hv], new_conv_state)."""
+    qkv = np.asarray(qkv, np.float64)
+    st = np.asarray(conv_state, np.float64)
+    w = np.asarray(conv_w, np.float64)
+    B, T, C = qkv.shape
+    K = w.shape[1]
+    x = np.concatenate([st, qkv], axis=1)                    # [B, K-1+T, C]
+    new_state = x[:, x.shape[1] - (K - 1):] if K > 1 else st
+    conv = np.zeros((B, T, C))
+    for j in range(K):                                        # cross-correlation, no flip
+        conv += w[None, None, :, j] * x[:, j:j + T]
+    act = silu(conv)
+    kd = Hk * Dk
+    q = act[..., :kd].reshape(B, T, Hk, Dk)
+    k = act[..., kd:2 * kd].reshape(B, T, Hk, Dk)
+    v = act[..., 2 * kd:].reshape(B, T, Hv, Dv)
+    inv = Dk ** -0.5
+    q = inv * inv * rms_norm(q, eps)
+    k = inv * rms_norm(k, eps)
+    g = compute_g(A_log, a, dt_bias)
+    beta = 1.0 / (1.0 + np.exp(-np.asarray(b, np.float64)))
+    return q, k, v, g, beta, new_state
+
+
+def gated_rmsnorm(x, z, weight, eps=1e-6):
+    """RMSNormGated (mlx-lm qwen3_next, not vendored; published Qwen3-Next
+    form): weight * rms_norm(x) * silu(z) over the last axis."""
+    x = np.asarray(x, np.float64)
+    return np.asarray(weight, np.float64) * rms_norm(x, eps) * silu(np.asarray(z, np.float64))
