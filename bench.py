@@ -49,6 +49,8 @@ def parse_args():
                     help="bounded CPU-baseline sample (0 disables it)")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the measurements of the next-row kernels (fused LM head)")
+    ap.add_argument("--only", choices=("lm_head", "layer", "prefill"), default=None,
+                    help="measure one next-row kernel alone and print its JSON (for profiling)")
     ap.add_argument("--probe", action="store_true",
                     help="for rocprofv3 --pmc runs: 3 explicit scans, 3 fused scans and 3 "
                          "calibration copies of 256 MiB, then exit without timing")
@@ -116,7 +118,7 @@ def time_steps(torch, K: int, phases):
 
 
 def measure_lm_head(torch, dev, M=16, H=2560, V=151936, n=50):
-    """§8(f) row 1: fused greedy LM head + accept (MFMA, no logits) at the
+    """Fused greedy LM head + accept (MFMA, no logits) at the
     Qwen3.5-4B shape vs the unfused path (hipBLASLt bf16 logits via a 2-D
     F.linear, then the greedy-accept kernel).  HBM-bound on the weight."""
     from dflash_mlx.runtime import greedy_accept, lm_head_greedy_accept
@@ -159,6 +161,71 @@ def measure_lm_head(torch, dev, M=16, H=2560, V=151936, n=50):
     }
 
 
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def chunked_prefill_flops(T: int, heads: int, chunk: int = 64, D: int = 128) -> int:
+    """Algorithmic flops of the chunked prefill (one multiply-add = 2), counted
+    once per product of the chunk form regardless of how many bf16 passes the
+    kernels spend on it: K K^T, Q K^T, W = T'K, U~ = T_b V (phase 1) and
+    W S^T, Q S^T, P U, U^T K (phase 2) per (head, chunk), plus the triangular
+    inverse (C^3 / 3)."""
+    nc = -(-T // chunk)
+    per = (2 * chunk * chunk * D * 2 + 2 * chunk * chunk * D * 2
+           + 3 * chunk * D * D * 2 + chunk * chunk * D * 2 + chunk ** 3 // 3)
+    return heads * nc * per
+
+
+def measure_prefill(torch, dev, n=10):
+    """Chunked (WY / UT-transform) prefill on MFMA at config c3 (B=1,
+    T=8192, Hk=16, Hv=32, Dk=Dv=128, zero initial state) against the
+    sequential scan kernel on the same inputs."""
+    from dflash_mlx.gated_delta import (chunked_prefill_workspace_bytes, gated_delta_kernel,
+                                        gated_delta_prefill)
+    from dflash_mlx.workloads import CONFIGS, make_scan_inputs
+
+    cfg = CONFIGS[3]
+    x = make_scan_inputs(cfg)
+    d = {k: v.to(dev) for k, v in x.items() if not k.startswith("_")}
+    ws = torch.empty(chunked_prefill_workspace_bytes(cfg.B, cfg.T, cfg.Hv), dtype=torch.uint8,
+                     device=dev)
+    args = (d["q"], d["k"], d["v"], d["g"], d["beta"], d["state"])
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / reps
+
+    chunked_us = timed(lambda: gated_delta_prefill(*args, workspace=ws), n)
+    seq_us = timed(lambda: gated_delta_kernel(*args), 3)
+    tokens = cfg.B * cfg.T
+    flops = chunked_prefill_flops(cfg.T, cfg.B * cfg.Hv)
+    hbm = (2 * tokens * (2 * cfg.Hk * cfg.Dk + 2 * cfg.Hv * cfg.Dv) + 8 * tokens * cfg.Hv
+           + 2 * 4 * cfg.B * cfg.Hv * cfg.Dv * cfg.Dk)
+    tflops = flops / (chunked_us / 1e6) / 1e12
+    return {
+        "workload": cfg.name,
+        "shape": {"B": cfg.B, "T": cfg.T, "Hk": cfg.Hk, "Hv": cfg.Hv, "Dk": cfg.Dk, "Dv": cfg.Dv,
+                  "chunk": 64},
+        "chunked_us": round(chunked_us, 1),
+        "sequential_us": round(seq_us, 1),
+        "speedup_vs_sequential": round(seq_us / chunked_us, 2),
+        "tokens_per_s": round(tokens / (chunked_us / 1e6), 1),
+        "flops_alg": flops,
+        "tflops": round(tflops, 2),
+        "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "hbm_bytes_alg": hbm,
+        "hbm_frac": round(hbm / (chunked_us / 1e6) / 1e9 / PEAK_HBM_GBPS, 4),
+        "note": "per call incl. Python dispatch; two kernels (chunk prep, chunk state)",
+    }
+
+
 def _graph_time_us(torch, fn, n=20):
     """Average replay time of a HIP graph capturing fn (µs)."""
     s = torch.cuda.Stream()
@@ -182,7 +249,7 @@ def _graph_time_us(torch, fn, n=20):
 
 
 def measure_layer(torch, dev, L=24, B=1, T=16):
-    """§8(f) row 2: the gated-delta layer between its projections (prologue ->
+    """The gated-delta layer between its projections (prologue ->
     scan -> gated-norm epilogue) for L layers of the Qwen3.5-4B shape, each
     phase captured as one HIP graph of L launches, against the same prologue
     and epilogue written as torch op chains."""
@@ -307,10 +374,16 @@ def main() -> int:
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, "
               f"WORLD_SIZE={world}); this build runs on a single MI355X and the verify scan "
-              "would shard across GPUs with no communication (see DESIGN.md)", file=sys.stderr)
+              "would shard across GPUs by (sequence, head) with no communication", file=sys.stderr)
         return 2
 
     import torch
+
+    if args.only is not None:
+        dev = torch.device("cuda", 0)
+        fn = {"lm_head": measure_lm_head, "layer": measure_layer, "prefill": measure_prefill}
+        print(json.dumps({args.only: fn[args.only](torch, dev)}), flush=True)
+        return 0
 
     from dflash_mlx.step import StepShape, VerifyStepRunner
     from dflash_mlx.workloads import CONFIGS, ScanConfig, make_accept_inputs, make_scan_inputs
@@ -435,6 +508,8 @@ def main() -> int:
         line["next_rows"] = {"lm_head_greedy_accept": measure_lm_head(torch, dev)}
         print("[bench] next rows: gated-delta layer prologue/epilogue", file=sys.stderr, flush=True)
         line["next_rows"]["gdn_layer"] = measure_layer(torch, dev)
+        print("[bench] next rows: chunked prefill (config c3)", file=sys.stderr, flush=True)
+        line["next_rows"]["chunked_prefill"] = measure_prefill(torch, dev)
     if args.cpu_seconds > 0:
         print(f"[bench] cpu baseline (~{args.cpu_seconds:.0f} s)", file=sys.stderr, flush=True)
         line["cpu_baseline"] = cpu_baseline(cfg, x, acc, (conv_in, qkv), args.cpu_seconds)

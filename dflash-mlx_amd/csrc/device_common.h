@@ -23,11 +23,13 @@ __device__ __forceinline__ float bf16_hi(uint32_t packed) {
 
 // fp32 -> bf16, round to nearest, ties to even; NaN stays a quiet NaN.
 // This is the rounding torch's Tensor.to(torch.bfloat16) applies.
+// Branch-free (a select, not a jump), so it does not split the caller's basic
+// blocks around memory operations.
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t quiet_nan = (u >> 16) | 0x0040u;
+  return (uint16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? quiet_nan : rounded);
 }
 
 // fp16 -> fp32 (exact).

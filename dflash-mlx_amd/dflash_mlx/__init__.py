@@ -16,8 +16,10 @@ from .adapters import (
 from .cache import ArraysCache, KVCache
 from .gated_delta import (
     advance_gated_delta_states,
+    chunked_prefill_workspace_bytes,
     conv_rollback,
     gated_delta_kernel,
+    gated_delta_prefill,
     gated_delta_verify,
     gated_delta_verify_rollback,
     tape_select,
@@ -37,8 +39,10 @@ __all__ = [
     "Qwen35TargetAdapter",
     "adapter_for_model_type",
     "advance_gated_delta_states",
+    "chunked_prefill_workspace_bytes",
     "conv_rollback",
     "gated_delta_kernel",
+    "gated_delta_prefill",
     "gated_delta_verify",
     "gated_delta_verify_rollback",
     "greedy_accept",

@@ -18,7 +18,7 @@ INCLUDE_DIR = ROOT_DIR.parent / "include"
 LIB_NAME = "libdflash_gfx950.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 
-SOURCES = ["gdn_scan.hip", "gdn_layer_ops.hip", "greedy_accept.hip", "lm_head_argmax.hip",
+SOURCES = ["gdn_scan.hip", "gdn_layer_ops.hip", "gdn_chunked.hip", "greedy_accept.hip", "lm_head_argmax.hip",
            "rollback.hip", "abi.cpp"]
 HEADERS = ["device_common.h", "host_common.h", "accept_common.h"]
 

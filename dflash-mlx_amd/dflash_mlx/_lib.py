@@ -42,6 +42,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP, _VP],
     ),
+    "dflash_gdn_chunked_prefill_workspace_bytes": (_SZ, [_I, _I, _I, _I, _I]),
+    "dflash_gdn_chunked_prefill": (
+        _I,
+        [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP, _VP, _SZ, _VP],
+    ),
     "dflash_greedy_accept_workspace_bytes": (_SZ, [_I, _I, _I]),
     "dflash_greedy_accept": (
         _I,

@@ -143,6 +143,45 @@ def gated_delta_kernel(q, k, v, g, beta, state, mask=None):
     return out, final
 
 
+def chunked_prefill_workspace_bytes(B: int, T: int, Hv: int, Dk: int = 128, Dv: int = 128) -> int:
+    return int(_lib.load().dflash_gdn_chunked_prefill_workspace_bytes(B, T, Hv, Dk, Dv))
+
+
+def gated_delta_prefill(q, k, v, g, beta, state, workspace: torch.Tensor | None = None):
+    """Prompt prefill of one gated-delta layer: (out, final_state), chunked form.
+
+    The recurrence of ``gated_delta_kernel`` evaluated 64 tokens at a time on
+    the matrix cores (the prompt pass gated_delta_update,
+    custom_qwen35_model.py:790-801).  Agrees with the sequential scan to fp32
+    rounding.  ``workspace``: optional uint8 device buffer of at least
+    ``chunked_prefill_workspace_bytes(B, T, Hv)`` bytes (else allocated)."""
+    B, T, Hk, Hv, Dk, Dv = _check_scan_inputs(q, k, v, g, beta, state)
+    q, k, v, g, beta, state, strides = _prep(q, k, v, g, beta, state)
+    dev = k.device
+    out = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
+    final = torch.empty((B, Hv, Dv, Dk), dtype=_STATE_DTYPE, device=dev)
+    if B == 0 or T == 0:
+        final.copy_(state)
+        return out, final
+    need = chunked_prefill_workspace_bytes(B, T, Hv, Dk, Dv)
+    if need == 0:
+        raise ValueError(f"chunked prefill supports Dk == Dv == 128 (got Dk={Dk}, Dv={Dv})")
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    elif workspace.numel() * workspace.element_size() < need:
+        raise ValueError(f"workspace holds {workspace.numel() * workspace.element_size()} bytes, "
+                         f"{need} needed")
+    _require_device("workspace", workspace, dev)
+    _lib.call(
+        "dflash_gdn_chunked_prefill",
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(g), _lib.ptr(beta), state.data_ptr(),
+        out.data_ptr(), final.data_ptr(), B, T, Hk, Hv, Dk, Dv, strides,
+        workspace.data_ptr(), workspace.numel() * workspace.element_size(),
+        _lib.stream_handle(dev),
+    )
+    return out, final
+
+
 def gated_delta_verify_rollback(q, k, v, g, beta, state, prev_tape, prev_accepted,
                                 accepted_period: int | None = None, tape_out=None):
     """Verify scan with the previous step's rollback fused into the state load.

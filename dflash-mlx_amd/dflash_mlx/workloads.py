@@ -51,6 +51,7 @@ CONFIGS: dict[int, ScanConfig] = {
                   state_std=0.05, V=151936, seed=1),
     2: ScanConfig("c2-batched-b32", B=32, T=16, Hk=16, Hv=32, Dk=128, Dv=128, state_std=0.05,
                   V=151936, seed=2),
+    3: ScanConfig("c3-prefill-8k", B=1, T=8192, Hk=16, Hv=32, Dk=128, Dv=128, seed=3),
 }
 
 

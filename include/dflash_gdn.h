@@ -142,6 +142,34 @@ int dflash_gdn_replay(const void* k, const void* v, const float* g,
                       void* stream);
 
 /*
+ * Prompt prefill of one gated-delta layer in chunked (WY / UT-transform) form.
+ *
+ * Replaces the prompt-pass scan mlx_lm gated_delta_update(q, k, v, a, b,
+ * A_log, dt_bias, state) (dflash_mlx/custom_qwen35_model.py:790-801, reached
+ * from the prefill at dflash_mlx/runtime.py:384-388) for long prompts: the
+ * same recurrence as dflash_gdn_verify_scan (same q/k/v/g/beta/state layouts
+ * and strides; out and final_state; no tape, no lengths), evaluated over
+ * chunks of 64 tokens so the token-token and token-state products run on the
+ * matrix cores.  Results agree with the sequential scan to fp32 rounding
+ * (the order of the sums differs), not bit for bit.
+ *
+ * workspace: device memory of at least
+ * dflash_gdn_chunked_prefill_workspace_bytes(B, T, Hv, Dk, Dv) bytes,
+ * 16-byte aligned, no initial contents needed (about 82 KB per head per
+ * 64 tokens).  final_state may be NULL and must not alias state_in.
+ * Supported: Dk == Dv == 128, Hv % Hk == 0.
+ */
+size_t dflash_gdn_chunked_prefill_workspace_bytes(int B, int T, int Hv,
+                                                  int Dk, int Dv);
+int dflash_gdn_chunked_prefill(const void* q, const void* k, const void* v,
+                               const float* g, const float* beta,
+                               const float* state_in, void* out,
+                               float* final_state, int B, int T, int Hk,
+                               int Hv, int Dk, int Dv, const int64_t* strides,
+                               void* workspace, size_t workspace_bytes,
+                               void* stream);
+
+/*
  * Greedy verify accept: argmax over the vocabulary, then the longest prefix of
  * the draft that agrees with it.
  *

@@ -167,6 +167,72 @@ def scan_matrix_form(q, k, v, g, beta, state):
     return out, S, (np.stack(tape, axis=0) if T else None)
 
 
+def chunk_intermediates(k, v, g, beta, chunk: int = 64):
+    """Per-chunk quantities of the chunked (WY / UT-transform) evaluation of
+    the scan, fp64, for one head: k [T, Dk], v [T, Dv], g, beta [T].
+
+    Per chunk of C tokens (the last one zero-padded: k = v = 0, beta = 0,
+    g = 1) with G = cumsum(log g) and gamma = exp(G):
+      A[i,j] = beta_i exp(G_i - G_j) k_i.k_j (j < i),  T = (I + A)^-1 by
+      forward substitution, W = T diag(beta gamma) K, U~ = T diag(beta) V.
+    Returns a list of dicts with G, W, Ut, K per chunk."""
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    T_len, Dk = k.shape
+    Dv = v.shape[1]
+    res = []
+    for c0 in range(0, T_len, chunk):
+        n = min(chunk, T_len - c0)
+        K = np.zeros((chunk, Dk)); V = np.zeros((chunk, Dv))
+        bt = np.zeros(chunk); lg = np.zeros(chunk)
+        K[:n] = k[c0:c0 + n]; V[:n] = v[c0:c0 + n]
+        bt[:n] = beta[c0:c0 + n]; lg[:n] = np.log(np.asarray(g[c0:c0 + n], np.float64))
+        G = np.cumsum(lg)
+        i, j = np.indices((chunk, chunk))
+        A = np.where(j < i, bt[:, None] * np.exp(G[:, None] - G[None, :]) * (K @ K.T), 0.0)
+        Tm = np.zeros((chunk, chunk))
+        for r in range(chunk):
+            Tm[r] = -(A[r, :r] @ Tm[:r])
+            Tm[r, r] = 1.0
+        res.append(dict(n=n, G=G, K=K, W=Tm @ ((bt * np.exp(G))[:, None] * K),
+                        Ut=Tm @ (bt[:, None] * V)))
+    return res
+
+
+def scan_chunked_form(q, k, v, g, beta, state, chunk: int = 64):
+    """fp64 chunked statement of the scan (the evaluation order the chunked
+    prefill kernel uses), returning (out, final_state).  Per chunk, from S0:
+      U = U~ - W S0^T,  O = diag(gamma) Q S0^T + P U with
+      P[i,j] = exp(G_i - G_j) q_i.k_j (j <= i),
+      S = gamma_C S0 + (diag(exp(G_C - G)) U)^T K.
+    Agrees with the token-by-token recurrence up to rounding; the CPU tests
+    check that against scan_c and scan_matrix_form."""
+    q = np.asarray(q, np.float64)
+    B, T_len, Hk, Dk = q.shape
+    Hv, Dv = v.shape[2], v.shape[3]
+    rep = Hv // Hk
+    out = np.zeros((B, T_len, Hv, Dv))
+    fin = np.array(state, dtype=np.float64, copy=True)
+    for b in range(B):
+        for hv in range(Hv):
+            hk = hv // rep
+            S = fin[b, hv]
+            chunks = chunk_intermediates(k[b, :, hk], v[b, :, hv], g[b, :, hv], beta[b, :, hv],
+                                         chunk)
+            for ci, ch in enumerate(chunks):
+                c0, n, G = ci * chunk, ch["n"], ch["G"]
+                Q = np.zeros((chunk, Dk))
+                Q[:n] = q[b, c0:c0 + n, hk]
+                i, j = np.indices((chunk, chunk))
+                P = np.where(j <= i, np.exp(G[:, None] - G[None, :]) * (Q @ ch["K"].T), 0.0)
+                U = ch["Ut"] - ch["W"] @ S.T
+                O = np.exp(G)[:, None] * (Q @ S.T) + P @ U
+                S = np.exp(G[-1]) * S + (np.exp(G[-1] - G)[:, None] * U).T @ ch["K"]
+                out[b, c0:c0 + n, hv] = O[:n]
+            fin[b, hv] = S
+    return out, fin
+
+
 def advance_gated_delta_states(initial_states, keys, values, g, beta):
     """Replay contract of custom_qwen35_model.py:97-139: keys are already
     repeated to Hv heads; returns the state after all keys.shape[1] tokens

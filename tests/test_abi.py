@@ -35,6 +35,7 @@ def test_header_declares_expected_entry_points():
         "dflash_greedy_accept_workspace_bytes", "dflash_greedy_accept", "dflash_tape_select",
         "dflash_conv_rollback", "dflash_lm_head_accept_workspace_bytes",
         "dflash_lm_head_greedy_accept", "dflash_gdn_prologue", "dflash_gdn_gated_rmsnorm",
+        "dflash_gdn_chunked_prefill_workspace_bytes", "dflash_gdn_chunked_prefill",
     ])
 
 
