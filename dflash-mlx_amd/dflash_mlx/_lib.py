@@ -47,6 +47,20 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP, _VP, _SZ, _VP],
     ),
+    "dflash_add_rmsnorm": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, ctypes.c_float, _VP]),
+    "dflash_swiglu": (_I, [_VP, _VP, _I, _I, _VP]),
+    "dflash_attn_prep": (
+        _I,
+        [_VP, _I64, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _I, ctypes.c_float,
+         ctypes.c_float, _VP],
+    ),
+    "dflash_attn_verify_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
+    "dflash_attn_verify": (
+        _I,
+        [_VP, _VP, _VP, _VP, _VP, _I64, _VP, _I, _I, _I, _I, _I, _I, _I, ctypes.c_float, _VP,
+         _SZ, _VP],
+    ),
+    "dflash_commit_accept": (_I, [_VP, _VP, _VP, _I, _I, _VP]),
     "dflash_greedy_accept_workspace_bytes": (_SZ, [_I, _I, _I]),
     "dflash_greedy_accept": (
         _I,

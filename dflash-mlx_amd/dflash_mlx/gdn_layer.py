@@ -141,10 +141,10 @@ def gated_rmsnorm(x, z, weight, eps: float = 1e-6):
     if z.stride(-1) != 1:
         z = z.contiguous()
     y = torch.empty_like(x)
+    w = weight.to(torch.bfloat16).contiguous()  # held until the launch is enqueued
     strides = (ctypes.c_int64 * 3)(*z.stride()[:3])
-    _lib.call("dflash_gdn_gated_rmsnorm", x.data_ptr(), z.data_ptr(), strides,
-              weight.to(torch.bfloat16).contiguous().data_ptr(), y.data_ptr(), B, T, H, D,
-              float(eps), _lib.stream_handle(dev))
+    _lib.call("dflash_gdn_gated_rmsnorm", x.data_ptr(), z.data_ptr(), strides, w.data_ptr(),
+              y.data_ptr(), B, T, H, D, float(eps), _lib.stream_handle(dev))
     return y
 
 

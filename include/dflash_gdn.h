@@ -314,6 +314,87 @@ int dflash_conv_rollback(const void* const* conv_in, const void* const* qkv,
                          int64_t qkv_batch_stride, int64_t qkv_row_stride,
                          int elem_bytes, void* stream);
 
+/*
+ * ---- The rest of the hybrid target's verify step (config c4) ----
+ * Cache lengths `lens` are int32 [B] in device memory, so a whole verify step
+ * (append, attend, accept, commit) needs no host round trip.
+ */
+
+/*
+ * Residual add + RMSNorm of the decoder layers: DecoderLayer.__call__
+ * (dflash_mlx/custom_qwen35_model.py:841-845) with nn.RMSNorm input /
+ * post-attention layernorms (:824-827) and the final norm (:881).
+ *   h = bf16(x + r) -> h_out;  y = bf16(h * rsqrt(mean(h^2) + eps) * weight)
+ * r may be NULL (then h = x and h_out is not written).  x, r, h_out, y are
+ * bf16 [M, H] contiguous, weight bf16 [H]; h_out may alias x.  fp32
+ * arithmetic.  Supported: H % 8 == 0, H <= 4096.
+ */
+int dflash_add_rmsnorm(const void* x, const void* r, const void* weight,
+                       void* h_out, void* y, int M, int H, float eps,
+                       void* stream);
+
+/*
+ * The MLP's gating (mlx-lm Qwen3NextMLP, called at
+ * dflash_mlx/custom_qwen35_model.py:845): out = bf16(silu(gate) * up) with
+ * gate_up bf16 [M, 2I] = [gate | up] (one GEMM of the stacked gate/up
+ * projections) and out bf16 [M, I].  Supported: I % 8 == 0.
+ */
+int dflash_swiglu(const void* gate_up, void* out, int M, int I, void* stream);
+
+/*
+ * Gated full-attention layer, before the attention itself
+ * (forward_full_attention_layer_explicit, custom_qwen35_model.py:496-522):
+ * from the stacked q/k/v projection rows proj [B*T, proj_row_stride] bf16,
+ * laid out [Hq x (query D | gate D), Hkv x key D, Hkv x value D]:
+ *   q = rope(rms_norm(query) * q_norm_w)      -> q_out [B, T, Hq, D] bf16
+ *   k = rope(rms_norm(key) * k_norm_w)        -> k_cache[b, h, pos]
+ *   v                                          -> vt_cache[b, h, :, pos]
+ * with pos = lens[b] + t.  k_cache is [B, Hkv, Smax, D], vt_cache is the
+ * value cache transposed, [B, Hkv, D, Smax] (keys contiguous per feature).
+ * Rotary (nn.RoPE, traditional=False): feature i < rot_dims/2 pairs with
+ * i + rot_dims/2 at angle pos * rope_base^(-2i/rot_dims); features past
+ * rot_dims pass through.  Positions >= Smax are not written (the caller keeps
+ * lens + T <= Smax).  Supported: D == 128, rot_dims in {0,16,32,64,128}.
+ */
+int dflash_attn_prep(const void* proj, int64_t proj_row_stride,
+                     const void* q_norm_w, const void* k_norm_w,
+                     const int32_t* lens, void* k_cache, void* vt_cache,
+                     void* q_out, int B, int T, int Hq, int Hkv, int D,
+                     int Smax, int rot_dims, float rope_base, float eps,
+                     void* stream);
+
+/*
+ * Verify attention over the cache (custom_qwen35_model.py:524-534): causal
+ * SDPA of the T block queries against the lens[b] + T cached keys (query t
+ * sees keys 0 .. lens[b] + t), output * sigmoid(gate) with the gate read from
+ * the projection rows (head h at h*2D + D of row b*T + t).
+ *   out[b, t, h*D .. h*D+D) = bf16(softmax(scale * q k^T) v * sigmoid(gate))
+ * Split over 64-key ranges on MFMA, then one merge.  max_len is a host-side
+ * upper bound of lens[b] + T (it sizes the grid; max_len <= Smax).  Cache
+ * positions past lens[b] + T are read and given zero weight, so the caches
+ * must hold finite values there (allocate them zero-filled).  workspace: at
+ * least dflash_attn_verify_workspace_bytes(B, Hq, Hkv, max_len) bytes.
+ * Supported: D == 128, T <= 16, Hq / Hkv <= 4, Smax % 64 == 0.
+ */
+size_t dflash_attn_verify_workspace_bytes(int B, int Hq, int Hkv, int max_len);
+int dflash_attn_verify(const void* q, const void* k_cache,
+                       const void* vt_cache, const int32_t* lens,
+                       const void* gate_src, int64_t gate_row_stride,
+                       void* out, int B, int T, int Hq, int Hkv, int D,
+                       int Smax, int max_len, float scale, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/*
+ * Commit a greedy accept on the device: keep[b] = clamp(matched[b], 0, T-1)
+ * + 1 (the block's first token plus the accepted drafts, accepted_inputs of
+ * runtime.py:146) and, if lens is not NULL, lens[b] += keep[b] (the KV trim
+ * of adapters.py:505-508 seen from the other side: the caches keep the
+ * accepted positions).  keep feeds dflash_gdn_verify_scan_rollback and
+ * dflash_conv_rollback of the next step.
+ */
+int dflash_commit_accept(const int32_t* matched, int32_t* keep, int32_t* lens,
+                         int B, int T, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,230 @@
+"""The hybrid target's verify step (config c4) end to end on the GPU.
+
+* Parity: a small hybrid model (3 gated-delta layers + 1 attention layer,
+  hidden 256, ragged batch of 2 with different cache lengths) against the CPU
+  oracle of the whole step (oracle/hybrid_oracle.model_step, bf16 rounding at
+  the GPU path's points): final hidden and logits within 3e-2 of the oracle's
+  scale, the per-token state tape of the first layer within 1e-2, the greedy
+  accept exactly consistent with the GPU's own posterior, and the posterior
+  equal to the oracle's wherever the oracle's top-1 margin is clear.
+* Rollback, bit-exact: a step whose accept is forced to a tokens and the next
+  step give exactly the results and caches of a fresh run whose block agrees
+  only on those a tokens (causality of every mixer + the commit).
+* HIP graphs: forward and commit captured once and replayed for several steps
+  (with eager work between) equal eager steps bit for bit.
+* The full c4 shape runs (32 layers, 4096-token cache) and is deterministic.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from dflash_mlx.gdn_layer import GatedDeltaConfig
+from dflash_mlx.hybrid_model import HybridConfig, HybridVerifyRunner, HybridWeights
+from oracle import hybrid_oracle as ho
+from oracle import oracle as gdn_oracle
+
+pytestmark = pytest.mark.gpu
+
+SMALL = HybridConfig(hidden_size=256, num_hidden_layers=4, intermediate_size=512, vocab_size=1000,
+                     num_attention_heads=4, num_key_value_heads=1, head_dim=128,
+                     linear=GatedDeltaConfig(linear_num_key_heads=2, linear_num_value_heads=4))
+
+
+def _np(x):
+    return x.float().cpu().numpy().astype(np.float64)
+
+
+def _np_weights(w: HybridWeights):
+    layers = []
+    for lw in w.layers:
+        d = {k: _np(v) for k, v in lw.items() if k != "gdn"}
+        if "gdn" in lw:
+            g = lw["gdn"]
+            d.update(conv_w=_np(g.conv_weight), A_log=_np(g.A_log), dt_bias=_np(g.dt_bias),
+                     norm_w=_np(g.norm_weight))
+        layers.append(d)
+    return dict(embed=_np(w.embed), final_norm=_np(w.final_norm), lm_head=_np(w.lm_head),
+                layers=layers)
+
+
+def _initial_state(cfg, B, lens, seed):
+    lc = cfg.linear
+    gen = torch.Generator().manual_seed(seed)
+    K1, C = lc.linear_conv_kernel_dim - 1, lc.conv_dim
+    Hv, Dv, Dk = lc.linear_num_value_heads, lc.linear_value_head_dim, lc.linear_key_head_dim
+    S = max(lens)
+    conv = [torch.randn(B, K1, C, generator=gen).bfloat16() for _ in range(cfg.n_linear)]
+    rec = [0.05 * torch.randn(B, Hv, Dv, Dk, generator=gen) for _ in range(cfg.n_linear)]
+    k = [torch.randn(B, cfg.num_key_value_heads, S, cfg.head_dim, generator=gen).bfloat16()
+         for _ in range(cfg.n_attention)]
+    v = [torch.randn(B, cfg.num_key_value_heads, S, cfg.head_dim, generator=gen).bfloat16()
+         for _ in range(cfg.n_attention)]
+    for kk, vv in zip(k, v):  # positions past each sequence's length are empty
+        for b, L in enumerate(lens):
+            kk[b, :, L:] = 0
+            vv[b, :, L:] = 0
+    return dict(lens=list(lens), conv=conv, rec=rec, k=k, v=v)
+
+
+def _runner(cfg, w, st, B, T, Smax, device):
+    r = HybridVerifyRunner(cfg, w, B, T, Smax, device)
+    r.set_state(st["lens"], [c.to(device) for c in st["conv"]], [s.to(device) for s in st["rec"]],
+                [k.to(device) for k in st["k"]], [v.to(device) for v in st["v"]])
+    return r
+
+
+def test_small_hybrid_step_matches_oracle(device):
+    cfg, B, T, Smax = SMALL, 2, 16, 256
+    w = HybridWeights.random(cfg, device, seed=11, on_device=False)
+    st = _initial_state(cfg, B, [20, 100], seed=12)
+    tokens = torch.randint(0, cfg.vocab_size, (B, T), generator=torch.Generator().manual_seed(13),
+                           dtype=torch.int32)
+    run = _runner(cfg, w, st, B, T, Smax, device)
+    run.tokens.copy_(tokens)
+    print("[hybrid small] forward", flush=True)
+    run.forward_accept()
+    torch.cuda.synchronize()
+    o_state = dict(lens=np.array(st["lens"]), conv=[_np(c) for c in st["conv"]],
+                   rec=[_np(s) for s in st["rec"]], k=[_np(k) for k in st["k"]],
+                   v=[_np(v) for v in st["v"]])
+    ref = ho.model_step(cfg, _np_weights(w), o_state, tokens.numpy(), cfg.rms_norm_eps)
+    hid = _np(run.xn).reshape(B, T, -1)
+    hid_err = np.max(np.abs(hid - ref["hidden"])) / np.max(np.abs(ref["hidden"]))
+    logits = _np(run.logits())
+    log_err = np.max(np.abs(logits - ref["logits"])) / np.max(np.abs(ref["logits"]))
+    tape_err = np.max(np.abs(_np(run.tape[0]) - ref["tape"][0])) / np.max(np.abs(ref["tape"][0]))
+    print(f"  hidden rel {hid_err:.2e}  logits rel {log_err:.2e}  tape[0] rel {tape_err:.2e}",
+          flush=True)
+    assert hid_err <= 3e-2 and log_err <= 3e-2 and tape_err <= 1e-2
+    post = run.posterior.cpu().numpy()
+    matched = run.matched.cpu().numpy()
+    bonus = run.bonus.cpu().numpy()
+    toks = tokens.numpy()
+    for b in range(B):
+        m = gdn_oracle.longest_prefix_match(toks[b, 1:], post[b, :-1])
+        assert matched[b] == m and bonus[b] == post[b, m]
+    srt = np.sort(ref["logits"], axis=-1)
+    clear = (srt[..., -1] - srt[..., -2]) > 0.1 * np.max(np.abs(ref["logits"]))
+    assert np.array_equal(post[clear], ref["posterior"][clear])
+    print(f"  posterior equal on {int(clear.sum())} clear-margin rows of {B * T}", flush=True)
+
+
+def _force_step(run, keep_minus_one):
+    run.forward_accept()
+    run.matched.copy_(torch.tensor(keep_minus_one, dtype=torch.int32))
+    run.commit()
+
+
+def test_rollback_equals_fresh_prefix_run_bit_exact(device):
+    cfg, B, T, Smax = SMALL, 2, 16, 256
+    w = HybridWeights.random(cfg, device, seed=21, on_device=False)
+    st = _initial_state(cfg, B, [33, 64], seed=22)
+    g = torch.Generator().manual_seed(23)
+    x1 = torch.randint(0, cfg.vocab_size, (B, T), generator=g, dtype=torch.int32)
+    x2 = torch.randint(0, cfg.vocab_size, (B, T), generator=g, dtype=torch.int32)
+    keep = [5, 11]
+    y1 = x1.clone()
+    for b, a in enumerate(keep):  # agree only on the kept tokens
+        y1[b, a:] = (x1[b, a:] + 1 + b) % cfg.vocab_size
+    outs = []
+    for blk in (x1, y1):
+        run = _runner(cfg, w, st, B, T, Smax, device)
+        run.tokens.copy_(blk)
+        _force_step(run, [a - 1 for a in keep])
+        run.tokens.copy_(x2)
+        run.forward_accept()
+        torch.cuda.synchronize()
+        lens = run.lens.cpu().tolist()
+        assert lens == [L + a for L, a in zip(st["lens"], keep)]
+        kv = []
+        for kc, vc in zip(run.k_cache, run.vt_cache):
+            kv.append(torch.cat([kc[b, :, :lens[b] + T].flatten() for b in range(B)]))
+            kv.append(torch.cat([vc[b, :, :, :lens[b] + T].flatten() for b in range(B)]))
+        outs.append(dict(xn=run.xn.clone(), post=run.posterior.clone(), tape=[t.clone() for t in run.tape],
+                         state=[s.clone() for s in run.state], conv=[c.clone() for c in run.conv],
+                         kv=kv))
+    a, b = outs
+    print("[hybrid rollback] comparing", flush=True)
+    assert torch.equal(a["xn"], b["xn"])
+    assert torch.equal(a["post"], b["post"])
+    for k in ("tape", "state", "conv", "kv"):
+        for ta, tb in zip(a[k], b[k]):
+            assert torch.equal(ta, tb), k
+
+
+def test_graph_replays_equal_eager_steps(device):
+    cfg, B, T, Smax = SMALL, 2, 16, 256
+    w = HybridWeights.random(cfg, device, seed=31, on_device=False)
+    st = _initial_state(cfg, B, [40, 3], seed=32)
+    eager = _runner(cfg, w, st, B, T, Smax, device)
+    graphed = _runner(cfg, w, st, B, T, Smax, device)
+    graphed.forward_accept()  # first eager call (lazy per-device setup), then restore
+    torch.cuda.synchronize()
+    graphed.set_state(st["lens"], [c.to(device) for c in st["conv"]],
+                      [s.to(device) for s in st["rec"]], [k.to(device) for k in st["k"]],
+                      [v.to(device) for v in st["v"]])
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g_fwd, g_commit = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_fwd, stream=s):
+        graphed.forward_accept()
+    with torch.cuda.graph(g_commit, stream=s):
+        graphed.commit()
+    torch.cuda.synchronize()
+    gen = torch.Generator().manual_seed(33)
+    for step, forced in enumerate([[3, 0], [15, 7], [0, 9], [6, 6]]):
+        blk = torch.randint(0, cfg.vocab_size, (B, T), generator=gen, dtype=torch.int32)
+        eager.tokens.copy_(blk)
+        graphed.tokens.copy_(blk)
+        eager.forward_accept()
+        junk = torch.randn(1 << 18, device=device).sum()  # unrelated eager work
+        g_fwd.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(graphed.xn, eager.xn), step
+        assert torch.equal(graphed.posterior, eager.posterior), step
+        assert torch.equal(graphed.matched, eager.matched), step
+        for r in (eager, graphed):
+            r.matched.copy_(torch.tensor(forced, dtype=torch.int32))
+        eager.commit()
+        g_commit.replay()
+        torch.cuda.synchronize()
+        print(f"[hybrid graph step {step}] lens {graphed.lens.cpu().tolist()} junk {float(junk):.2f}",
+              flush=True)
+        assert torch.equal(graphed.lens, eager.lens)
+        assert torch.equal(graphed.keep, eager.keep)
+        for ta, tb in zip(graphed.conv + graphed.tape + graphed.k_cache + graphed.vt_cache,
+                          eager.conv + eager.tape + eager.k_cache + eager.vt_cache):
+            assert torch.equal(ta, tb), step
+
+
+def test_c4_full_shape_step_runs_and_is_deterministic(device):
+    cfg, B, T, Smax, L0 = HybridConfig(), 1, 16, 4160, 4096
+    print("[hybrid c4] building random weights on the device", flush=True)
+    w = HybridWeights.random(cfg, device, seed=41, on_device=True)
+    lc = cfg.linear
+    gen = torch.Generator(device=device).manual_seed(42)
+    conv = [torch.randn(B, 3, lc.conv_dim, generator=gen, device=device).bfloat16()
+            for _ in range(cfg.n_linear)]
+    rec = [0.05 * torch.randn(B, lc.linear_num_value_heads, 128, 128, generator=gen, device=device)
+           for _ in range(cfg.n_linear)]
+    k = [torch.randn(B, 4, L0, 128, generator=gen, device=device).bfloat16() for _ in range(cfg.n_attention)]
+    v = [torch.randn(B, 4, L0, 128, generator=gen, device=device).bfloat16() for _ in range(cfg.n_attention)]
+    tokens = torch.randint(0, cfg.vocab_size, (B, T), generator=gen, device=device, dtype=torch.int32)
+    results = []
+    for _ in range(2):
+        run = HybridVerifyRunner(cfg, w, B, T, Smax, device)
+        run.set_state([L0], conv, rec, k, v)
+        run.tokens.copy_(tokens)
+        run.step()
+        run.step()
+        torch.cuda.synchronize()
+        results.append((run.xn.clone(), run.posterior.clone(), run.lens.clone(), run.keep.clone()))
+        del run
+    (xa, pa, la, ka), (xb, pb, lb, kb) = results
+    print(f"[hybrid c4] lens {la.tolist()} keep {ka.tolist()} posterior[0,:4] {pa[0, :4].tolist()}",
+          flush=True)
+    assert torch.isfinite(xa.float()).all()
+    assert torch.equal(xa, xb) and torch.equal(pa, pb) and torch.equal(la, lb)
+    assert 1 <= int(ka[0]) <= T and int(la[0]) > L0
