@@ -67,26 +67,45 @@ __device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); 
 
 // ------------------------------------------------------------ add + RMSNorm
 // h = bf16(x + r) (the residual stream, stored to h_out), y = bf16(h *
-// rsqrt(mean(h^2) + eps) * w), fp32 arithmetic.  One wave per row; each lane
-// keeps its 8-element chunks in registers (H <= 512 * MAXC).
-template <int MAXC>
+// rsqrt(mean(h^2) + eps) * w), fp32 arithmetic.  The branch r is either bf16
+// [M, H] or (PART) the fp32 split-K partial sums of the projection that
+// produced it, rp[nsplit][M][H], rounded to bf16 after the sum (where the
+// projection's own output would be rounded).  One 256-thread workgroup per
+// row (verify steps have only B*T rows): thread t owns the 8-element chunks
+// t and t + 256 (H <= 4096), keeps them in registers, and issues all of its
+// loads (x, and every split of r) before using any.
+template <bool PART>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* x, const uint16_t* r,
+                                                          const float* rp, int nsplit,
                                                           const uint16_t* w, uint16_t* h_out,
                                                           uint16_t* y, int M, int H, float eps) {
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= M) return;
+  __shared__ float wsum[4];
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
   const int nch = H >> 3;
   const uint16_t* xr = x + (int64_t)row * H;
   const uint16_t* rr = r != nullptr ? r + (int64_t)row * H : nullptr;
-  float v[MAXC][8];
+  const bool has_r = PART || rr != nullptr;
+  float v[2][8];
   float ss = 0.f;
 #pragma unroll
-  for (int c = 0; c < MAXC; ++c) {
-    const int ch = lane + 64 * c;
+  for (int c = 0; c < 2; ++c) {
+    const int ch = tid + 256 * c;
     if (ch < nch) {
       unpack8(ld16(xr + ch * 8), v[c]);
-      if (rr != nullptr) {
+      if (PART) {
+        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+        const float* src = rp + (int64_t)row * H + ch * 8;
+        const int64_t sstride = (int64_t)M * H;
+#pragma unroll 8
+        for (int k = 0; k < nsplit; ++k) {
+          s0 += *reinterpret_cast<const f32x4*>(src + k * sstride);
+          s1 += *reinterpret_cast<const f32x4*>(src + k * sstride + 4);
+        }
+        const float rv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[c][e] = bf16_round(v[c][e] + bf16_round(rv[e]));
+      } else if (rr != nullptr) {
         float rv[8];
         unpack8(ld16(rr + ch * 8), rv);
 #pragma unroll
@@ -97,12 +116,15 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* x, con
     }
   }
   ss = wave_sum(ss);
+  if ((tid & 63) == 0) wsum[tid >> 6] = ss;
+  __syncthreads();
+  ss = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
   const float inv = 1.f / sqrtf(ss / (float)H + eps);
 #pragma unroll
-  for (int c = 0; c < MAXC; ++c) {
-    const int ch = lane + 64 * c;
+  for (int c = 0; c < 2; ++c) {
+    const int ch = tid + 256 * c;
     if (ch < nch) {
-      if (rr != nullptr && h_out != nullptr)
+      if (has_r && h_out != nullptr)
         *reinterpret_cast<u32x4*>(h_out + (int64_t)row * H + ch * 8) = pack8(v[c]);
       float wv[8], o[8];
       unpack8(ld16(w + ch * 8), wv);
@@ -444,28 +466,44 @@ __global__ void commit_accept_kernel(const int32_t* matched, int32_t* keep, int3
 
 using namespace dflash;
 
-extern "C" int dflash_add_rmsnorm(const void* x, const void* r, const void* weight, void* h_out,
-                                  void* y, int M, int H, float eps, void* stream) {
-  if (M < 0 || H <= 0 || H % 8 != 0 || H > 512 * 8) return DFLASH_ERR_SHAPE;
+namespace dflash {
+namespace {
+int launch_add_rmsnorm(const void* x, const void* r, const float* rp, int nsplit, const void* weight,
+                       void* h_out, void* y, int M, int H, float eps, void* stream) {
+  if (M < 0 || H <= 0 || H % 8 != 0 || H > 512 * 8 || nsplit < 0) return DFLASH_ERR_SHAPE;
   if (M == 0) return DFLASH_OK;
   if (x == nullptr || weight == nullptr || y == nullptr) return DFLASH_ERR_NULL;
-  if (((uintptr_t)x & 15) || ((uintptr_t)r & 15) || ((uintptr_t)weight & 15) ||
-      ((uintptr_t)h_out & 15) || ((uintptr_t)y & 15))
+  if (((uintptr_t)x & 15) || ((uintptr_t)r & 15) || ((uintptr_t)rp & 15) ||
+      ((uintptr_t)weight & 15) || ((uintptr_t)h_out & 15) || ((uintptr_t)y & 15))
     return DFLASH_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid((unsigned)ceil_div(M, 4));
+  const dim3 grid((unsigned)M);
   const auto* xp = static_cast<const uint16_t*>(x);
-  const auto* rp = static_cast<const uint16_t*>(r);
+  const auto* rpb = static_cast<const uint16_t*>(r);
   const auto* wp = static_cast<const uint16_t*>(weight);
   auto* hp = static_cast<uint16_t*>(h_out);
   auto* yp = static_cast<uint16_t*>(y);
-  if (H <= 512 * 2)
-    hipLaunchKernelGGL(add_rmsnorm_kernel<2>, grid, dim3(256), 0, s, xp, rp, wp, hp, yp, M, H, eps);
-  else if (H <= 512 * 5)
-    hipLaunchKernelGGL(add_rmsnorm_kernel<5>, grid, dim3(256), 0, s, xp, rp, wp, hp, yp, M, H, eps);
+  if (rp != nullptr)
+    hipLaunchKernelGGL(add_rmsnorm_kernel<true>, grid, dim3(256), 0, s, xp, nullptr, rp, nsplit, wp,
+                       hp, yp, M, H, eps);
   else
-    hipLaunchKernelGGL(add_rmsnorm_kernel<8>, grid, dim3(256), 0, s, xp, rp, wp, hp, yp, M, H, eps);
+    hipLaunchKernelGGL(add_rmsnorm_kernel<false>, grid, dim3(256), 0, s, xp, rpb, nullptr, 0, wp,
+                       hp, yp, M, H, eps);
   return to_status(hipGetLastError());
+}
+}  // namespace
+}  // namespace dflash
+
+extern "C" int dflash_add_rmsnorm(const void* x, const void* r, const void* weight, void* h_out,
+                                  void* y, int M, int H, float eps, void* stream) {
+  return launch_add_rmsnorm(x, r, nullptr, 0, weight, h_out, y, M, H, eps, stream);
+}
+
+extern "C" int dflash_add_rmsnorm_splitk(const void* x, const float* r_partials, int nsplit,
+                                         const void* weight, void* h_out, void* y, int M, int H,
+                                         float eps, void* stream) {
+  if (r_partials == nullptr || nsplit < 1) return DFLASH_ERR_NULL;
+  return launch_add_rmsnorm(x, nullptr, r_partials, nsplit, weight, h_out, y, M, H, eps, stream);
 }
 
 extern "C" int dflash_swiglu(const void* gate_up, void* out, int M, int I, void* stream) {

@@ -1,0 +1,294 @@
+// Verify-sized GEMMs: out[M, N] = x[M, K] . W[N, K]^T with M = B*T <= 64.
+//
+// Every projection of the hybrid target's verify step (the stacked
+// gated-delta in_proj, out_proj, the attention q/k/v and o projections, the
+// MLP gate/up and down; dflash_mlx/custom_qwen35_model.py:726-736 and the
+// Linear layers of mlx-lm Qwen3NextAttention / Qwen3NextMLP) is this shape: a
+// stream of the bf16 weight against 16 activation rows.  The kernel is built
+// for the stream:
+//   - A workgroup (4 waves) owns 64 * VT consecutive weight rows and a range
+//     of k-steps (split-K grid dimension); each wave owns 16 * VT rows.
+//   - Weight loads are coalesced (8 lanes read one row's 128-byte k-step line,
+//     8 rows per load instruction) and run D k-steps ahead in a register
+//     ring; each step goes through the wave's private LDS tile into MFMA
+//     fragment order (no barrier: a wave's LDS operations complete in order).
+//   - v_mfma_f32_16x16x32_bf16 with A = 16 weight rows, B = 16 activation
+//     rows (L2-resident); fp32 accumulation; lane (r16 = l % 16, g = l / 16)
+//     holds elements 16g .. 16g+15 of the 64-wide step for both operands, so
+//     the contraction is exact whatever order the hardware gives the k-slots.
+//   - Epilogue, nsplit == 1 requested: bf16 (round to nearest even) into
+//     out.  nsplit > 1 requested: fp32 partial sums into
+//     out_f32[split][M][N] for the splits actually used (see
+//     dflash_gemm_splits); the consumer sums them (dflash_add_rmsnorm_splitk,
+//     dflash_splitk_reduce).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "dflash_gdn.h"
+#include "device_common.h"
+#include "host_common.h"
+
+namespace dflash {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kGThreads = 256;
+constexpr int kGKStep = 64;
+constexpr int kGTileRowBytes = 128 + 16;
+
+struct GemmParams {
+  const uint16_t* x;
+  int64_t xs;  // activation row stride (elements)
+  const uint16_t* w;
+  int64_t ws;  // weight row stride (elements)
+  uint16_t* out;
+  int64_t os;  // output row stride (elements)
+  float* part;  // [nsplit][M][N] when f32_out
+  int M, N, K, nsplit, ks_per_split, f32_out;
+};
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+template <int MT, int VT>
+struct GStage {
+  u32x4 a[2 * VT];
+  u32x4 b[MT][2];
+};
+
+// KW = waves of the workgroup that share one group of weight rows: 1 (each
+// wave streams its own 16*VT rows over the split's k-range) or 4 (the four
+// waves stream the same 16*VT rows over quarters of the k-range and merge
+// their sums through LDS: four times the loads in flight per output tile,
+// without partial sums in memory).
+template <int MT, int VT, int D, int KW>
+__global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams p) {
+  __shared__ __attribute__((aligned(16))) unsigned char atile[kGThreads / 64][VT * 16 * kGTileRowBytes];
+  __shared__ f32x4 red[KW > 1 ? KW - 1 : 1][VT * MT][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+  constexpr int kRowGroups = (kGThreads / 64) / KW;  // row groups per workgroup
+  const int kpart = wave % KW;                        // this wave's quarter of the k-range
+  const int nwave = (blockIdx.x * kRowGroups + wave / KW) * VT * 16;
+  const int split = blockIdx.y;
+  const int nks_all = p.K / kGKStep;
+  const int split_begin = split * p.ks_per_split;
+  const int split_len = min(p.ks_per_split, nks_all - split_begin);
+  const int part_len = (split_len + KW - 1) / KW;
+  const int ks_begin = split_begin + min(kpart * part_len, split_len);
+  const int nks = min(part_len, split_begin + split_len - ks_begin);
+
+  const uint16_t* wrow[2 * VT];
+#pragma unroll
+  for (int i = 0; i < 2 * VT; ++i) {
+    const int n = min(nwave + i * 8 + (lane >> 3), p.N - 1);  // tail rows re-read row N-1
+    wrow[i] = p.w + (int64_t)n * p.ws + (int64_t)ks_begin * kGKStep + (lane & 7) * 8;
+  }
+  const uint16_t* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    xrow[mt] = p.x + (int64_t)min(mt * 16 + r16, p.M - 1) * p.xs + (int64_t)ks_begin * kGKStep + g * 16;
+
+  auto load = [&](GStage<MT, VT>& st, int ks) {
+    const int off = ks * kGKStep;
+#pragma unroll
+    for (int i = 0; i < 2 * VT; ++i) st.a[i] = *reinterpret_cast<const u32x4*>(wrow[i] + off);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      st.b[mt][0] = *reinterpret_cast<const u32x4*>(xrow[mt] + off);
+      st.b[mt][1] = *reinterpret_cast<const u32x4*>(xrow[mt] + off + 8);
+    }
+  };
+
+  f32x4 acc[VT][MT];
+#pragma unroll
+  for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[vt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  unsigned char* tile = atile[wave];
+
+  GStage<MT, VT> ring[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d)
+    if (d < nks) load(ring[d], d);
+
+  for (int ks0 = 0; ks0 < nks; ks0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int ks = ks0 + d;
+      if (ks < nks) {
+#pragma unroll
+        for (int i = 0; i < 2 * VT; ++i)
+          *reinterpret_cast<u32x4*>(tile + (i * 8 + (lane >> 3)) * kGTileRowBytes + (lane & 7) * 16) =
+              ring[d].a[i];
+        u32x4 a[VT][2];
+#pragma unroll
+        for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            a[vt][h] = *reinterpret_cast<const u32x4*>(tile + (vt * 16 + r16) * kGTileRowBytes + (2 * g + h) * 16);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int vt = 0; vt < VT; ++vt) {
+            acc[vt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                as_bf16x8(a[vt][0]), as_bf16x8(ring[d].b[mt][0]), acc[vt][mt], 0, 0, 0);
+            acc[vt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                as_bf16x8(a[vt][1]), as_bf16x8(ring[d].b[mt][1]), acc[vt][mt], 0, 0, 0);
+          }
+        if (ks + D < nks) load(ring[d], ks + D);
+      }
+    }
+  }
+
+  if (KW > 1) {  // merge the k-quarters: waves 1..KW-1 hand their sums to wave 0
+    if (kpart > 0) {
+#pragma unroll
+      for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) red[kpart - 1][vt * MT + mt][lane] = acc[vt][mt];
+    }
+    __syncthreads();
+    if (kpart > 0) return;
+#pragma unroll
+    for (int q = 0; q < KW - 1; ++q)
+#pragma unroll
+      for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[vt][mt] += red[q][vt * MT + mt][lane];
+  }
+  // Lane (r16, g) of tile (vt, mt) holds out[m = mt*16 + r16][n = nwave + vt*16 + 4g .. +3].
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + r16;
+    if (m >= p.M) continue;
+#pragma unroll
+    for (int vt = 0; vt < VT; ++vt) {
+      const int n = nwave + vt * 16 + 4 * g;
+      if (n >= p.N) continue;
+      const f32x4 v = acc[vt][mt];
+      if (p.f32_out) {
+        float* dst = p.part + ((int64_t)split * p.M + m) * p.N + n;
+        if (n + 4 <= p.N && (p.N & 3) == 0) {  // rows 16-byte aligned only when N % 4 == 0
+          *reinterpret_cast<f32x4*>(dst) = v;
+        } else {
+          for (int i = 0; i < min(4, p.N - n); ++i) dst[i] = v[i];
+        }
+      } else {
+        uint16_t* dst = p.out + (int64_t)m * p.os + n;
+        if (n + 4 <= p.N) {
+          *reinterpret_cast<u32x2*>(dst) =
+              u32x2{(uint32_t)f32_to_bf16_rne(v.x) | ((uint32_t)f32_to_bf16_rne(v.y) << 16),
+                    (uint32_t)f32_to_bf16_rne(v.z) | ((uint32_t)f32_to_bf16_rne(v.w) << 16)};
+        } else {
+          for (int i = 0; i < min(4, p.N - n); ++i) dst[i] = f32_to_bf16_rne(v[i]);
+        }
+      }
+    }
+  }
+}
+
+// out[m][n] = bf16(sum_s part[s][m][n]).
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, int nsplit, int M,
+                                                            int N, uint16_t* out, int64_t os) {
+  const int64_t nv = (int64_t)M * (N / 4);
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < nv; e += (int64_t)gridDim.x * 256) {
+    const int m = (int)(e / (N / 4));
+    const int n = (int)(e - (int64_t)m * (N / 4)) * 4;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < nsplit; ++k)
+      s += *reinterpret_cast<const f32x4*>(part + ((int64_t)k * M + m) * N + n);
+    *reinterpret_cast<u32x2*>(out + (int64_t)m * os + n) =
+        u32x2{(uint32_t)f32_to_bf16_rne(s.x) | ((uint32_t)f32_to_bf16_rne(s.y) << 16),
+              (uint32_t)f32_to_bf16_rne(s.z) | ((uint32_t)f32_to_bf16_rne(s.w) << 16)};
+  }
+}
+
+template <int MT, int VT, int KW>
+hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
+  constexpr int D = MT == 1 ? 4 : (MT == 2 ? 4 : 2);
+  const int rows_per_wg = (kGThreads / 64 / KW) * VT * 16;
+  const dim3 grid((unsigned)ceil_div(p.N, rows_per_wg), (unsigned)p.nsplit);
+  hipLaunchKernelGGL((skinny_gemm_kernel<MT, VT, D, KW>), grid, dim3(kGThreads), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int VT, int KW>
+hipError_t launch_m(const GemmParams& p, hipStream_t s) {
+  const int mt = (int)ceil_div(p.M, 16);
+  return mt == 1 ? launch_gemm<1, VT, KW>(p, s) : mt == 2 ? launch_gemm<2, VT, KW>(p, s)
+       : mt == 3 ? launch_gemm<3, VT, KW>(p, s) : launch_gemm<4, VT, KW>(p, s);
+}
+
+}  // namespace
+}  // namespace dflash
+
+using namespace dflash;
+
+extern "C" int dflash_gemm_bf16(const void* x, int64_t x_row_stride, const void* w,
+                                int64_t w_row_stride, void* out, int64_t out_row_stride, int M,
+                                int N, int K, int nsplit, int rows_per_wave, int k_waves,
+                                void* stream) {
+  if (M < 0 || M > 64 || N <= 0 || K <= 0 || K % kGKStep != 0 || nsplit < 1) return DFLASH_ERR_SHAPE;
+  if ((rows_per_wave != 16 && rows_per_wave != 32) || (k_waves != 1 && k_waves != 4))
+    return DFLASH_ERR_UNSUPPORTED;
+  if (M == 0) return DFLASH_OK;
+  if (x == nullptr || w == nullptr || out == nullptr) return DFLASH_ERR_NULL;
+  if (((uintptr_t)x & 15) || ((uintptr_t)w & 15) || (x_row_stride % 8) || (w_row_stride % 8) ||
+      x_row_stride < K || w_row_stride < K)
+    return DFLASH_ERR_ALIGN;
+  GemmParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.xs = x_row_stride;
+  p.w = static_cast<const uint16_t*>(w);
+  p.ws = w_row_stride;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  const int nks = K / kGKStep;
+  const int want = std::min(nsplit, nks);
+  p.ks_per_split = (int)ceil_div(nks, want);
+  p.nsplit = (int)ceil_div(nks, p.ks_per_split);  // no empty split
+  p.f32_out = nsplit > 1;  // as requested: the consumer reads fp32 partials
+  if (p.f32_out) {
+    if ((uintptr_t)out & 15) return DFLASH_ERR_ALIGN;
+    p.part = static_cast<float*>(out);
+  } else {
+    if (((uintptr_t)out & 7) || (out_row_stride % 4) || out_row_stride < N) return DFLASH_ERR_ALIGN;
+    p.out = static_cast<uint16_t*>(out);
+    p.os = out_row_stride;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (rows_per_wave == 16)
+    e = k_waves == 1 ? launch_m<1, 1>(p, s) : launch_m<1, 4>(p, s);
+  else
+    e = k_waves == 1 ? launch_m<2, 1>(p, s) : launch_m<2, 4>(p, s);
+  return to_status(e);
+}
+
+extern "C" int dflash_gemm_splits(int K, int nsplit) {
+  if (K <= 0 || K % kGKStep != 0 || nsplit < 1) return DFLASH_ERR_SHAPE;
+  const int nks = K / kGKStep;
+  nsplit = std::min(nsplit, nks);
+  const int per = (int)ceil_div(nks, nsplit);
+  return (int)ceil_div(nks, per);
+}
+
+extern "C" int dflash_splitk_reduce(const float* partials, int nsplit, int M, int N, void* out,
+                                    int64_t out_row_stride, void* stream) {
+  if (M < 0 || N <= 0 || N % 4 != 0 || nsplit < 1) return DFLASH_ERR_SHAPE;
+  if (M == 0) return DFLASH_OK;
+  if (partials == nullptr || out == nullptr) return DFLASH_ERR_NULL;
+  if (((uintptr_t)partials & 15) || ((uintptr_t)out & 7) || (out_row_stride % 4)) return DFLASH_ERR_ALIGN;
+  const int64_t nv = (int64_t)M * (N / 4);
+  const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(nv, 256), 1024);
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     partials, nsplit, M, N, static_cast<uint16_t*>(out), out_row_stride);
+  return to_status(hipGetLastError());
+}

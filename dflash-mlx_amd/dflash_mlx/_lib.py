@@ -48,6 +48,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP, _VP, _SZ, _VP],
     ),
     "dflash_add_rmsnorm": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, ctypes.c_float, _VP]),
+    "dflash_add_rmsnorm_splitk": (
+        _I, [_VP, _VP, _I, _VP, _VP, _VP, _I, _I, ctypes.c_float, _VP]),
+    "dflash_gemm_bf16": (_I, [_VP, _I64, _VP, _I64, _VP, _I64, _I, _I, _I, _I, _I, _I, _VP]),
+    "dflash_gemm_splits": (_I, [_I, _I]),
+    "dflash_splitk_reduce": (_I, [_VP, _I, _I, _I, _VP, _I64, _VP]),
     "dflash_swiglu": (_I, [_VP, _VP, _I, _I, _VP]),
     "dflash_attn_prep": (
         _I,

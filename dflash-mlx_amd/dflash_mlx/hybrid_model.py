@@ -13,8 +13,11 @@ KV caches (runtime.py:149-160; adapters.py:505-560).
 once:
 
 * GEMMs: the stacked projections of each layer (gated-delta in_proj
-  qkv|z|b|a, attention q|k|v, MLP gate|up, and the output projections) as
-  plain bf16 ``torch.mm`` on hipBLASLt;
+  qkv|z|b|a, attention q|k|v, MLP gate|up, and the output projections) on
+  this package's verify-sized GEMM (``dflash_gemm_bf16``: the weight
+  streamed once against the 16 block rows, split-K where N is small, the
+  partial sums folded into the next add + RMSNorm), or as plain bf16
+  ``torch.mm`` on hipBLASLt (``gemm="hipblaslt"``);
 * everything else on this package's gfx950 kernels through the C ABI:
   residual add + RMSNorm, the gated-delta prologue, the scan with the previous
   step's rollback fused into its state load (per-token tape), the gated
@@ -141,7 +144,13 @@ class HybridVerifyRunner:
     for B sequences of T block tokens, with caches of Smax positions."""
 
     def __init__(self, cfg: HybridConfig, weights: HybridWeights, B: int, T: int, Smax: int,
-                 device: torch.device):
+                 device: torch.device, gemm: str = "dflash"):
+        """gemm: "dflash" runs every projection on this package's verify-sized
+        GEMM (dflash_gemm_bf16, split-K partials summed by the consumer);
+        "hipblaslt" runs them as torch.mm (for comparison)."""
+        if gemm not in ("dflash", "hipblaslt"):
+            raise ValueError(f"gemm must be 'dflash' or 'hipblaslt', got {gemm!r}")
+        self.gemm = gemm
         if T > 16 or B * T > 64:
             raise ValueError("the verify step takes T <= 16 block tokens and B*T <= 64 rows")
         if Smax % 64:
@@ -191,10 +200,71 @@ class HybridVerifyRunner:
         self.bonus = e(B, dt=i32)
         V = cfg.vocab_size
         self.lm_ws = e(max(int(lib.dflash_lm_head_accept_workspace_bytes(B, T, V)), 8), dt=torch.uint8)
+        self._build_gemms()
         self._build_args()
         self.graph = None
 
     # ------------------------------------------------------------------ setup
+    # (requested splits, weight rows per wave, waves sharing a row group) per
+    # projection, from a sweep of cold-weight timings at M = 16 on MI355X:
+    # bf16 output where the next kernel needs it as bf16, fp32 split-K
+    # partials where the next add + RMSNorm sums them.
+    GEMM_PLAN = {"w_in": (1, 32, 4), "w_out": (8, 16, 4), "w_qkv": (1, 32, 4),
+                 "w_o": (8, 32, 4), "w_gu": (1, 32, 4), "w_down": (8, 32, 4)}
+
+    def _build_gemms(self):
+        """Argument tuples of every projection GEMM, and the split-K partial
+        buffer (fp32 [splits, M, N]) shared by the consumers in order."""
+        cfg, B, T = self.cfg, self.B, self.T
+        M, H, I = B * T, cfg.hidden_size, cfg.intermediate_size
+        lc = cfg.linear
+        dims = {"w_in": (cfg.in_proj_rows, H), "w_out": (H, lc.value_dim),
+                "w_qkv": (cfg.attn_proj_rows, H),
+                "w_o": (H, cfg.num_attention_heads * cfg.head_dim),
+                "w_gu": (2 * I, H), "w_down": (H, I)}
+        lib = _lib.load()
+        self.splits = {k: int(lib.dflash_gemm_splits(dims[k][1], plan[0])) if plan[0] > 1 else 0
+                       for k, plan in self.GEMM_PLAN.items()}
+        part_elems = max([self.splits[k] * M * dims[k][0] for k in dims] + [1])
+        self.part = torch.empty(part_elems, dtype=torch.float32, device=self.device)
+        pp = self.part.data_ptr()
+
+        def args(x, name, w, out_ptr, out_stride):
+            n, k = dims[name]
+            ns, rpw, kw = self.GEMM_PLAN[name]
+            return (x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out_ptr, out_stride, M, n,
+                    k, ns, rpw, kw)
+
+        def dst(name, bf16_out):
+            return (pp, 0) if self.splits[name] else (bf16_out.data_ptr(), bf16_out.stride(0))
+
+        self._gemm_args = []
+        gi = 0
+        for i in range(cfg.num_hidden_layers):
+            lw = self.w.layers[i]
+            a = {"gu": args(self.xn, "w_gu", lw["w_gu"], *dst("w_gu", self.gu)),
+                 "down": args(self.mlp_act, "w_down", lw["w_down"], *dst("w_down", self.r))}
+            if cfg.is_linear(i):
+                a["in"] = args(self.xn, "w_in", lw["w_in"], *dst("w_in", self.proj[gi]))
+                a["out"] = args(self.gnorm.view(M, -1), "w_out", lw["w_out"], *dst("w_out", self.r))
+                gi += 1
+            else:
+                a["qkv"] = args(self.xn, "w_qkv", lw["w_qkv"], *dst("w_qkv", self.aproj))
+                a["o"] = args(self.attn_out, "w_o", lw["w_o"], *dst("w_o", self.r))
+            self._gemm_args.append(a)
+
+    def _residual(self, name, w_norm, stream):
+        """h += the branch just produced by projection `name`; xn = norm(h)."""
+        cfg = self.cfg
+        M, H, eps = self.B * self.T, cfg.hidden_size, float(cfg.rms_norm_eps)
+        h, xn = self.h.data_ptr(), self.xn.data_ptr()
+        if self.splits[name]:
+            _lib.call("dflash_add_rmsnorm_splitk", h, self.part.data_ptr(), self.splits[name],
+                      w_norm.data_ptr(), h, xn, M, H, eps, stream)
+        else:
+            _lib.call("dflash_add_rmsnorm", h, self.r.data_ptr(), w_norm.data_ptr(), h, xn, M, H,
+                      eps, stream)
+
     def _build_args(self):
         cfg, lc, B, T = self.cfg, self.cfg.linear, self.B, self.T
         C, Hk, Hv = lc.conv_dim, lc.linear_num_key_heads, lc.linear_num_value_heads
@@ -281,6 +351,49 @@ class HybridVerifyRunner:
         """Embed self.tokens, run the 32 layers, the final norm and the fused
         LM-head greedy accept into posterior / matched / bonus.  The recurrent
         states are rolled back on load to the previous step's keep counts."""
+        if self.gemm == "hipblaslt":
+            return self._forward_accept_hipblaslt()
+        cfg, B, T = self.cfg, self.B, self.T
+        stream = _lib.stream_handle(self.device)
+        call = _lib.call
+        M, H, I = B * T, cfg.hidden_size, cfg.intermediate_size
+        eps = float(cfg.rms_norm_eps)
+        torch.index_select(self.w.embed, 0, self.tokens.view(-1), out=self.h)
+        call("dflash_add_rmsnorm", self.h.data_ptr(), None, self.w.layers[0]["ln_in"].data_ptr(),
+             self.h.data_ptr(), self.xn.data_ptr(), M, H, eps, stream)
+        gi = ai = 0
+        for i in range(cfg.num_hidden_layers):
+            lw = self.w.layers[i]
+            ga = self._gemm_args[i]
+            if i > 0:
+                self._residual("w_down", lw["ln_in"], stream)
+            if cfg.is_linear(i):
+                prologue, scan, gnorm = self._gdn_args[gi]
+                call("dflash_gemm_bf16", *ga["in"], stream)
+                call("dflash_gdn_prologue", *prologue, stream)
+                call("dflash_gdn_verify_scan_rollback", *scan, stream)
+                call("dflash_gdn_gated_rmsnorm", *gnorm, stream)
+                call("dflash_gemm_bf16", *ga["out"], stream)
+                self._residual("w_out", lw["ln_post"], stream)
+                gi += 1
+            else:
+                prep, attn = self._attn_args[ai]
+                call("dflash_gemm_bf16", *ga["qkv"], stream)
+                if self.splits["w_qkv"]:
+                    call("dflash_splitk_reduce", self.part.data_ptr(), self.splits["w_qkv"], M,
+                         cfg.attn_proj_rows, self.aproj.data_ptr(), cfg.attn_proj_rows, stream)
+                call("dflash_attn_prep", *prep, stream)
+                call("dflash_attn_verify", *attn, stream)
+                call("dflash_gemm_bf16", *ga["o"], stream)
+                self._residual("w_o", lw["ln_post"], stream)
+                ai += 1
+            call("dflash_gemm_bf16", *ga["gu"], stream)
+            call("dflash_swiglu", self.gu.data_ptr(), self.mlp_act.data_ptr(), M, I, stream)
+            call("dflash_gemm_bf16", *ga["down"], stream)
+        self._residual("w_down", self.w.final_norm, stream)
+        call("dflash_lm_head_greedy_accept", *self._lm_args, stream)
+
+    def _forward_accept_hipblaslt(self):
         cfg, B, T = self.cfg, self.B, self.T
         stream = _lib.stream_handle(self.device)
         call = _lib.call

@@ -334,6 +334,48 @@ int dflash_add_rmsnorm(const void* x, const void* r, const void* weight,
                        void* stream);
 
 /*
+ * dflash_add_rmsnorm with the branch given as the fp32 split-K partial sums
+ * of the projection that produced it (dflash_gemm_bf16 with nsplit > 1):
+ *   r = bf16(sum_s r_partials[s][m][:]),  h = bf16(x + r),  y as above.
+ * r_partials is fp32 [nsplit, M, H] contiguous, 16-byte aligned.
+ */
+int dflash_add_rmsnorm_splitk(const void* x, const float* r_partials,
+                              int nsplit, const void* weight, void* h_out,
+                              void* y, int M, int H, float eps, void* stream);
+
+/*
+ * Verify-sized projection GEMM: out[M, N] = x[M, K] . w[N, K]^T, bf16 in,
+ * fp32 accumulation, M <= 64 (the block rows of a verify step).  Every
+ * Linear of the target's layers at verify time (custom_qwen35_model.py:726-
+ * 736; mlx-lm Qwen3NextAttention / Qwen3NextMLP projections) has this shape:
+ * a stream of the weight against 16 rows, which library GEMMs tuned for
+ * large M serve at a fraction of HBM bandwidth.
+ * nsplit: split-K factor requested; dflash_gemm_splits(K, nsplit) is the
+ * number of splits actually used.  With nsplit == 1, out is bf16 [M, N] with
+ * row stride out_row_stride (elements; multiple of 4, 8-byte aligned).  With
+ * nsplit > 1, out is fp32 partial sums [dflash_gemm_splits(K, nsplit), M, N]
+ * (16-byte aligned) for dflash_add_rmsnorm_splitk or dflash_splitk_reduce.
+ * rows_per_wave (16 or 32) sets the weight rows a wavefront streams; k_waves
+ * (1 or 4) how many of a workgroup's 4 wavefronts share those rows, each
+ * streaming a quarter of the k-range (4: a workgroup covers rows_per_wave
+ * rows, merged through LDS; 1: it covers 4 * rows_per_wave rows).
+ * Supported: K % 64 == 0, row strides multiples of 8 elements, 16-byte
+ * aligned x and w.
+ */
+int dflash_gemm_bf16(const void* x, int64_t x_row_stride, const void* w,
+                     int64_t w_row_stride, void* out, int64_t out_row_stride,
+                     int M, int N, int K, int nsplit, int rows_per_wave,
+                     int k_waves, void* stream);
+int dflash_gemm_splits(int K, int nsplit);
+
+/*
+ * out[m, n] = bf16(sum_s partials[s, m, n]) for partials fp32 [nsplit, M, N]
+ * (N % 4 == 0), out bf16 with row stride out_row_stride.
+ */
+int dflash_splitk_reduce(const float* partials, int nsplit, int M, int N,
+                         void* out, int64_t out_row_stride, void* stream);
+
+/*
  * The MLP's gating (mlx-lm Qwen3NextMLP, called at
  * dflash_mlx/custom_qwen35_model.py:845): out = bf16(silu(gate) * up) with
  * gate_up bf16 [M, 2I] = [gate | up] (one GEMM of the stacked gate/up

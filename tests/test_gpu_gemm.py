@@ -1,0 +1,108 @@
+"""GPU parity of the verify-sized projection GEMM (dflash_gemm_bf16) and its
+split-K consumers against an fp32 torch reference of the same bf16 inputs.
+
+out = bf16(x . w^T): within one bf16 rounding of the fp32 reference
+(|err| <= 2^-8 |ref| + 1e-3 * rms(ref), fp32 accumulation in a different
+order); split-K partials summed in fp32: within 1e-4 of the reference's
+scale.  Shapes: every projection of the config-c4 step at M = 16, other M up
+to 64, N tails, both wave widths.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from dflash_mlx import _lib
+
+pytestmark = pytest.mark.gpu
+
+C4_SHAPES = [  # (N, K, nsplit): in_proj, out_proj, attn qkv, o_proj, gate|up, down
+    (12352, 2560, 1), (2560, 4096, 8), (5120, 2560, 4), (2560, 2048, 8), (18432, 2560, 1),
+    (2560, 9216, 8)]
+
+
+def _ref(x, w):
+    return x.float() @ w.float().t()
+
+
+def _run(device, M, N, K, nsplit, rpw, seed, kw=4):
+    g = torch.Generator(device=device).manual_seed(seed)
+    x = torch.randn(M, K, generator=g, device=device).bfloat16()
+    w = (0.02 * torch.randn(N, K, generator=g, device=device)).bfloat16()
+    lib = _lib.load()
+    used = int(lib.dflash_gemm_splits(K, nsplit))
+    if nsplit > 1:
+        out = torch.full((used, M, N), float("nan"), device=device)
+    else:
+        out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=device)
+    _lib.call("dflash_gemm_bf16", x.data_ptr(), K, w.data_ptr(), K, out.data_ptr(), N, M, N, K,
+              nsplit, rpw, kw, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    return x, w, out, used
+
+
+@pytest.mark.parametrize("kw", [1, 4])
+@pytest.mark.parametrize("N,K,nsplit", C4_SHAPES)
+def test_gemm_c4_shapes(device, N, K, nsplit, kw):
+    M = 16
+    print(f"[gemm] M={M} N={N} K={K} nsplit={nsplit} k_waves={kw}", flush=True)
+    x, w, out, used = _run(device, M, N, K, nsplit, 16 if kw == 1 else 32, seed=N + K, kw=kw)
+    ref = _ref(x, w)
+    scale = ref.pow(2).mean().sqrt().item()
+    if nsplit > 1:
+        assert used == min(nsplit, K // 64) or used <= nsplit
+        got = out.sum(0)
+        err = (got - ref).abs().max().item()
+        assert err <= 1e-4 * scale + 1e-5, err
+    else:
+        err = ((out.float() - ref).abs() - (2 ** -8) * ref.abs()).max().item()
+        assert err <= 1e-3 * scale, err
+
+
+@pytest.mark.parametrize("M,N,K,rpw,nsplit,kw", [
+    (1, 100, 64, 16, 1, 1), (37, 1000, 640, 32, 1, 1), (64, 777, 1024, 16, 3, 1),
+    (23, 300, 4096, 32, 5, 1), (16, 5120, 2560, 32, 4, 1), (1, 100, 64, 16, 1, 4),
+    (37, 1000, 640, 32, 1, 4), (64, 777, 1024, 16, 3, 4), (23, 300, 192, 32, 5, 4),
+    (16, 40, 128, 16, 1, 4)])
+def test_gemm_ragged(device, M, N, K, rpw, nsplit, kw):
+    x, w, out, used = _run(device, M, N, K, nsplit, rpw, seed=M * 7 + N, kw=kw)
+    ref = _ref(x, w)
+    scale = ref.pow(2).mean().sqrt().item()
+    got = out.sum(0) if nsplit > 1 else out.float()
+    tol = (1e-4 * scale + 1e-5) if nsplit > 1 else None
+    if nsplit > 1:
+        assert (got - ref).abs().max().item() <= tol
+        assert torch.isfinite(out).all()  # every used split's every element written
+    else:
+        assert ((got - ref).abs() - (2 ** -8) * ref.abs()).max().item() <= 1e-3 * scale
+
+
+def test_splitk_consumers(device):
+    """add+RMSNorm and the reduce read the same partials the GEMM wrote:
+    bf16(sum) then the residual add, as the unsplit path does."""
+    M, N, K, H = 16, 2560, 4096, 2560
+    x, w, part, used = _run(device, M, N, K, 8, 16, seed=5)
+    r_bf = torch.empty(M, N, dtype=torch.bfloat16, device=device)
+    _lib.call("dflash_splitk_reduce", part.data_ptr(), used, M, N, r_bf.data_ptr(), N,
+              _lib.stream_handle(device))
+    resid = torch.randn(M, H, device=device).bfloat16()
+    wn = torch.ones(H, dtype=torch.bfloat16, device=device)
+    h1, y1 = resid.clone(), torch.empty_like(resid)
+    h2, y2 = resid.clone(), torch.empty_like(resid)
+    _lib.call("dflash_add_rmsnorm_splitk", h1.data_ptr(), part.data_ptr(), used, wn.data_ptr(),
+              h1.data_ptr(), y1.data_ptr(), M, H, 1e-6, _lib.stream_handle(device))
+    _lib.call("dflash_add_rmsnorm", h2.data_ptr(), r_bf.data_ptr(), wn.data_ptr(), h2.data_ptr(),
+              y2.data_ptr(), M, H, 1e-6, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    assert torch.equal(r_bf, part.sum(0).bfloat16()) or \
+        (r_bf.float() - part.sum(0)).abs().max().item() <= 2 ** -7 * part.sum(0).abs().max().item()
+    assert torch.equal(h1, h2) and torch.equal(y1, y2)
+
+
+def test_gemm_rejects_bad_arguments(device):
+    lib = _lib.load()
+    assert lib.dflash_gemm_bf16(None, 64, None, 64, None, 8, 65, 8, 64, 1, 16, 1, None) == -2  # M>64
+    assert lib.dflash_gemm_bf16(None, 64, None, 64, None, 8, 16, 8, 100, 1, 16, 1, None) == -2  # K%64
+    assert lib.dflash_gemm_bf16(None, 64, None, 64, None, 8, 16, 8, 64, 1, 24, 1, None) == -3  # width
+    assert lib.dflash_gemm_bf16(None, 64, None, 64, None, 8, 16, 8, 64, 1, 16, 2, None) == -3  # k_waves
+    assert lib.dflash_gemm_splits(4096, 8) == 8 and lib.dflash_gemm_splits(128, 8) == 2
