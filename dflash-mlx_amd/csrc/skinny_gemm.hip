@@ -17,7 +17,10 @@
 //     holds elements 16g .. 16g+15 of the 64-wide step for both operands, so
 //     the contraction is exact whatever order the hardware gives the k-slots.
 //   - Epilogue, nsplit == 1 requested: bf16 (round to nearest even) into
-//     out.  nsplit > 1 requested: fp32 partial sums into
+//     out, or (dflash_gemm_bf16_swiglu) the MLP gating silu(gate) * up of a
+//     weight whose 32-row blocks are 16 gate rows then the 16 matching up
+//     rows: a wave's two row tiles are then the gate and up of the same
+//     output columns, and the gate|up product never leaves registers.  nsplit > 1 requested: fp32 partial sums into
 //     out_f32[split][M][N] for the splits actually used (see
 //     dflash_gemm_splits); the consumer sums them (dflash_add_rmsnorm_splitk,
 //     dflash_splitk_reduce).
@@ -49,6 +52,7 @@ struct GemmParams {
   int64_t os;  // output row stride (elements)
   float* part;  // [nsplit][M][N] when f32_out
   int M, N, K, nsplit, ks_per_split, f32_out;
+  int swiglu;  // bf16 epilogue silu(tile 0) * tile 1 into column block N/2 (VT == 2)
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -172,6 +176,18 @@ __global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams
       const int n = nwave + vt * 16 + 4 * g;
       if (n >= p.N) continue;
       const f32x4 v = acc[vt][mt];
+      if (VT == 2 && p.swiglu) {  // rows nwave.. are gate, nwave+16.. the matching up rows
+        if (vt == 1) continue;
+        const f32x4 u = acc[1][mt];
+        const int j = (nwave >> 1) + 4 * g;  // output column
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = v[i] / (1.f + __expf(-v[i])) * u[i];
+        *reinterpret_cast<u32x2*>(p.out + (int64_t)m * p.os + j) =
+            u32x2{(uint32_t)f32_to_bf16_rne(o[0]) | ((uint32_t)f32_to_bf16_rne(o[1]) << 16),
+                  (uint32_t)f32_to_bf16_rne(o[2]) | ((uint32_t)f32_to_bf16_rne(o[3]) << 16)};
+        continue;
+      }
       if (p.f32_out) {
         float* dst = p.part + ((int64_t)split * p.M + m) * p.N + n;
         if (n + 4 <= p.N && (p.N & 3) == 0) {  // rows 16-byte aligned only when N % 4 == 0
@@ -270,6 +286,35 @@ extern "C" int dflash_gemm_bf16(const void* x, int64_t x_row_stride, const void*
   else
     e = k_waves == 1 ? launch_m<2, 1>(p, s) : launch_m<2, 4>(p, s);
   return to_status(e);
+}
+
+extern "C" int dflash_gemm_bf16_swiglu(const void* x, int64_t x_row_stride, const void* w_pairs,
+                                       int64_t w_row_stride, void* out, int64_t out_row_stride,
+                                       int M, int N, int K, int k_waves, void* stream) {
+  if (M < 0 || M > 64 || N <= 0 || N % 32 != 0 || K <= 0 || K % kGKStep != 0)
+    return DFLASH_ERR_SHAPE;
+  if (k_waves != 1 && k_waves != 4) return DFLASH_ERR_UNSUPPORTED;
+  if (M == 0) return DFLASH_OK;
+  if (x == nullptr || w_pairs == nullptr || out == nullptr) return DFLASH_ERR_NULL;
+  if (((uintptr_t)x & 15) || ((uintptr_t)w_pairs & 15) || (x_row_stride % 8) ||
+      (w_row_stride % 8) || x_row_stride < K || w_row_stride < K || ((uintptr_t)out & 7) ||
+      (out_row_stride % 4) || out_row_stride < N / 2)
+    return DFLASH_ERR_ALIGN;
+  GemmParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.xs = x_row_stride;
+  p.w = static_cast<const uint16_t*>(w_pairs);
+  p.ws = w_row_stride;
+  p.out = static_cast<uint16_t*>(out);
+  p.os = out_row_stride;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.ks_per_split = K / kGKStep;
+  p.nsplit = 1;
+  p.swiglu = 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return to_status(k_waves == 1 ? launch_m<2, 1>(p, s) : launch_m<2, 4>(p, s));
 }
 
 extern "C" int dflash_gemm_splits(int K, int nsplit) {

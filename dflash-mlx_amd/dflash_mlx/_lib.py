@@ -52,6 +52,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I, [_VP, _VP, _I, _VP, _VP, _VP, _I, _I, ctypes.c_float, _VP]),
     "dflash_gemm_bf16": (_I, [_VP, _I64, _VP, _I64, _VP, _I64, _I, _I, _I, _I, _I, _I, _VP]),
     "dflash_gemm_splits": (_I, [_I, _I]),
+    "dflash_gemm_bf16_swiglu": (_I, [_VP, _I64, _VP, _I64, _VP, _I64, _I, _I, _I, _I, _VP]),
     "dflash_splitk_reduce": (_I, [_VP, _I, _I, _I, _VP, _I64, _VP]),
     "dflash_swiglu": (_I, [_VP, _VP, _I, _I, _VP]),
     "dflash_attn_prep": (

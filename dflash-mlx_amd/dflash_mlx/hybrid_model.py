@@ -16,7 +16,8 @@ once:
   qkv|z|b|a, attention q|k|v, MLP gate|up, and the output projections) on
   this package's verify-sized GEMM (``dflash_gemm_bf16``: the weight
   streamed once against the 16 block rows, split-K where N is small, the
-  partial sums folded into the next add + RMSNorm), or as plain bf16
+  partial sums folded into the next add + RMSNorm, the MLP gating fused into
+  the gate|up projection), or as plain bf16
   ``torch.mm`` on hipBLASLt (``gemm="hipblaslt"``);
 * everything else on this package's gfx950 kernels through the C ABI:
   residual add + RMSNorm, the gated-delta prologue, the scan with the previous
@@ -235,6 +236,16 @@ class HybridVerifyRunner:
             return (x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out_ptr, out_stride, M, n,
                     k, ns, rpw, kw)
 
+        def gate_up_pairs(lw):
+            """w_gu [gate; up] rows regrouped into 32-row blocks (16 gate rows,
+            then the 16 up rows of the same columns) for the fused-SwiGLU GEMM;
+            made once per weight set."""
+            if "w_gu_pairs" not in lw:
+                w = lw["w_gu"]
+                lw["w_gu_pairs"] = w.view(2, I // 16, 16, H).transpose(0, 1).reshape(2 * I, H) \
+                    .contiguous()
+            return lw["w_gu_pairs"]
+
         def dst(name, bf16_out):
             return (pp, 0) if self.splits[name] else (bf16_out.data_ptr(), bf16_out.stride(0))
 
@@ -242,7 +253,9 @@ class HybridVerifyRunner:
         gi = 0
         for i in range(cfg.num_hidden_layers):
             lw = self.w.layers[i]
-            a = {"gu": args(self.xn, "w_gu", lw["w_gu"], *dst("w_gu", self.gu)),
+            wp = gate_up_pairs(lw)
+            a = {"gu": (self.xn.data_ptr(), H, wp.data_ptr(), H, self.mlp_act.data_ptr(), I, M, 2 * I,
+                        H, self.GEMM_PLAN["w_gu"][2]),
                  "down": args(self.mlp_act, "w_down", lw["w_down"], *dst("w_down", self.r))}
             if cfg.is_linear(i):
                 a["in"] = args(self.xn, "w_in", lw["w_in"], *dst("w_in", self.proj[gi]))
@@ -387,8 +400,7 @@ class HybridVerifyRunner:
                 call("dflash_gemm_bf16", *ga["o"], stream)
                 self._residual("w_o", lw["ln_post"], stream)
                 ai += 1
-            call("dflash_gemm_bf16", *ga["gu"], stream)
-            call("dflash_swiglu", self.gu.data_ptr(), self.mlp_act.data_ptr(), M, I, stream)
+            call("dflash_gemm_bf16_swiglu", *ga["gu"], stream)
             call("dflash_gemm_bf16", *ga["down"], stream)
         self._residual("w_down", self.w.final_norm, stream)
         call("dflash_lm_head_greedy_accept", *self._lm_args, stream)

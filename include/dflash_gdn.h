@@ -369,6 +369,19 @@ int dflash_gemm_bf16(const void* x, int64_t x_row_stride, const void* w,
 int dflash_gemm_splits(int K, int nsplit);
 
 /*
+ * The MLP's gate/up projection with its gating fused (Qwen3NextMLP,
+ * custom_qwen35_model.py:845: down(silu(gate(x)) * up(x)) up to the down
+ * projection): out[M, N/2] = bf16(silu(x . G^T) * (x . U^T)) where w_pairs
+ * [N, K] holds 32-row blocks of 16 gate rows followed by the 16 up rows of the
+ * same output columns (block j: gate rows 16j .. 16j+15, then up rows 16j ..
+ * 16j+15).  Supported: N % 32 == 0, K % 64 == 0; k_waves as above.
+ */
+int dflash_gemm_bf16_swiglu(const void* x, int64_t x_row_stride,
+                            const void* w_pairs, int64_t w_row_stride,
+                            void* out, int64_t out_row_stride, int M, int N,
+                            int K, int k_waves, void* stream);
+
+/*
  * out[m, n] = bf16(sum_s partials[s, m, n]) for partials fp32 [nsplit, M, N]
  * (N % 4 == 0), out bf16 with row stride out_row_stride.
  */

@@ -214,8 +214,7 @@ def model_step(cfg, weights, state, tokens, eps=1e-6):
             ai += 1
         h, x = add_rmsnorm(h, r, lw["ln_post"], eps)
         x = bf16(x)
-        gu = bf16(x @ lw["w_gu"].T)
-        act = bf16(swiglu(gu))
+        act = bf16(swiglu(x @ lw["w_gu"].T))  # gating fused into the gate|up GEMM: one rounding
         r = bf16(act @ lw["w_down"].T)
     h, x = add_rmsnorm(h, r, weights["final_norm"], eps)
     x = bf16(x)

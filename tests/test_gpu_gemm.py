@@ -106,3 +106,23 @@ def test_gemm_rejects_bad_arguments(device):
     assert lib.dflash_gemm_bf16(None, 64, None, 64, None, 8, 16, 8, 64, 1, 24, 1, None) == -3  # width
     assert lib.dflash_gemm_bf16(None, 64, None, 64, None, 8, 16, 8, 64, 1, 16, 2, None) == -3  # k_waves
     assert lib.dflash_gemm_splits(4096, 8) == 8 and lib.dflash_gemm_splits(128, 8) == 2
+
+
+@pytest.mark.parametrize("M,I,K,kw", [(16, 9216, 2560, 4), (16, 9216, 2560, 1), (37, 64, 128, 4)])
+def test_gemm_swiglu_fused(device, M, I, K, kw):
+    """Paired gate/up weight: out = bf16(silu(x G^T) * (x U^T)) within two
+    bf16 ulps of the fp32 reference (silu of an fp32 product, one rounding)."""
+    g = torch.Generator(device=device).manual_seed(I + M)
+    x = torch.randn(M, K, generator=g, device=device).bfloat16()
+    w = (0.05 * torch.randn(2 * I, K, generator=g, device=device)).bfloat16()  # [gate; up]
+    pairs = w.view(2, I // 16, 16, K).transpose(0, 1).reshape(2 * I, K).contiguous()
+    out = torch.full((M, I), float("nan"), dtype=torch.bfloat16, device=device)
+    _lib.call("dflash_gemm_bf16_swiglu", x.data_ptr(), K, pairs.data_ptr(), K, out.data_ptr(), I, M,
+              2 * I, K, kw, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    gu = x.float() @ w.float().t()
+    ref = torch.nn.functional.silu(gu[:, :I]) * gu[:, I:]
+    scale = ref.pow(2).mean().sqrt().item()
+    err = ((out.float() - ref).abs() - 2 ** -7 * ref.abs()).max().item()
+    print(f"[gemm swiglu] M={M} I={I} K={K} kw={kw}: excess {err:.3e} (rms {scale:.3e})", flush=True)
+    assert err <= 1e-3 * scale
