@@ -17,7 +17,7 @@
 //     workgroup covers 16*R consecutive-by-stride rows of one (b, hv) head.
 //   - The tape dominates the bytes (T state copies per head), so it is
 //     written with non-temporal dwordx4 stores as soon as each token is done.
-//   - The inputs of token t+1 are loaded before token t is computed.
+//   - The inputs of tokens t+1 .. t+4 are in flight while token t is computed.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -124,7 +124,11 @@ __device__ __forceinline__ void store_f32_stream(float* p, const float* f) {
   }
 }
 
-template <int DK, int R>
+// PF: tokens of inputs in flight (register ring).  1 for launches that fill
+// the chip with workgroups; 4 when there are at most as many work items as
+// CUs (one layer of one sequence), where each step otherwise waits on its
+// own loads.
+template <int DK, int R, int PF>
 __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
   constexpr int VEC = (DK % 64 == 0) ? 4 : 2;
   constexpr int NCH = DK / (16 * VEC);
@@ -190,84 +194,94 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
     const float* bp = p.beta + b * p.b_sb + hv;
     float* tp = has_tape ? p.tape + head_base + sub * VEC : nullptr;
 
-    // Prefetch registers for the next token.
-    typename LD::raw k_raw[NCH], q_raw[NCH];
-    uint16_t v_raw[R];
-    float g_nx = 0.f, b_nx = 0.f;
-    auto fetch = [&](int t) {
+    // Inputs of the next PF tokens stay in flight in a register ring (slot
+    // t % PF holds token t).
+    typename LD::raw k_raw[PF][NCH], q_raw[PF][NCH];
+    uint16_t v_raw[PF][R];
+    float g_r[PF], b_r[PF];
+    auto fetch = [&](int slot, int t) {
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) k_raw[c] = LD::load(kp + t * p.k_st + c * 16 * VEC);
+      for (int c = 0; c < NCH; ++c) k_raw[slot][c] = LD::load(kp + t * p.k_st + c * 16 * VEC);
       if (has_q) {
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) q_raw[c] = LD::load(qp + t * p.q_st + c * 16 * VEC);
+        for (int c = 0; c < NCH; ++c) q_raw[slot][c] = LD::load(qp + t * p.q_st + c * 16 * VEC);
       }
 #pragma unroll
-      for (int r = 0; r < R; ++r) v_raw[r] = vp[t * p.v_st + row[r]];
-      g_nx = gp[t * p.g_st];
-      b_nx = bp[t * p.b_st];
+      for (int r = 0; r < R; ++r) v_raw[slot][r] = vp[t * p.v_st + row[r]];
+      g_r[slot] = gp[t * p.g_st];
+      b_r[slot] = bp[t * p.b_st];
     };
-    if (n > 0) fetch(0);
+    if (n > 0) {
+#pragma unroll
+      for (int d = 0; d < PF; ++d) fetch(d, min(d, n - 1));
+    }
 
     float okeep[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) okeep[r] = 0.f;
 
-    for (int t = 0; t < n; ++t) {
-      float kf[NCH][VEC], qf[NCH][VEC], vr[R];
+    for (int t0 = 0; t0 < n; t0 += PF) {
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) LD::unpack(k_raw[c], kf[c]);
-      if (has_q) {
+      for (int d = 0; d < PF; ++d) {
+        const int t = t0 + d;
+        if (t < n) {
+          float kf[NCH][VEC], qf[NCH][VEC], vr[R];
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) LD::unpack(q_raw[c], qf[c]);
-      }
+          for (int c = 0; c < NCH; ++c) LD::unpack(k_raw[d][c], kf[c]);
+          if (has_q) {
 #pragma unroll
-      for (int r = 0; r < R; ++r) vr[r] = bf16_bits_to_f32(v_raw[r]);
-      const float gt = g_nx;
-      const float bt = b_nx;
-      fetch(min(t + 1, n - 1));
-
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        // S <- g*S ; kv = S.k
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < NCH; ++c)
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) {
-            S[r][c][e] *= gt;
-            acc = fmaf(S[r][c][e], kf[c][e], acc);
+            for (int c = 0; c < NCH; ++c) LD::unpack(q_raw[d][c], qf[c]);
           }
-        const float kv = row16_sum(acc);
-        const float d = (vr[r] - kv) * bt;
-        // S += k (x) d
 #pragma unroll
-        for (int c = 0; c < NCH; ++c)
-#pragma unroll
-          for (int e = 0; e < VEC; ++e) S[r][c][e] = fmaf(kf[c][e], d, S[r][c][e]);
-        if (has_q) {
-          float o = 0.f;
-#pragma unroll
-          for (int c = 0; c < NCH; ++c)
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) o = fmaf(S[r][c][e], qf[c][e], o);
-          o = row16_sum(o);
-          if (sub == (t & 15)) okeep[r] = o;
-        }
-        if (has_tape) {
-          float* dst = tp + (int64_t)t * p.tape_tstride + (int64_t)row[r] * DK;
-#pragma unroll
-          for (int c = 0; c < NCH; ++c) store_f32_stream<VEC>(dst + c * 16 * VEC, S[r][c]);
-        }
-      }
+          for (int r = 0; r < R; ++r) vr[r] = bf16_bits_to_f32(v_raw[d][r]);
+          const float gt = g_r[d];
+          const float bt = b_r[d];
+          fetch(d, min(t + PF, n - 1));
 
-      // Lane s of each row group holds out for token (t & ~15) + s; flush
-      // every 16 tokens and at the end.
-      if (has_q && (((t & 15) == 15) || (t == n - 1))) {
-        const int t0 = t & ~15;
-        if (sub <= (t & 15)) {
-          uint16_t* op = p.out + (((int64_t)b * p.T + t0 + sub) * p.Hv + hv) * p.Dv;
 #pragma unroll
-          for (int r = 0; r < R; ++r) op[row[r]] = f32_to_bf16_rne(okeep[r]);
+          for (int r = 0; r < R; ++r) {
+            // S <- g*S ; kv = S.k
+            float acc = 0.f;
+#pragma unroll
+            for (int c = 0; c < NCH; ++c)
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) {
+                S[r][c][e] *= gt;
+                acc = fmaf(S[r][c][e], kf[c][e], acc);
+              }
+            const float kv = row16_sum(acc);
+            const float delta = (vr[r] - kv) * bt;
+            // S += k (x) delta
+#pragma unroll
+            for (int c = 0; c < NCH; ++c)
+#pragma unroll
+              for (int e = 0; e < VEC; ++e) S[r][c][e] = fmaf(kf[c][e], delta, S[r][c][e]);
+            if (has_q) {
+              float o = 0.f;
+#pragma unroll
+              for (int c = 0; c < NCH; ++c)
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) o = fmaf(S[r][c][e], qf[c][e], o);
+              o = row16_sum(o);
+              if (sub == (t & 15)) okeep[r] = o;
+            }
+            if (has_tape) {
+              float* dst = tp + (int64_t)t * p.tape_tstride + (int64_t)row[r] * DK;
+#pragma unroll
+              for (int c = 0; c < NCH; ++c) store_f32_stream<VEC>(dst + c * 16 * VEC, S[r][c]);
+            }
+          }
+
+          // Lane s of each row group holds out for token (t & ~15) + s; flush
+          // every 16 tokens and at the end.
+          if (has_q && (((t & 15) == 15) || (t == n - 1))) {
+            const int tb = t & ~15;
+            if (sub <= (t & 15)) {
+              uint16_t* op = p.out + (((int64_t)b * p.T + tb + sub) * p.Hv + hv) * p.Dv;
+#pragma unroll
+              for (int r = 0; r < R; ++r) op[row[r]] = f32_to_bf16_rne(okeep[r]);
+            }
+          }
         }
       }
     }
@@ -285,6 +299,7 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
 }
 
 int scan_grid(int items);
+int scan_cus();
 
 template <int DK>
 hipError_t launch_dk(const ScanParams& base, int R, int grid, int xcd, hipStream_t s) {
@@ -296,10 +311,14 @@ hipError_t launch_dk(const ScanParams& base, int R, int grid, int xcd, hipStream
   // xcd < 0: XCD-aware walk whenever the shapes allow it; 0: off; > 0: on if allowed.
   const bool xcd_ok = blocks % 8 == 0 && p.items % 8 == 0 && blocks < p.items;
   p.xcd_items = (xcd != 0 && xcd_ok) ? p.items / 8 : 0;
-  switch (R) {
-    case 1: hipLaunchKernelGGL((gdn_scan_kernel<DK, 1>), dim3(blocks), dim3(256), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((gdn_scan_kernel<DK, 2>), dim3(blocks), dim3(256), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((gdn_scan_kernel<DK, 4>), dim3(blocks), dim3(256), 0, s, p); break;
+  const bool deep = p.items <= scan_cus();
+  switch (R * (deep ? 10 : 1)) {
+    case 1: hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 1>), dim3(blocks), dim3(256), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((gdn_scan_kernel<DK, 2, 1>), dim3(blocks), dim3(256), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((gdn_scan_kernel<DK, 4, 1>), dim3(blocks), dim3(256), 0, s, p); break;
+    case 10: hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 4>), dim3(blocks), dim3(256), 0, s, p); break;
+    case 20: hipLaunchKernelGGL((gdn_scan_kernel<DK, 2, 4>), dim3(blocks), dim3(256), 0, s, p); break;
+    case 40: hipLaunchKernelGGL((gdn_scan_kernel<DK, 4, 4>), dim3(blocks), dim3(256), 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -316,17 +335,24 @@ int pick_rows(int Dv) {
 // Workgroups launched: at most 3 per CU, each walking several (head, row
 // block) items.  On MI355X this beat one workgroup per item by ~12 % on the
 // tape-write-bound verify shapes (fewer concurrent write streams).
-int scan_grid(int items) {
+// CUs of the current device (cached per device; 0 if unknown).
+int scan_cus() {
   static int cus[64] = {0};
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return items;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
   if (cus[dev] == 0) {
     int n = 0;
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      return items;
+      return 0;
     cus[dev] = n;
   }
-  const int cap = 3 * cus[dev];
+  return cus[dev];
+}
+
+int scan_grid(int items) {
+  const int cus = scan_cus();
+  if (cus == 0) return items;
+  const int cap = 3 * cus;
   return items < cap ? items : cap;
 }
 
