@@ -16,13 +16,14 @@
 // fp32, then W^T = K^T (T diag(beta gamma))^T and U~ = (T diag(beta)) V on
 // bf16 MFMA with T split into hi + lo bf16 halves.  Everything phase 2 reads
 // is written pre-arranged in the operand order of its MFMAs.
-// Phase 2 (chunk_state_kernel, sequential over chunks, parallel over (head,
+// Phase 2 (chunk_state_kernel, sequential over chunks, one wave per (head,
 // 16 state rows)): the state stays in registers in fp32; every product with
 // an fp32 operand splits it into hi + lo bf16 halves (x = hi + lo to about
 // 2^-16 relative) and accumulates hi*hi + hi*lo + lo*hi in fp32, so the state
 // keeps fp32-level accuracy over all chunks while running on the bf16 matrix
-// cores.  The next chunk's operands are prefetched into registers, and the two
-// barriers per chunk wait on LDS traffic only, not on those loads.
+// cores.  The wave owns all 128 columns of its 16 state rows, so the chunk
+// loop needs no LDS and no barrier: every intermediate comes out of one MFMA
+// in the register layout the next MFMA reads.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -40,19 +41,27 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int CH = 64;   // chunk length
 constexpr int D = 128;   // Dk = Dv supported by these kernels
-constexpr int RB = 16;   // state rows per phase-2 workgroup
+constexpr int RB = 16;   // state rows per phase-2 wave
 constexpr int KTP = 72;  // bf16 row pitch of the K^T / V^T tiles in LDS
 constexpr int TPF = 68;  // fp32 row pitch of A / T in LDS
 
-// Workspace of one (head, chunk), in bytes.  Layouts:
-//   W_HI / W_LO: bf16 [64 i][4 s][4 g][8]: slot t*4+e holds W[i][32s+16t+4g+e]
-//   KT:          bf16 [128 dk][64 j]        (K transposed)
-//   P_HI / P_LO: bf16 [64 i][64 j]          (row-major)
-//   UT:          fp32 [8 rb][4 w][64 lane][4]: U~[16w + 4(lane/16) + e][16rb + lane%16]
+// Workspace of one (head, chunk), in bytes.  Every matrix is stored as the
+// MFMA operand fragments phase 2 loads: fragment f is 64 lanes x 16 bytes,
+// lane l = r + 16g holding row r of the fragment's 16-row tile and, in slot
+// t*4+e, column 32s + 16t + 4g + e of k-step s.  That slot order is also the
+// order in which a pair of 16x16 result tiles holds its rows, so results feed
+// the next product without a shuffle; and each fragment is one 1 KB load of
+// eight whole cache lines.
+//   W_HI / W_LO: bf16 fragments [4 it][4 s]: W[16it + r][32s+16t+4g+e]
+//   Q:           bf16 fragments [4 it][4 s]: Q[16it + r][32s+16t+4g+e] (padded rows zero)
+//   KT:          bf16 fragments [8 dt][2 s]: K[32s+16t+4g+e][16dt + r]
+//   P_HI / P_LO: bf16 fragments [4 it][2 s]: P[16it + r][32s+16t+4g+e]
+//   UT:          fp32 [8 rb][4 it][64 lane][4]: U~[16it + 4(lane/16) + e][16rb + lane%16]
 //   EG:          fp32 [64] exp(G_i);  ED: fp32 [64] exp(G_63 - G_i)  (decays)
 constexpr size_t kWHi = 0;
 constexpr size_t kWLo = kWHi + CH * D * 2;
-constexpr size_t kKT = kWLo + CH * D * 2;
+constexpr size_t kQ = kWLo + CH * D * 2;
+constexpr size_t kKT = kQ + CH * D * 2;
 constexpr size_t kPHi = kKT + D * CH * 2;
 constexpr size_t kPLo = kPHi + CH * CH * 2;
 constexpr size_t kUT = kPLo + CH * CH * 2;
@@ -106,12 +115,6 @@ __device__ __forceinline__ void split4(f32x4 x, u32x2& hi, u32x2& lo) {
   lo = u32x2{pack_lo(x.x, x.y), pack_lo(x.z, x.w)};
 }
 
-// Workgroup barrier that waits for this wave's LDS traffic only: global loads
-// in flight (the next chunk's prefetch) stay in flight across it.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 __device__ __forceinline__ const uint16_t* krow(const ChunkParams& p, int b, int hk, int t) {
   return p.k + b * p.k_sb + (int64_t)t * p.k_st + hk * p.k_sh;
 }
@@ -124,6 +127,14 @@ __device__ __forceinline__ const uint16_t* vrow(const ChunkParams& p, int b, int
 
 __device__ __forceinline__ u32x4 ld16(const void* ptr) { return *reinterpret_cast<const u32x4*>(ptr); }
 __device__ __forceinline__ u32x2 ld8(const void* ptr) { return *reinterpret_cast<const u32x2*>(ptr); }
+__device__ __forceinline__ f32x4 ldf4(const void* ptr) { return *reinterpret_cast<const f32x4*>(ptr); }
+
+// bf16 element index of (row i, column j) of a [64][64] matrix stored as
+// fragments [4 it][2 s] (column j = 32s + 16t + 4g + e, row i = 16it + r).
+__device__ __forceinline__ int frag64(int i, int j) {
+  return (((i >> 4) * 2 + (j >> 5)) * 64 + (i & 15) + 16 * ((j >> 2) & 3)) * 8 + ((j >> 4) & 1) * 4 +
+         (j & 3);
+}
 
 // ------------------------------------------------------------------ phase 1
 // grid (NC, B*Hv), 256 threads.
@@ -246,18 +257,32 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
         sA[i][j] = (j < i) ? sBeta[i] * dec * vkk[e] : 0.f;
         const float pv = (j <= i) ? dec * vqk[e] : 0.f;
         const uint32_t hb = __float_as_uint(pv) & 0xFFFF0000u;
-        phi[i * CH + j] = (uint16_t)(hb >> 16);
-        plo[i * CH + j] = f32_to_bf16_rne(pv - __uint_as_float(hb));
+        phi[frag64(i, j)] = (uint16_t)(hb >> 16);
+        plo[frag64(i, j)] = f32_to_bf16_rne(pv - __uint_as_float(hb));
       }
     }
   }
-  // K^T to the workspace (rows of 64 tokens, 16-byte pieces).
+  // K^T fragments [8 dt][2 s]: 16 bytes per (dk, s, g).
   {
     uint16_t* kt = reinterpret_cast<uint16_t*>(ws + kKT);
-    for (int e = tid; e < D * (CH / 8); e += 256) {
-      const int dk = e >> 3, piece = e & 7;
-      *reinterpret_cast<u32x4*>(kt + dk * CH + piece * 8) =
-          *reinterpret_cast<const u32x4*>(&sKT[dk][piece * 8]);
+    for (int e = tid; e < D * 8; e += 256) {
+      const int dk = e >> 3, s = (e >> 2) & 1, g = e & 3;
+      const u32x2 a = *reinterpret_cast<const u32x2*>(&sKT[dk][32 * s + 4 * g]);
+      const u32x2 z = *reinterpret_cast<const u32x2*>(&sKT[dk][32 * s + 16 + 4 * g]);
+      *reinterpret_cast<u32x4*>(kt + (((dk >> 4) * 2 + s) * 64 + (dk & 15) + 16 * g) * 8) =
+          u32x4{a.x, a.y, z.x, z.y};
+    }
+  }
+  // Q fragments [4 it][4 s] (padded rows zero): 16 bytes per (i, s, g).
+  {
+    uint16_t* qw = reinterpret_cast<uint16_t*>(ws + kQ);
+    for (int e = tid; e < CH * 16; e += 256) {
+      const int i = e >> 4, s = (e >> 2) & 3, g = e & 3;
+      const bool valid = i < n;
+      const uint16_t* qr = qrow(p, b, hk, t0 + (valid ? i : n - 1)) + 32 * s + 4 * g;
+      const u32x2 a = ld8(qr), z = ld8(qr + 16);
+      *reinterpret_cast<u32x4*>(qw + (((i >> 4) * 4 + s) * 64 + (i & 15) + 16 * g) * 8) =
+          valid ? u32x4{a.x, a.y, z.x, z.y} : u32x4{0u, 0u, 0u, 0u};
     }
   }
   __syncthreads();
@@ -357,7 +382,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
         // aw: lane holds W[i][dk], dk = 16 tile + 4 g4 + e -> s = tile/2, t = tile%2.
         u32x2 hi, lo;
         split4(aw[x], hi, lo);
-        const int off = i * D + (tile >> 1) * 32 + g4 * 8 + (tile & 1) * 4;
+        const int off = ((it * 4 + (tile >> 1)) * 64 + lane) * 8 + (tile & 1) * 4;
         *reinterpret_cast<u32x2*>(whi + off) = hi;
         *reinterpret_cast<u32x2*>(wlo + off) = lo;
         // au: lane holds U~[16 it + 4 g4 + e][16 tile + r16] -> UT[tile][it][lane].
@@ -368,212 +393,256 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
 }
 
 // ------------------------------------------------------------------ phase 2
-// Per-wave operands of one chunk (wave w owns token rows 16w .. 16w+15 for the
-// W / Q / P products and state columns 32w .. 32w+31 for the state update).
-struct ChunkOps {
-  u32x4 whi[4], wlo[4];  // W rows, k-steps s = 0..3
-  u32x2 q[8];            // Q rows: [2s + t] = dk 32s + 16t + 4g .. +3
-  u32x4 phi[2], plo[2];  // P rows, j-steps 0..1
-  u32x4 kt[4];           // K^T rows 32w + 16t + r16, j-step s: [2t + s]
-  f32x4 ut;              // U~ for this lane's 4 token rows
-  f32x4 eg;              // exp(G) of this lane's 4 token rows
-  f32x4 ed;              // exp(G_end - G) of the same rows
-  float egC;             // exp(G_end)
+// A workgroup of two waves owns state rows r = 16rb + (lane % 16) of one head.
+// The state wave keeps all 128 columns of those rows in fp32 as the 8 result
+// tiles of the state update S^T[dk][r] (tile dt: lane holds columns
+// 16dt + 4g + e, g = lane / 16).  Read pairwise, tiles 2s and 2s+1 are
+// exactly the B operand of k-step s of the products with S (slot t*4+e =
+// column 32s+16t+4g+e), and the U tiles of the W product are the B operand
+// of P U and of the state update in the same way, so the state chain
+//   U = U~ - W S^T,  S^T <- gamma_C S^T + K^T diag(ED) U
+// is MFMAs and register arithmetic only.  It hands S and U (as bf16 hi / lo
+// operand halves) to the output wave through LDS, double-buffered, with one
+// barrier per chunk; the output wave computes O = diag(EG) Q S^T + P U one
+// chunk behind, off the chain.
+
+struct WOps {                // state wave, per chunk
+  u32x4 hi[4][4], lo[4][4];  // W rows, [token tile it][k-step s]
+  f32x4 ut[4];               // U~[16it + 4g + e][16rb + lane%16]
+  f32x4 ed[4];               // exp(G_63 - G) of the same token rows
+  float egC;                 // exp(G_63)
+};
+struct QOps {                // output wave, per chunk
+  u32x4 q[4][4];             // Q rows, [it][s]
+  u32x4 ph[4][2], pl[4][2];  // P rows, [it][s] (tiles 0, 1: k-step 0 only)
+  f32x4 eg[4];               // exp(G) of the lane's token rows
+};
+struct Exchange {            // one chunk's S and U operand halves, [k-step][lane]
+  u32x4 shi[4][64], slo[4][64];
+  u32x4 uh[2][64], ul[2][64];
 };
 
-__device__ __forceinline__ void load_ops(const ChunkParams& p, int bh, int b, int hk, int c, int rb,
-                                         int wave, int lane, ChunkOps& o) {
-  const int r16 = lane & 15, g4 = lane >> 4;
-  const uint8_t* ws = p.ws + ((int64_t)bh * p.NC + c) * kWsChunk;
-  const int i = wave * 16 + r16;
-  const uint16_t* whi = reinterpret_cast<const uint16_t*>(ws + kWHi) + i * D + g4 * 8;
-  const uint16_t* wlo = reinterpret_cast<const uint16_t*>(ws + kWLo) + i * D + g4 * 8;
+__device__ __forceinline__ void load_w(const uint8_t* wsc, uint32_t lf, uint32_t lu, uint32_t ld,
+                                       WOps& o) {
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    o.whi[s] = ld16(whi + s * 32);
-    o.wlo[s] = ld16(wlo + s * 32);
+  for (int it = 0; it < 4; ++it) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      o.hi[it][s] = ld16(wsc + kWHi + lf + (it * 4 + s) * 1024);
+      o.lo[it][s] = ld16(wsc + kWLo + lf + (it * 4 + s) * 1024);
+    }
   }
-  // Rows past T (partial last chunk) read row T-1 and are zeroed by a select:
-  // no branch around the loads.
-  const int t = c * CH + i;
-  const bool valid = t < p.T;
-  const uint16_t* qr = qrow(p, b, hk, valid ? t : p.T - 1) + 4 * g4;
 #pragma unroll
-  for (int x = 0; x < 8; ++x) {
-    const u32x2 qv = ld8(qr + (x >> 1) * 32 + (x & 1) * 16);
-    o.q[x] = u32x2{valid ? qv.x : 0u, valid ? qv.y : 0u};
+  for (int it = 0; it < 4; ++it) {
+    o.ut[it] = ldf4(wsc + kUT + lu + it * 1024);
+    o.ed[it] = ldf4(wsc + kED + ld + it * 64);
   }
-  const uint16_t* phi = reinterpret_cast<const uint16_t*>(ws + kPHi) + i * CH + g4 * 8;
-  const uint16_t* plo = reinterpret_cast<const uint16_t*>(ws + kPLo) + i * CH + g4 * 8;
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    o.phi[s] = ld16(phi + s * 32);
-    o.plo[s] = ld16(plo + s * 32);
-  }
-  const uint16_t* kt = reinterpret_cast<const uint16_t*>(ws + kKT) + (wave * 32 + r16) * CH + g4 * 8;
-#pragma unroll
-  for (int x = 0; x < 4; ++x) o.kt[x] = ld16(kt + (x >> 1) * 16 * CH + (x & 1) * 32);
-  o.ut = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(ws + kUT) +
-                                         ((rb * 4 + wave) * 64 + lane) * 4);
-  const float* eg = reinterpret_cast<const float*>(ws + kEG);
-  const float* ed = reinterpret_cast<const float*>(ws + kED);
-  o.eg = *reinterpret_cast<const f32x4*>(eg + wave * 16 + 4 * g4);
-  o.ed = *reinterpret_cast<const f32x4*>(ed + wave * 16 + 4 * g4);
-  o.egC = eg[CH - 1];
+  o.egC = *reinterpret_cast<const float*>(wsc + kEG + (CH - 1) * 4);
 }
 
-// The wave's own 8 state values (slot t*4+e = sown[t][e]) as hi / lo bf16
-// halves, published for the other waves; fetch_state gathers all 32 columns of
-// k-steps 0..3 (k-step s = the columns owned by wave s).
-__device__ __forceinline__ void publish_state(const f32x4 (&sown)[2], u32x4 (*sS)[4][64], int wave,
-                                              int lane) {
-  sS[0][wave][lane] = u32x4{pack_hi(sown[0].x, sown[0].y), pack_hi(sown[0].z, sown[0].w),
-                            pack_hi(sown[1].x, sown[1].y), pack_hi(sown[1].z, sown[1].w)};
-  sS[1][wave][lane] = u32x4{pack_lo(sown[0].x, sown[0].y), pack_lo(sown[0].z, sown[0].w),
-                            pack_lo(sown[1].x, sown[1].y), pack_lo(sown[1].z, sown[1].w)};
-}
-
-__device__ __forceinline__ void fetch_state(u32x4 (*sS)[4][64], int lane, u32x4 (&shi)[4],
-                                            u32x4 (&slo)[4]) {
+__device__ __forceinline__ void load_kt(const uint8_t* wsc, uint32_t lf, u32x4 (&kt)[8][2]) {
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    shi[s] = sS[0][s][lane];
-    slo[s] = sS[1][s][lane];
+  for (int dt = 0; dt < 8; ++dt) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) kt[dt][s] = ld16(wsc + kKT + lf + (dt * 2 + s) * 1024);
   }
 }
 
-// One chunk of phase 2 for this wave: U, the output rows, the state update.
-__device__ __forceinline__ void chunk_step(const ChunkParams& p, const ChunkOps& ops, int c, int b,
-                                           int hv, int rb, int wave, int lane, f32x4 (&sown)[2],
-                                           u32x4 (&shi)[4], u32x4 (&slo)[4], u32x4 (*sS)[4][64],
-                                           uint16_t (*sU)[RB][CH + 8]) {
+__device__ __forceinline__ void load_q(const uint8_t* wsc, uint32_t lf, uint32_t ld, QOps& o) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) o.q[it][s] = ld16(wsc + kQ + lf + (it * 4 + s) * 1024);
+#pragma unroll
+    for (int s = 0; s < (it < 2 ? 1 : 2); ++s) {
+      o.ph[it][s] = ld16(wsc + kPHi + lf + (it * 2 + s) * 1024);
+      o.pl[it][s] = ld16(wsc + kPLo + lf + (it * 2 + s) * 1024);
+    }
+    o.eg[it] = ldf4(wsc + kEG + ld + it * 64);
+  }
+}
+
+// Tiles x0 (slots 0..3) and x1 (slots 4..7) as one B operand, hi and lo halves.
+__device__ __forceinline__ void split_pair(f32x4 x0, f32x4 x1, u32x4& hi, u32x4& lo) {
+  hi = u32x4{pack_hi(x0.x, x0.y), pack_hi(x0.z, x0.w), pack_hi(x1.x, x1.y), pack_hi(x1.z, x1.w)};
+  lo = u32x4{pack_lo(x0.x, x0.y), pack_lo(x0.z, x0.w), pack_lo(x1.x, x1.y), pack_lo(x1.z, x1.w)};
+}
+
+// Workgroup barrier that waits for this wave's LDS traffic only: global loads
+// in flight stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Output rows 16it + 4g + e (e = 0..3) of column r: bf16, rounded to nearest even.
+template <bool GUARD>
+__device__ __forceinline__ void store_out(uint16_t* obase, int64_t row_stride, f32x4 o, int row0,
+                                          int nvalid) {
+  const uint32_t p01 = cvt_pk_bf16(o.x, o.y), p23 = cvt_pk_bf16(o.z, o.w);
+  const uint16_t v[4] = {(uint16_t)p01, (uint16_t)(p01 >> 16), (uint16_t)p23, (uint16_t)(p23 >> 16)};
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    if (!GUARD || row0 + e < nvalid) obase[(row0 + e) * row_stride] = v[e];
+}
+
+__device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb, int lane,
+                                           Exchange* xb) {
   const int r16 = lane & 15;
   const int g4 = lane >> 4;
-  const int t0 = c * CH;
-
-  // (a) U = U~ - W S^T for this wave's 16 token rows x 16 state rows.
-  f32x4 a0 = {0.f, 0.f, 0.f, 0.f}, a1 = {0.f, 0.f, 0.f, 0.f}, a2 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    a0 = mfma(ops.whi[s], shi[s], a0);
-    a1 = mfma(ops.whi[s], slo[s], a1);
-    a2 = mfma(ops.wlo[s], shi[s], a2);
-  }
-  const f32x4 u = ops.ut - (a0 + a1 + a2);
-  const f32x4 ud = ops.ed * u;
-  {
-    u32x2 hi, lo;
-    const int j = wave * 16 + 4 * g4;
-    split4(u, hi, lo);
-    *reinterpret_cast<u32x2*>(&sU[0][r16][j]) = hi;
-    *reinterpret_cast<u32x2*>(&sU[1][r16][j]) = lo;
-    split4(ud, hi, lo);
-    *reinterpret_cast<u32x2*>(&sU[2][r16][j]) = hi;
-    *reinterpret_cast<u32x2*>(&sU[3][r16][j]) = lo;
-  }
-  lds_barrier();
-
-  // (b) O = diag(gamma) Q S^T + P U.
-  f32x4 o0 = {0.f, 0.f, 0.f, 0.f}, o1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    const u32x4 qa = {ops.q[2 * s].x, ops.q[2 * s].y, ops.q[2 * s + 1].x, ops.q[2 * s + 1].y};
-    o0 = mfma(qa, shi[s], o0);
-    o1 = mfma(qa, slo[s], o1);
-  }
-  f32x4 o = ops.eg * (o0 + o1);
-  {
-    f32x4 p0 = {0.f, 0.f, 0.f, 0.f}, p1 = {0.f, 0.f, 0.f, 0.f}, p2 = {0.f, 0.f, 0.f, 0.f};
-    // Both j-steps for every wave (P is exactly zero above the diagonal), so
-    // the loop has no wave-dependent branch.
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const u32x4 uh = *reinterpret_cast<const u32x4*>(&sU[0][r16][s * 32 + g4 * 8]);
-      const u32x4 ul = *reinterpret_cast<const u32x4*>(&sU[1][r16][s * 32 + g4 * 8]);
-      p0 = mfma(ops.phi[s], uh, p0);
-      p1 = mfma(ops.phi[s], ul, p1);
-      p2 = mfma(ops.plo[s], uh, p2);
-    }
-    o += p0 + p1 + p2;
-  }
-  {
-    const float ov[4] = {o.x, o.y, o.z, o.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int t = t0 + wave * 16 + 4 * g4 + e;
-      if (t < p.T)
-        p.out[(((int64_t)b * p.T + t) * p.Hv + hv) * D + rb * RB + r16] = f32_to_bf16_rne(ov[e]);
-    }
-  }
-
-  // (c) own state columns: S^T[dk][r] = gamma_C S^T + sum_j K^T[dk][j] Ud[j][r].
-  const float gam = ops.egC;
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    f32x4 acc = gam * sown[t];
-    f32x4 acc2 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const u32x4 dh = *reinterpret_cast<const u32x4*>(&sU[2][r16][s * 32 + g4 * 8]);
-      const u32x4 dl = *reinterpret_cast<const u32x4*>(&sU[3][r16][s * 32 + g4 * 8]);
-      acc = mfma(ops.kt[2 * t + s], dh, acc);
-      acc2 = mfma(ops.kt[2 * t + s], dl, acc2);
-    }
-    sown[t] = acc + acc2;
-  }
-  publish_state(sown, sS, wave, lane);
-  lds_barrier();
-  fetch_state(sS, lane, shi, slo);
-}
-
-// grid (B*Hv, D / RB), 256 threads.
-__global__ __launch_bounds__(256) void chunk_state_kernel(const ChunkParams p) {
-  __shared__ u32x4 sS[2][4][64];  // state exchange: hi / lo halves, [owner wave][lane]
-  __shared__ __attribute__((aligned(16))) uint16_t sU[4][RB][CH + 8];  // U hi/lo, Ud hi/lo, [r][j]
-  const int bh = blockIdx.x;
-  const int rb = blockIdx.y;
-  const int b = bh / p.Hv;
-  const int hv = bh - b * p.Hv;
-  const int hk = hv / p.rep;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int r16 = lane & 15;
-  const int g4 = lane >> 4;
-
-  // Own state columns: sown[t] = S[16rb + r16][32 wave + 16 t + 4 g4 + (0..3)].
-  f32x4 sown[2];
-  {
-    const float* s0 = p.state_in + ((int64_t)bh * D + rb * RB + r16) * D + wave * 32 + 4 * g4;
-    sown[0] = *reinterpret_cast<const f32x4*>(s0);
-    sown[1] = *reinterpret_cast<const f32x4*>(s0 + 16);
-  }
-  publish_state(sown, sS, wave, lane);
-  ChunkOps opsA;
-  load_ops(p, bh, b, hk, 0, rb, wave, lane, opsA);
-  lds_barrier();
-  // Full state as the B operand of the W / Q products: k-step s holds the
-  // columns owned by wave s, in the slot order of the W workspace layout.
-  u32x4 shi[4], slo[4];
-  fetch_state(sS, lane, shi, slo);
-
-  // Two operand sets in turn: the loads of chunk c + 1 are in flight while
-  // chunk c computes, with no register copies between iterations.
-  // The prefetch past the last chunk re-reads the last chunk (unconditional
-  // loads keep the wait counts exact: no branch merges around them).
+  const uint32_t lf = lane * 16;              // operand fragments
+  const uint32_t lu = rb * 4096 + lane * 16;  // U~
+  const uint32_t ld = g4 * 16;                // ED
+  const uint8_t* ws0 = p.ws + (int64_t)bh * p.NC * kWsChunk;
   const int last = p.NC - 1;
-  ChunkOps opsB;
-  for (int c = 0; c < p.NC; c += 2) {
-    load_ops(p, bh, b, hk, min(c + 1, last), rb, wave, lane, opsB);
-    chunk_step(p, opsA, c, b, hv, rb, wave, lane, sown, shi, slo, sS, sU);
-    if (c + 1 >= p.NC) break;
-    load_ops(p, bh, b, hk, min(c + 2, last), rb, wave, lane, opsA);
-    chunk_step(p, opsB, c + 1, b, hv, rb, wave, lane, sown, shi, slo, sS, sU);
+
+  f32x4 sT[8];
+  {
+    const float* s0 = p.state_in + ((int64_t)bh * D + rb * RB + r16) * D + 4 * g4;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) sT[dt] = ldf4(s0 + 16 * dt);
+  }
+  WOps w;
+  u32x4 kt[8][2];
+  load_w(ws0, lf, lu, ld, w);
+  load_kt(ws0, lf, kt);
+  for (int c = 0; c < p.NC; ++c) {
+    // Chunks past the last re-read the last one: the loads stay unconditional.
+    const uint8_t* wsn = ws0 + (int64_t)min(c + 1, last) * kWsChunk;
+    Exchange& x = xb[c & 1];
+
+    // S as the B operand (k = state column), hi / lo halves, shared.
+    u32x4 shi[4], slo[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      split_pair(sT[2 * s], sT[2 * s + 1], shi[s], slo[s]);
+      x.shi[s][lane] = shi[s];
+      x.slo[s][lane] = slo[s];
+    }
+
+    // U = U~ - W S^T and Ud = diag(ED) U, token tile it.
+    f32x4 u[4], ud[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        acc = mfma(w.hi[it][s], shi[s], acc);
+        acc = mfma(w.hi[it][s], slo[s], acc);
+        acc = mfma(w.lo[it][s], shi[s], acc);
+      }
+      u[it] = w.ut[it] - acc;
+      ud[it] = w.ed[it] * u[it];
+    }
+    const float egC = w.egC;
+    load_w(wsn, lf, lu, ld, w);  // this chunk's W is consumed
+
+    // U (shared) and Ud as the B operand (k = token), hi / lo halves.
+    u32x4 dh[2], dl[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      u32x4 uh, ul;
+      split_pair(u[2 * s], u[2 * s + 1], uh, ul);
+      x.uh[s][lane] = uh;
+      x.ul[s][lane] = ul;
+      split_pair(ud[2 * s], ud[2 * s + 1], dh[s], dl[s]);
+    }
+    lds_barrier();  // chunk c's S and U are visible to the output wave
+
+    // S^T = gamma_C S^T + K^T Ud  (K^T exact in bf16: two terms).
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      f32x4 a = egC * sT[dt];
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        a = mfma(kt[dt][s], dh[s], a);
+        a = mfma(kt[dt][s], dl[s], a);
+      }
+      sT[dt] = a;
+    }
+    load_kt(wsn, lf, kt);
   }
   if (p.final_state != nullptr) {
-    float* s1 = p.final_state + ((int64_t)bh * D + rb * RB + r16) * D + wave * 32 + 4 * g4;
-    *reinterpret_cast<f32x4*>(s1) = sown[0];
-    *reinterpret_cast<f32x4*>(s1 + 16) = sown[1];
+    float* s1 = p.final_state + ((int64_t)bh * D + rb * RB + r16) * D + 4 * g4;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(s1 + 16 * dt) = sT[dt];
   }
+}
+
+__device__ __forceinline__ void output_wave(const ChunkParams& p, int bh, int rb, int lane,
+                                            const Exchange* xb) {
+  const int r16 = lane & 15;
+  const int g4 = lane >> 4;
+  const uint32_t lf = lane * 16;
+  const uint32_t ld = g4 * 16;  // EG
+  const int b = bh / p.Hv;
+  const int hv = bh - b * p.Hv;
+  const uint8_t* ws0 = p.ws + (int64_t)bh * p.NC * kWsChunk;
+  const int last = p.NC - 1;
+  const int64_t orow = (int64_t)p.Hv * D;  // out row stride (elements)
+
+  QOps qo;
+  load_q(ws0, lf, ld, qo);
+  for (int c = 0; c < p.NC; ++c) {
+    lds_barrier();  // the state wave has published chunk c
+    const Exchange& x = xb[c & 1];
+    u32x4 shi[4], slo[4], uh[2], ul[2];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      shi[s] = x.shi[s][lane];
+      slo[s] = x.slo[s][lane];
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      uh[s] = x.uh[s][lane];
+      ul[s] = x.ul[s][lane];
+    }
+    const int nvalid = p.T - c * CH;
+    uint16_t* obase = p.out + ((int64_t)b * p.T + (int64_t)c * CH) * orow + hv * D + rb * RB + r16;
+    f32x4 o[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      o[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        o[it] = mfma(qo.q[it][s], shi[s], o[it]);
+        o[it] = mfma(qo.q[it][s], slo[s], o[it]);
+      }
+      o[it] = qo.eg[it] * o[it];
+#pragma unroll
+      for (int s = 0; s < (it < 2 ? 1 : 2); ++s) {
+        o[it] = mfma(qo.ph[it][s], uh[s], o[it]);
+        o[it] = mfma(qo.ph[it][s], ul[s], o[it]);
+        o[it] = mfma(qo.pl[it][s], uh[s], o[it]);
+      }
+    }
+    load_q(ws0 + (int64_t)min(c + 1, last) * kWsChunk, lf, ld, qo);  // this chunk's Q, P consumed
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      if (nvalid >= CH)
+        store_out<false>(obase, orow, o[it], 16 * it + 4 * g4, nvalid);
+      else
+        store_out<true>(obase, orow, o[it], 16 * it + 4 * g4, nvalid);
+    }
+  }
+}
+
+// grid 64 * ceil(B*Hv / 8) two-wave workgroups.  Workgroup id x -> head
+// bh = 8 (x / 64) + x % 8, rows 16 ((x / 8) % 8): the 8 workgroups of a head
+// share x % 8, which places them on one XCD (workgroups go round-robin over
+// the 8 XCDs), so a chunk's operands come from HBM once and from that XCD's
+// L2 for the other 7.  Both waves pass the same number of barriers (one per
+// chunk) and leave together.
+__global__ __launch_bounds__(128) void chunk_state_kernel(const ChunkParams p) {
+  __shared__ Exchange xb[2];
+  const int id = blockIdx.x;
+  const int rb = (id >> 3) & 7;
+  const int bh = (id >> 6) * 8 + (id & 7);
+  if (bh >= p.B * p.Hv) return;  // uniform over the workgroup
+  const int lane = threadIdx.x & 63;
+  if (threadIdx.x < 64)
+    state_wave(p, bh, rb, lane, xb);
+  else
+    output_wave(p, bh, rb, lane, xb);
 }
 
 }  // namespace
@@ -641,6 +710,6 @@ extern "C" int dflash_gdn_chunked_prefill(const void* q, const void* k, const vo
   hipLaunchKernelGGL(chunk_prep_kernel, dim3(p.NC, nbh), dim3(256), 0, s, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(chunk_state_kernel, dim3(nbh, D / RB), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(chunk_state_kernel, dim3((unsigned)(64 * ceil_div(nbh, 8))), dim3(128), 0, s, p);
   return to_status(hipGetLastError());
 }
