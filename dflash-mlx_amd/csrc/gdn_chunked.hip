@@ -406,8 +406,10 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
 // barrier per chunk; the output wave computes O = diag(EG) Q S^T + P U one
 // chunk behind, off the chain.
 
-struct WOps {                // state wave, per chunk
-  u32x4 hi[4][4], lo[4][4];  // W rows, [token tile it][k-step s]
+struct WOps {                // state wave, per chunk: W rows, [token tile it][k-step s]
+  u32x4 hi[4][4], lo[4][4];
+};
+struct UOps {                // state wave, per chunk (loaded at the chunk's start)
   f32x4 ut[4];               // U~[16it + 4g + e][16rb + lane%16]
   f32x4 ed[4];               // exp(G_63 - G) of the same token rows
   float egC;                 // exp(G_63)
@@ -422,8 +424,7 @@ struct Exchange {            // one chunk's S and U operand halves, [k-step][lan
   u32x4 uh[2][64], ul[2][64];
 };
 
-__device__ __forceinline__ void load_w(const uint8_t* wsc, uint32_t lf, uint32_t lu, uint32_t ld,
-                                       WOps& o) {
+__device__ __forceinline__ void load_w(const uint8_t* wsc, uint32_t lf, WOps& o) {
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
 #pragma unroll
@@ -432,6 +433,9 @@ __device__ __forceinline__ void load_w(const uint8_t* wsc, uint32_t lf, uint32_t
       o.lo[it][s] = ld16(wsc + kWLo + lf + (it * 4 + s) * 1024);
     }
   }
+}
+
+__device__ __forceinline__ void load_u(const uint8_t* wsc, uint32_t lu, uint32_t ld, UOps& o) {
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     o.ut[it] = ldf4(wsc + kUT + lu + it * 1024);
@@ -503,12 +507,17 @@ __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb,
   }
   WOps w;
   u32x4 kt[8][2];
-  load_w(ws0, lf, lu, ld, w);
+  load_w(ws0, lf, w);
   load_kt(ws0, lf, kt);
   for (int c = 0; c < p.NC; ++c) {
     // Chunks past the last re-read the last one: the loads stay unconditional.
+    const uint8_t* wsc = ws0 + (int64_t)c * kWsChunk;
     const uint8_t* wsn = ws0 + (int64_t)min(c + 1, last) * kWsChunk;
     Exchange& x = xb[c & 1];
+    // U~ and the decays are needed only after the W product: loaded here,
+    // they are not carried across iterations.
+    UOps uo;
+    load_u(wsc, lu, ld, uo);
 
     // S as the B operand (k = state column), hi / lo halves, shared.
     u32x4 shi[4], slo[4];
@@ -530,11 +539,15 @@ __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb,
         acc = mfma(w.hi[it][s], slo[s], acc);
         acc = mfma(w.lo[it][s], shi[s], acc);
       }
-      u[it] = w.ut[it] - acc;
-      ud[it] = w.ed[it] * u[it];
+      u[it] = uo.ut[it] - acc;
+      ud[it] = uo.ed[it] * u[it];
     }
-    const float egC = w.egC;
-    load_w(wsn, lf, lu, ld, w);  // this chunk's W is consumed
+    const float egC = uo.egC;
+    // This chunk's W is consumed: fetch the next.  The fences keep the W and
+    // K^T groups in program order, so waiting for W never waits for K^T.
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(wsn, lf, w);
+    __builtin_amdgcn_sched_barrier(0);
 
     // U (shared) and Ud as the B operand (k = token), hi / lo halves.
     u32x4 dh[2], dl[2];
@@ -559,7 +572,9 @@ __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb,
       }
       sT[dt] = a;
     }
+    __builtin_amdgcn_sched_barrier(0);
     load_kt(wsn, lf, kt);
+    __builtin_amdgcn_sched_barrier(0);
   }
   if (p.final_state != nullptr) {
     float* s1 = p.final_state + ((int64_t)bh * D + rb * RB + r16) * D + 4 * g4;
@@ -580,8 +595,25 @@ __device__ __forceinline__ void output_wave(const ChunkParams& p, int bh, int rb
   const int last = p.NC - 1;
   const int64_t orow = (int64_t)p.Hv * D;  // out row stride (elements)
 
+  // L2 prefetch: the output wave has slack on the chain, so it touches one
+  // dword per 128-byte line of chunk c + 3 of this head (its eighth of the
+  // lines), for the state wave's W and K^T loads two chunks later.  Each
+  // touch is consumed (waited for) one chunk after it is issued, and after
+  // that chunk's own loads, so in-order completion never holds them up.
+  const uint32_t t0o = min((uint32_t)((rb * 113 + lane) * 128), (uint32_t)(kWsChunk - 4));
+  const uint32_t t1o = min((uint32_t)((rb * 113 + min(lane + 64, 112)) * 128), (uint32_t)(kWsChunk - 4));
   QOps qo;
   load_q(ws0, lf, ld, qo);
+  // The first touches (chunk 2) go after chunk 0's Q / P loads, as in the
+  // loop, so the wait for Q / P at the loop head counts the same on entry.
+  __builtin_amdgcn_sched_barrier(0);
+  uint32_t ta, tb;
+  {
+    const uint32_t* tq = reinterpret_cast<const uint32_t*>(ws0 + (int64_t)min(2, last) * kWsChunk);
+    ta = tq[t0o >> 2];
+    tb = tq[t1o >> 2];
+  }
+  __builtin_amdgcn_sched_barrier(0);
   for (int c = 0; c < p.NC; ++c) {
     lds_barrier();  // the state wave has published chunk c
     const Exchange& x = xb[c & 1];
@@ -615,7 +647,6 @@ __device__ __forceinline__ void output_wave(const ChunkParams& p, int bh, int rb
         o[it] = mfma(qo.pl[it][s], uh[s], o[it]);
       }
     }
-    load_q(ws0 + (int64_t)min(c + 1, last) * kWsChunk, lf, ld, qo);  // this chunk's Q, P consumed
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       if (nvalid >= CH)
@@ -623,7 +654,21 @@ __device__ __forceinline__ void output_wave(const ChunkParams& p, int bh, int rb
       else
         store_out<true>(obase, orow, o[it], 16 * it + 4 * g4, nvalid);
     }
+    // Loads after the stores: waiting for them next chunk never depends on
+    // how many stores the guarded path issued.
+    __builtin_amdgcn_sched_barrier(0);
+    load_q(ws0 + (int64_t)min(c + 1, last) * kWsChunk, lf, ld, qo);  // this chunk's Q, P consumed
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("" ::"v"(ta), "v"(tb));
+    {
+      const uint32_t* tq =
+          reinterpret_cast<const uint32_t*>(ws0 + (int64_t)min(c + 3, last) * kWsChunk);
+      ta = tq[t0o >> 2];
+      tb = tq[t1o >> 2];
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
+  asm volatile("" ::"v"(ta), "v"(tb));
 }
 
 // grid 64 * ceil(B*Hv / 8) two-wave workgroups.  Workgroup id x -> head
