@@ -129,18 +129,11 @@ __device__ __forceinline__ u32x4 ld16(const void* ptr) { return *reinterpret_cas
 __device__ __forceinline__ u32x2 ld8(const void* ptr) { return *reinterpret_cast<const u32x2*>(ptr); }
 __device__ __forceinline__ f32x4 ldf4(const void* ptr) { return *reinterpret_cast<const f32x4*>(ptr); }
 
-// bf16 element index of (row i, column j) of a [64][64] matrix stored as
-// fragments [4 it][2 s] (column j = 32s + 16t + 4g + e, row i = 16it + r).
-__device__ __forceinline__ int frag64(int i, int j) {
-  return (((i >> 4) * 2 + (j >> 5)) * 64 + (i & 15) + 16 * ((j >> 2) & 3)) * 8 + ((j >> 4) & 1) * 4 +
-         (j & 3);
-}
-
 // ------------------------------------------------------------------ phase 1
 // grid (NC, B*Hv), 256 threads.
 __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
-  __shared__ float sA[CH][TPF];
-  __shared__ float sT[CH][TPF];
+  __shared__ __attribute__((aligned(16))) float sA[CH][TPF];
+  __shared__ __attribute__((aligned(16))) float sT[CH][TPF];
   __shared__ __attribute__((aligned(16))) uint16_t sKT[D][KTP];
   __shared__ __attribute__((aligned(16))) uint16_t sVT[D][KTP];
   __shared__ float sG[CH];
@@ -159,43 +152,78 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   const int g4 = lane >> 4;
   uint8_t* ws = p.ws + ((int64_t)bh * p.NC + c) * kWsChunk;
 
-  // K^T and V^T tiles (padded tokens are zero).  Rows past the chunk's valid
-  // tokens read row n-1 and are zeroed by a select, so all eight 16-byte
-  // loads of a thread are in flight together.
+  // All global loads first, so their latencies overlap.  Rows past the
+  // chunk's valid tokens read row n-1 and are zeroed by a select (no branch
+  // around the loads).
+  //  kk / vv: rows 4jq..4jq+3 of K and V, bf16 columns 8 piece .. +7, for
+  //           the transposed tiles K^T / V^T;
+  //  kf / qf: this wave's 16 token rows of K and Q as MFMA fragments in slot
+  //           order (k-step s: columns 32s+4g..+3 and 32s+16+4g..+3).
+  const int piece = tid & 15, jq = tid >> 4;
+  u32x4 kk[4], vv[4], kf[4], qf[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int jr = min(4 * jq + r, n - 1);
+    kk[r] = ld16(krow(p, b, hk, t0 + jr) + piece * 8);
+    vv[r] = ld16(vrow(p, b, hv, t0 + jr) + piece * 8);
+  }
+  const int ti = wave * 16 + r16;
+  const bool vi = ti < n;
   {
-    u32x4 kk[4], vv[4];
+    const uint16_t* kr = krow(p, b, hk, t0 + min(ti, n - 1)) + 4 * g4;
+    const uint16_t* qr = qrow(p, b, hk, t0 + min(ti, n - 1)) + 4 * g4;
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int e = tid + 256 * m;
-      const int j = e >> 4, piece = e & 15;
-      const int jr = j < n ? j : n - 1;
-      kk[m] = ld16(krow(p, b, hk, t0 + jr) + piece * 8);
-      vv[m] = ld16(vrow(p, b, hv, t0 + jr) + piece * 8);
+    for (int s = 0; s < 4; ++s) {
+      const u32x2 k0 = ld8(kr + 32 * s), k1 = ld8(kr + 32 * s + 16);
+      const u32x2 q0 = ld8(qr + 32 * s), q1 = ld8(qr + 32 * s + 16);
+      kf[s] = vi ? u32x4{k0.x, k0.y, k1.x, k1.y} : u32x4{0u, 0u, 0u, 0u};
+      qf[s] = vi ? u32x4{q0.x, q0.y, q1.x, q1.y} : u32x4{0u, 0u, 0u, 0u};
     }
+  }
+  float lg = 0.f, bt = 0.f;
+  if (wave == 0 && lane < n) {
+    lg = logf(fmaxf(p.g[b * p.g_sb + (int64_t)(t0 + lane) * p.g_st + hv], 1e-38f));
+    bt = p.beta[b * p.b_sb + (int64_t)(t0 + lane) * p.b_st + hv];
+  }
+
+  // K^T and V^T tiles (padded tokens zero): a 4-token x 8-column block per
+  // thread, transposed in registers and written as 8-byte rows of 4 tokens.
+  {
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int e = tid + 256 * m;
-      const int j = e >> 4, piece = e & 15;
-      const bool valid = j < n;
-      const uint32_t kw[4] = {kk[m].x, kk[m].y, kk[m].z, kk[m].w};
-      const uint32_t vw[4] = {vv[m].x, vv[m].y, vv[m].z, vv[m].w};
-#pragma unroll
-      for (int x = 0; x < 4; ++x) {
-        const uint32_t kx = valid ? kw[x] : 0u, vx = valid ? vw[x] : 0u;
-        sKT[piece * 8 + 2 * x][j] = (uint16_t)kx;
-        sKT[piece * 8 + 2 * x + 1][j] = (uint16_t)(kx >> 16);
-        sVT[piece * 8 + 2 * x][j] = (uint16_t)vx;
-        sVT[piece * 8 + 2 * x + 1][j] = (uint16_t)(vx >> 16);
+    for (int r = 0; r < 4; ++r) {
+      if (4 * jq + r >= n) {
+        kk[r] = u32x4{0u, 0u, 0u, 0u};
+        vv[r] = u32x4{0u, 0u, 0u, 0u};
       }
     }
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      const uint32_t k0 = kk[0][x], k1 = kk[1][x], k2 = kk[2][x], k3 = kk[3][x];
+      const uint32_t v0 = vv[0][x], v1 = vv[1][x], v2 = vv[2][x], v3 = vv[3][x];
+      // column 2x: low halves of tokens 0..3; column 2x+1: high halves.
+      *reinterpret_cast<u32x2*>(&sKT[piece * 8 + 2 * x][4 * jq]) =
+          u32x2{__builtin_amdgcn_perm(k1, k0, 0x05040100u), __builtin_amdgcn_perm(k3, k2, 0x05040100u)};
+      *reinterpret_cast<u32x2*>(&sKT[piece * 8 + 2 * x + 1][4 * jq]) =
+          u32x2{__builtin_amdgcn_perm(k1, k0, 0x07060302u), __builtin_amdgcn_perm(k3, k2, 0x07060302u)};
+      *reinterpret_cast<u32x2*>(&sVT[piece * 8 + 2 * x][4 * jq]) =
+          u32x2{__builtin_amdgcn_perm(v1, v0, 0x05040100u), __builtin_amdgcn_perm(v3, v2, 0x05040100u)};
+      *reinterpret_cast<u32x2*>(&sVT[piece * 8 + 2 * x + 1][4 * jq]) =
+          u32x2{__builtin_amdgcn_perm(v1, v0, 0x07060302u), __builtin_amdgcn_perm(v3, v2, 0x07060302u)};
+    }
+  }
+  // This wave's K fragments, shared (the A operand of the other waves' K K^T
+  // and Q K^T tiles); they live in sT's space until T is formed.
+  u32x4(*sKf)[64] = reinterpret_cast<u32x4(*)[64]>(&sT[0][0]);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) sKf[wave * 4 + s][lane] = kf[s];
+  // Q fragments go to the workspace as loaded.
+  {
+    u32x4* qw = reinterpret_cast<u32x4*>(ws + kQ);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qw[(wave * 4 + s) * 64 + lane] = qf[s];
   }
   // Cumulative log-decay and beta (padded tokens: g = 1, beta = 0).
   if (wave == 0) {
-    float lg = 0.f, bt = 0.f;
-    if (lane < n) {
-      lg = logf(fmaxf(p.g[b * p.g_sb + (int64_t)(t0 + lane) * p.g_st + hv], 1e-38f));
-      bt = p.beta[b * p.b_sb + (int64_t)(t0 + lane) * p.b_st + hv];
-    }
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) {
       const float o = __shfl_up(lg, off, 64);
@@ -209,56 +237,49 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   }
   __syncthreads();
 
-  // K K^T -> A (strictly lower, scaled), Q K^T -> P (lower, decay-masked).
-  // Wave w computes the 16-row tile w; tiles above the diagonal are zero.
+  // K K^T -> A (strictly lower, scaled) and Q K^T -> P (lower, decay-masked)
+  // for this wave's token rows i = 16 wave + r16, computed transposed
+  // (A operand = K rows j, B operand = this wave's K / Q rows), so lane
+  // (r16, g4) holds columns j = 16 jt + 4 g4 + e: four consecutive entries
+  // of row i, written to A as one 16-byte row piece, and tile pair
+  // (2s, 2s+1) is exactly P fragment (wave, s).  Tiles above the diagonal
+  // are zero (A's are never read).
   {
-    const int i0 = wave * 16;
-    uint16_t* phi = reinterpret_cast<uint16_t*>(ws + kPHi);
-    uint16_t* plo = reinterpret_cast<uint16_t*>(ws + kPLo);
-    // A-operand rows (this wave's 16 tokens) once, for all column tiles.
-    const int ti = i0 + r16;
-    const bool vi = ti < n;
-    const uint16_t* kri = krow(p, b, hk, t0 + (vi ? ti : n - 1)) + g4 * 8;
-    const uint16_t* qri = qrow(p, b, hk, t0 + (vi ? ti : n - 1)) + g4 * 8;
-    u32x4 ka[D / 32], qa[D / 32];
+    const int i = wave * 16 + r16;
+    const float gi = sG[i], bi = sBeta[i];
+    uint32_t phw[4], plw[4];  // one fragment (8 slots) as hi / lo words
 #pragma unroll
-    for (int ks = 0; ks < D / 32; ++ks) {
-      const u32x4 kv = ld16(kri + ks * 32), qv = ld16(qri + ks * 32);
-      ka[ks] = vi ? kv : u32x4{0u, 0u, 0u, 0u};
-      qa[ks] = vi ? qv : u32x4{0u, 0u, 0u, 0u};
-    }
     for (int jt = 0; jt < 4; ++jt) {
-      const int j0 = jt * 16;
-      f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
       if (jt <= wave) {
-        const int tj = j0 + r16;
-        const bool vj = tj < n;
-        const uint16_t* krj = krow(p, b, hk, t0 + (vj ? tj : n - 1)) + g4 * 8;
-        u32x4 kb[D / 32];
+        f32x4 kq = {0.f, 0.f, 0.f, 0.f}, qq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks) {
-          const u32x4 kv = ld16(krj + ks * 32);
-          kb[ks] = vj ? kv : u32x4{0u, 0u, 0u, 0u};
+        for (int s = 0; s < 4; ++s) {
+          const u32x4 ka = sKf[jt * 4 + s][lane];
+          kq = mfma(ka, kf[s], kq);
+          qq = mfma(ka, qf[s], qq);
         }
+        float av[4], pv[4];
 #pragma unroll
-        for (int ks = 0; ks < D / 32; ++ks) {
-          kk = mfma(ka[ks], kb[ks], kk);
-          qk = mfma(qa[ks], kb[ks], qk);
+        for (int e = 0; e < 4; ++e) {
+          const int j = jt * 16 + 4 * g4 + e;
+          const float dec = (j <= i) ? __expf(gi - sG[j]) : 0.f;
+          av[e] = (j < i) ? bi * dec * kq[e] : 0.f;
+          pv[e] = dec * qq[e];
         }
+        *reinterpret_cast<f32x4*>(&sA[i][jt * 16 + 4 * g4]) = f32x4{av[0], av[1], av[2], av[3]};
+        phw[(jt & 1) * 2] = pack_hi(pv[0], pv[1]);
+        phw[(jt & 1) * 2 + 1] = pack_hi(pv[2], pv[3]);
+        plw[(jt & 1) * 2] = pack_lo(pv[0], pv[1]);
+        plw[(jt & 1) * 2 + 1] = pack_lo(pv[2], pv[3]);
+      } else {
+        phw[(jt & 1) * 2] = phw[(jt & 1) * 2 + 1] = 0u;
+        plw[(jt & 1) * 2] = plw[(jt & 1) * 2 + 1] = 0u;
       }
-      // Tile element (i, j): lane holds j = j0 + r16, i = i0 + 4*g4 + e.
-      const float vkk[4] = {kk.x, kk.y, kk.z, kk.w};
-      const float vqk[4] = {qk.x, qk.y, qk.z, qk.w};
-      const int j = j0 + r16;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int i = i0 + g4 * 4 + e;
-        const float dec = (j <= i) ? __expf(sG[i] - sG[j]) : 0.f;
-        sA[i][j] = (j < i) ? sBeta[i] * dec * vkk[e] : 0.f;
-        const float pv = (j <= i) ? dec * vqk[e] : 0.f;
-        const uint32_t hb = __float_as_uint(pv) & 0xFFFF0000u;
-        phi[frag64(i, j)] = (uint16_t)(hb >> 16);
-        plo[frag64(i, j)] = f32_to_bf16_rne(pv - __uint_as_float(hb));
+      // Phase 2 reads P fragments (it, s) with s < (it < 2 ? 1 : 2).
+      if ((jt & 1) && (jt >> 1) < (wave < 2 ? 1 : 2)) {
+        const int f = wave * 2 + (jt >> 1);
+        reinterpret_cast<u32x4*>(ws + kPHi)[f * 64 + lane] = u32x4{phw[0], phw[1], phw[2], phw[3]};
+        reinterpret_cast<u32x4*>(ws + kPLo)[f * 64 + lane] = u32x4{plw[0], plw[1], plw[2], plw[3]};
       }
     }
   }
@@ -271,18 +292,6 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
       const u32x2 z = *reinterpret_cast<const u32x2*>(&sKT[dk][32 * s + 16 + 4 * g]);
       *reinterpret_cast<u32x4*>(kt + (((dk >> 4) * 2 + s) * 64 + (dk & 15) + 16 * g) * 8) =
           u32x4{a.x, a.y, z.x, z.y};
-    }
-  }
-  // Q fragments [4 it][4 s] (padded rows zero): 16 bytes per (i, s, g).
-  {
-    uint16_t* qw = reinterpret_cast<uint16_t*>(ws + kQ);
-    for (int e = tid; e < CH * 16; e += 256) {
-      const int i = e >> 4, s = (e >> 2) & 3, g = e & 3;
-      const bool valid = i < n;
-      const uint16_t* qr = qrow(p, b, hk, t0 + (valid ? i : n - 1)) + 32 * s + 4 * g;
-      const u32x2 a = ld8(qr), z = ld8(qr + 16);
-      *reinterpret_cast<u32x4*>(qw + (((i >> 4) * 4 + s) * 64 + (i & 15) + 16 * g) * 8) =
-          valid ? u32x4{a.x, a.y, z.x, z.y} : u32x4{0u, 0u, 0u, 0u};
     }
   }
   __syncthreads();
