@@ -274,7 +274,9 @@ def measure_hybrid(torch, dev, steps=40):
     wbytes = 2 * (w.lm_head.numel() + w.final_norm.numel() + B * T * cfg.hidden_size)
     for lw in w.layers:
         for k_, v_ in lw.items():
-            if isinstance(v_, torch.Tensor) and k_ != "w_gu_pairs":  # one copy of gate|up is read
+            # one copy of each weight is read: skip the regrouped gate|up and the
+            # fragment-tiled copies the GEMMs stream in place of the originals
+            if isinstance(v_, torch.Tensor) and k_ != "w_gu_pairs" and not k_.endswith("_tiled"):
                 wbytes += 2 * v_.numel()
     tape_bytes = 4 * cfg.n_linear * (T + 1) * B * lc.linear_num_value_heads * \
         lc.linear_value_head_dim * lc.linear_key_head_dim

@@ -16,6 +16,12 @@
 //     rows (L2-resident); fp32 accumulation; lane (r16 = l % 16, g = l / 16)
 //     holds elements 16g .. 16g+15 of the 64-wide step for both operands, so
 //     the contraction is exact whatever order the hardware gives the k-slots.
+//   - Tiled weights (dflash_weight_tile_bf16, once at load time): the weight
+//     stored as those A fragments, [N/16 row tiles][K/64 k-steps][2 halves]
+//     [64 lanes][8], so every fragment is one contiguous 1 KB load straight
+//     into MFMA registers (no LDS step) and a workgroup's rows are one
+//     contiguous stretch of memory.  Same k-slots, so the same sums, bit for
+//     bit, as the row-major path.
 //   - Epilogue, nsplit == 1 requested: bf16 (round to nearest even) into
 //     out, or (dflash_gemm_bf16_swiglu) the MLP gating silu(gate) * up of a
 //     weight whose 32-row blocks are 16 gate rows then the 16 matching up
@@ -68,7 +74,7 @@ struct GStage {
 // waves stream the same 16*VT rows over quarters of the k-range and merge
 // their sums through LDS: four times the loads in flight per output tile,
 // without partial sums in memory).
-template <int MT, int VT, int D, int KW>
+template <int MT, int VT, int D, int KW, bool TILED>
 __global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams p) {
   __shared__ __attribute__((aligned(16))) unsigned char atile[kGThreads / 64][VT * 16 * kGTileRowBytes];
   __shared__ f32x4 red[KW > 1 ? KW - 1 : 1][VT * MT][64];
@@ -88,10 +94,19 @@ __global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams
   const int nks = min(part_len, split_begin + split_len - ks_begin);
 
   const uint16_t* wrow[2 * VT];
+  if (TILED) {  // fragment (row tile, k-step, half): 1 KB at ((rt * nks_all + ks) * 2 + h) KB
 #pragma unroll
-  for (int i = 0; i < 2 * VT; ++i) {
-    const int n = min(nwave + i * 8 + (lane >> 3), p.N - 1);  // tail rows re-read row N-1
-    wrow[i] = p.w + (int64_t)n * p.ws + (int64_t)ks_begin * kGKStep + (lane & 7) * 8;
+    for (int vt = 0; vt < VT; ++vt) {
+      const int rt = min(nwave / 16 + vt, p.N / 16 - 1);  // tail tiles re-read the last
+      wrow[2 * vt] = p.w + ((int64_t)rt * nks_all + ks_begin) * (2 * 512) + lane * 8;
+      wrow[2 * vt + 1] = wrow[2 * vt] + 512;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 2 * VT; ++i) {
+      const int n = min(nwave + i * 8 + (lane >> 3), p.N - 1);  // tail rows re-read row N-1
+      wrow[i] = p.w + (int64_t)n * p.ws + (int64_t)ks_begin * kGKStep + (lane & 7) * 8;
+    }
   }
   const uint16_t* xrow[MT];
 #pragma unroll
@@ -100,8 +115,9 @@ __global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams
 
   auto load = [&](GStage<MT, VT>& st, int ks) {
     const int off = ks * kGKStep;
+    const int woff = TILED ? ks * 1024 : off;
 #pragma unroll
-    for (int i = 0; i < 2 * VT; ++i) st.a[i] = *reinterpret_cast<const u32x4*>(wrow[i] + off);
+    for (int i = 0; i < 2 * VT; ++i) st.a[i] = *reinterpret_cast<const u32x4*>(wrow[i] + woff);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       st.b[mt][0] = *reinterpret_cast<const u32x4*>(xrow[mt] + off);
@@ -126,16 +142,24 @@ __global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams
     for (int d = 0; d < D; ++d) {
       const int ks = ks0 + d;
       if (ks < nks) {
-#pragma unroll
-        for (int i = 0; i < 2 * VT; ++i)
-          *reinterpret_cast<u32x4*>(tile + (i * 8 + (lane >> 3)) * kGTileRowBytes + (lane & 7) * 16) =
-              ring[d].a[i];
         u32x4 a[VT][2];
+        if (TILED) {
 #pragma unroll
-        for (int vt = 0; vt < VT; ++vt)
+          for (int vt = 0; vt < VT; ++vt) {
+            a[vt][0] = ring[d].a[2 * vt];
+            a[vt][1] = ring[d].a[2 * vt + 1];
+          }
+        } else {
 #pragma unroll
-          for (int h = 0; h < 2; ++h)
-            a[vt][h] = *reinterpret_cast<const u32x4*>(tile + (vt * 16 + r16) * kGTileRowBytes + (2 * g + h) * 16);
+          for (int i = 0; i < 2 * VT; ++i)
+            *reinterpret_cast<u32x4*>(tile + (i * 8 + (lane >> 3)) * kGTileRowBytes + (lane & 7) * 16) =
+                ring[d].a[i];
+#pragma unroll
+          for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+              a[vt][h] = *reinterpret_cast<const u32x4*>(tile + (vt * 16 + r16) * kGTileRowBytes + (2 * g + h) * 16);
+        }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -225,20 +249,38 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, i
   }
 }
 
-template <int MT, int VT, int KW>
+template <int MT, int VT, int KW, bool TILED>
 hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
   constexpr int D = MT == 1 ? 4 : (MT == 2 ? 4 : 2);
   const int rows_per_wg = (kGThreads / 64 / KW) * VT * 16;
   const dim3 grid((unsigned)ceil_div(p.N, rows_per_wg), (unsigned)p.nsplit);
-  hipLaunchKernelGGL((skinny_gemm_kernel<MT, VT, D, KW>), grid, dim3(kGThreads), 0, s, p);
+  hipLaunchKernelGGL((skinny_gemm_kernel<MT, VT, D, KW, TILED>), grid, dim3(kGThreads), 0, s, p);
   return hipGetLastError();
 }
 
-template <int VT, int KW>
+template <int VT, int KW, bool TILED = false>
 hipError_t launch_m(const GemmParams& p, hipStream_t s) {
   const int mt = (int)ceil_div(p.M, 16);
-  return mt == 1 ? launch_gemm<1, VT, KW>(p, s) : mt == 2 ? launch_gemm<2, VT, KW>(p, s)
-       : mt == 3 ? launch_gemm<3, VT, KW>(p, s) : launch_gemm<4, VT, KW>(p, s);
+  return mt == 1 ? launch_gemm<1, VT, KW, TILED>(p, s) : mt == 2 ? launch_gemm<2, VT, KW, TILED>(p, s)
+       : mt == 3 ? launch_gemm<3, VT, KW, TILED>(p, s) : launch_gemm<4, VT, KW, TILED>(p, s);
+}
+
+// dst = src stored as A fragments: dst[((rt * (K/64) + ks) * 2 + h) * 512 + lane * 8 + e]
+//   = src[16 rt + lane % 16][64 ks + 16 (lane / 16) + 8 h + e].
+__global__ __launch_bounds__(256) void weight_tile_kernel(const uint16_t* src, int64_t ss,
+                                                          uint16_t* dst, int N, int K) {
+  const int nks = K / kGKStep;
+  const int64_t nfrag = (int64_t)(N / 16) * nks * 2 * 64;  // 16-byte pieces
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < nfrag; e += (int64_t)gridDim.x * 256) {
+    const int lane = (int)(e & 63);
+    const int64_t f = e >> 6;  // (rt * nks + ks) * 2 + h
+    const int h = (int)(f & 1);
+    const int64_t tk = f >> 1;
+    const int ks = (int)(tk % nks);
+    const int rt = (int)(tk / nks);
+    const uint16_t* s = src + (int64_t)(16 * rt + (lane & 15)) * ss + 64 * ks + 16 * (lane >> 4) + 8 * h;
+    *reinterpret_cast<u32x4*>(dst + e * 8) = *reinterpret_cast<const u32x4*>(s);
+  }
 }
 
 }  // namespace
@@ -336,4 +378,94 @@ extern "C" int dflash_splitk_reduce(const float* partials, int nsplit, int M, in
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
                      partials, nsplit, M, N, static_cast<uint16_t*>(out), out_row_stride);
   return to_status(hipGetLastError());
+}
+
+extern "C" size_t dflash_weight_tile_bytes(int N, int K) {
+  if (N <= 0 || K <= 0 || N % 16 != 0 || K % kGKStep != 0) return 0;
+  return (size_t)N * K * 2;
+}
+
+extern "C" int dflash_weight_tile_bf16(const void* w, int64_t w_row_stride, void* w_tiled, int N,
+                                       int K, void* stream) {
+  if (N <= 0 || K <= 0 || N % 16 != 0 || K % kGKStep != 0) return DFLASH_ERR_SHAPE;
+  if (w == nullptr || w_tiled == nullptr) return DFLASH_ERR_NULL;
+  if (((uintptr_t)w & 15) || ((uintptr_t)w_tiled & 15) || (w_row_stride % 8) || w_row_stride < K)
+    return DFLASH_ERR_ALIGN;
+  const int64_t nfrag = (int64_t)N * K / 8;
+  const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(nfrag, 256), 4096);
+  hipLaunchKernelGGL(weight_tile_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     static_cast<const uint16_t*>(w), w_row_stride, static_cast<uint16_t*>(w_tiled),
+                     N, K);
+  return to_status(hipGetLastError());
+}
+
+extern "C" int dflash_gemm_bf16_tiled(const void* x, int64_t x_row_stride, const void* w_tiled,
+                                      void* out, int64_t out_row_stride, int M, int N, int K,
+                                      int nsplit, int rows_per_wave, int k_waves, void* stream) {
+  if (M < 0 || M > 64 || N <= 0 || N % 16 != 0 || K <= 0 || K % kGKStep != 0 || nsplit < 1)
+    return DFLASH_ERR_SHAPE;
+  if ((rows_per_wave != 16 && rows_per_wave != 32 && rows_per_wave != 64) ||
+      (k_waves != 1 && k_waves != 4))
+    return DFLASH_ERR_UNSUPPORTED;
+  if (M == 0) return DFLASH_OK;
+  if (x == nullptr || w_tiled == nullptr || out == nullptr) return DFLASH_ERR_NULL;
+  if (((uintptr_t)x & 15) || ((uintptr_t)w_tiled & 15) || (x_row_stride % 8) || x_row_stride < K)
+    return DFLASH_ERR_ALIGN;
+  GemmParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.xs = x_row_stride;
+  p.w = static_cast<const uint16_t*>(w_tiled);
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  const int nks = K / kGKStep;
+  const int want = std::min(nsplit, nks);
+  p.ks_per_split = (int)ceil_div(nks, want);
+  p.nsplit = (int)ceil_div(nks, p.ks_per_split);
+  p.f32_out = nsplit > 1;
+  if (p.f32_out) {
+    if ((uintptr_t)out & 15) return DFLASH_ERR_ALIGN;
+    p.part = static_cast<float*>(out);
+  } else {
+    if (((uintptr_t)out & 7) || (out_row_stride % 4) || out_row_stride < N) return DFLASH_ERR_ALIGN;
+    p.out = static_cast<uint16_t*>(out);
+    p.os = out_row_stride;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (rows_per_wave == 16)
+    e = k_waves == 1 ? launch_m<1, 1, true>(p, s) : launch_m<1, 4, true>(p, s);
+  else if (rows_per_wave == 32)
+    e = k_waves == 1 ? launch_m<2, 1, true>(p, s) : launch_m<2, 4, true>(p, s);
+  else
+    e = k_waves == 1 ? launch_m<4, 1, true>(p, s) : launch_m<4, 4, true>(p, s);
+  return to_status(e);
+}
+
+extern "C" int dflash_gemm_bf16_swiglu_tiled(const void* x, int64_t x_row_stride,
+                                             const void* w_pairs_tiled, void* out,
+                                             int64_t out_row_stride, int M, int N, int K,
+                                             int k_waves, void* stream) {
+  if (M < 0 || M > 64 || N <= 0 || N % 32 != 0 || K <= 0 || K % kGKStep != 0)
+    return DFLASH_ERR_SHAPE;
+  if (k_waves != 1 && k_waves != 4) return DFLASH_ERR_UNSUPPORTED;
+  if (M == 0) return DFLASH_OK;
+  if (x == nullptr || w_pairs_tiled == nullptr || out == nullptr) return DFLASH_ERR_NULL;
+  if (((uintptr_t)x & 15) || ((uintptr_t)w_pairs_tiled & 15) || (x_row_stride % 8) ||
+      x_row_stride < K || ((uintptr_t)out & 7) || (out_row_stride % 4) || out_row_stride < N / 2)
+    return DFLASH_ERR_ALIGN;
+  GemmParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.xs = x_row_stride;
+  p.w = static_cast<const uint16_t*>(w_pairs_tiled);
+  p.out = static_cast<uint16_t*>(out);
+  p.os = out_row_stride;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.ks_per_split = K / kGKStep;
+  p.nsplit = 1;
+  p.swiglu = 1;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return to_status(k_waves == 1 ? launch_m<2, 1, true>(p, s) : launch_m<2, 4, true>(p, s));
 }

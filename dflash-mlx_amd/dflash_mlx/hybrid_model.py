@@ -145,13 +145,21 @@ class HybridVerifyRunner:
     for B sequences of T block tokens, with caches of Smax positions."""
 
     def __init__(self, cfg: HybridConfig, weights: HybridWeights, B: int, T: int, Smax: int,
-                 device: torch.device, gemm: str = "dflash"):
+                 device: torch.device, gemm: str = "dflash", weight_layout: str = "tiled"):
         """gemm: "dflash" runs every projection on this package's verify-sized
-        GEMM (dflash_gemm_bf16, split-K partials summed by the consumer);
-        "hipblaslt" runs them as torch.mm (for comparison)."""
+        GEMM (split-K partials summed by the consumer); "hipblaslt" runs them
+        as torch.mm (for comparison).  weight_layout (dflash GEMMs): "tiled"
+        streams weights re-laid out once as MFMA fragments
+        (dflash_weight_tile_bf16, cached in the layer dicts as "<name>_tiled";
+        same sums bit for bit) wherever the row count is a multiple of 16 (the
+        rest stay row-major), "rowmajor" streams the nn.Linear [N, K] weights
+        as they are."""
         if gemm not in ("dflash", "hipblaslt"):
             raise ValueError(f"gemm must be 'dflash' or 'hipblaslt', got {gemm!r}")
+        if weight_layout not in ("tiled", "rowmajor"):
+            raise ValueError(f"weight_layout must be 'tiled' or 'rowmajor', got {weight_layout!r}")
         self.gemm = gemm
+        self.tiled = weight_layout == "tiled"
         if T > 16 or B * T > 64:
             raise ValueError("the verify step takes T <= 16 block tokens and B*T <= 64 rows")
         if Smax % 64:
@@ -212,6 +220,9 @@ class HybridVerifyRunner:
     # partials where the next add + RMSNorm sums them.
     GEMM_PLAN = {"w_in": (1, 32, 4), "w_out": (8, 16, 4), "w_qkv": (1, 32, 4),
                  "w_o": (8, 32, 4), "w_gu": (1, 32, 4), "w_down": (8, 32, 4)}
+    # the same for fragment-tiled weights (rows_per_wave 64 exists only there)
+    TILED_PLAN = {"w_in": (1, 64, 4), "w_out": (8, 16, 4), "w_qkv": (1, 32, 4),
+                  "w_o": (8, 16, 4), "w_gu": (1, 32, 4), "w_down": (8, 32, 4)}
 
     def _build_gemms(self):
         """Argument tuples of every projection GEMM, and the split-K partial
@@ -224,17 +235,42 @@ class HybridVerifyRunner:
                 "w_o": (H, cfg.num_attention_heads * cfg.head_dim),
                 "w_gu": (2 * I, H), "w_down": (H, I)}
         lib = _lib.load()
+        plan_of = self.TILED_PLAN if self.tiled else self.GEMM_PLAN
+        self.plan = plan_of
         self.splits = {k: int(lib.dflash_gemm_splits(dims[k][1], plan[0])) if plan[0] > 1 else 0
-                       for k, plan in self.GEMM_PLAN.items()}
+                       for k, plan in plan_of.items()}
         part_elems = max([self.splits[k] * M * dims[k][0] for k in dims] + [1])
         self.part = torch.empty(part_elems, dtype=torch.float32, device=self.device)
         pp = self.part.data_ptr()
 
-        def args(x, name, w, out_ptr, out_stride):
+        stream = _lib.stream_handle(self.device)
+
+        def tiled(lw, key, w):
+            """The fragment-tiled copy of weight w, made once per weight set."""
+            tkey = key + "_tiled"
+            if tkey not in lw:
+                n, k = w.shape
+                t = torch.empty(int(lib.dflash_weight_tile_bytes(n, k)) // 2, dtype=torch.bfloat16,
+                                device=self.device)
+                _lib.call("dflash_weight_tile_bf16", w.data_ptr(), w.stride(0), t.data_ptr(), n, k,
+                          stream)
+                lw[tkey] = t
+            return lw[tkey]
+
+        def args(lw, x, name, out_ptr, out_stride):
+            """(entry point, arguments) of projection `name` of layer dict lw."""
             n, k = dims[name]
-            ns, rpw, kw = self.GEMM_PLAN[name]
-            return (x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out_ptr, out_stride, M, n,
-                    k, ns, rpw, kw)
+            ns, rpw, kw = plan_of[name]
+            if self.tiled and n % 16 == 0:  # the fragment layout needs whole 16-row tiles
+                return ("dflash_gemm_bf16_tiled",
+                        (x.data_ptr(), x.stride(0), tiled(lw, name, lw[name]).data_ptr(), out_ptr,
+                         out_stride, M, n, k, ns, rpw, kw))
+            w = lw[name]
+            # row-major kernel widths; the split count stays the one the
+            # consumers were set up for
+            rpw, kw = self.GEMM_PLAN[name][1], self.GEMM_PLAN[name][2]
+            return ("dflash_gemm_bf16", (x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0),
+                                         out_ptr, out_stride, M, n, k, ns, rpw, kw))
 
         def gate_up_pairs(lw):
             """w_gu [gate; up] rows regrouped into 32-row blocks (16 gate rows,
@@ -254,17 +290,24 @@ class HybridVerifyRunner:
         for i in range(cfg.num_hidden_layers):
             lw = self.w.layers[i]
             wp = gate_up_pairs(lw)
-            a = {"gu": (self.xn.data_ptr(), H, wp.data_ptr(), H, self.mlp_act.data_ptr(), I, M, 2 * I,
-                        H, self.GEMM_PLAN["w_gu"][2]),
-                 "down": args(self.mlp_act, "w_down", lw["w_down"], *dst("w_down", self.r))}
+            if self.tiled:
+                gu = ("dflash_gemm_bf16_swiglu_tiled",
+                      (self.xn.data_ptr(), H, tiled(lw, "w_gu_pairs", wp).data_ptr(),
+                       self.mlp_act.data_ptr(), I, M, 2 * I, H, plan_of["w_gu"][2]))
+            else:
+                gu = ("dflash_gemm_bf16_swiglu",
+                      (self.xn.data_ptr(), H, wp.data_ptr(), H, self.mlp_act.data_ptr(), I, M, 2 * I,
+                       H, plan_of["w_gu"][2]))
+            a = {"gu": gu, "down": args(lw, self.mlp_act, "w_down", *dst("w_down", self.r))}
             if cfg.is_linear(i):
-                a["in"] = args(self.xn, "w_in", lw["w_in"], *dst("w_in", self.proj[gi]))
-                a["out"] = args(self.gnorm.view(M, -1), "w_out", lw["w_out"], *dst("w_out", self.r))
+                a["in"] = args(lw, self.xn, "w_in", *dst("w_in", self.proj[gi]))
+                a["out"] = args(lw, self.gnorm.view(M, -1), "w_out", *dst("w_out", self.r))
                 gi += 1
             else:
-                a["qkv"] = args(self.xn, "w_qkv", lw["w_qkv"], *dst("w_qkv", self.aproj))
-                a["o"] = args(self.attn_out, "w_o", lw["w_o"], *dst("w_o", self.r))
+                a["qkv"] = args(lw, self.xn, "w_qkv", *dst("w_qkv", self.aproj))
+                a["o"] = args(lw, self.attn_out, "w_o", *dst("w_o", self.r))
             self._gemm_args.append(a)
+        torch.cuda.synchronize(self.device)
 
     def _residual(self, name, w_norm, stream):
         """h += the branch just produced by projection `name`; xn = norm(h)."""
@@ -382,26 +425,26 @@ class HybridVerifyRunner:
                 self._residual("w_down", lw["ln_in"], stream)
             if cfg.is_linear(i):
                 prologue, scan, gnorm = self._gdn_args[gi]
-                call("dflash_gemm_bf16", *ga["in"], stream)
+                call(ga["in"][0], *ga["in"][1], stream)
                 call("dflash_gdn_prologue", *prologue, stream)
                 call("dflash_gdn_verify_scan_rollback", *scan, stream)
                 call("dflash_gdn_gated_rmsnorm", *gnorm, stream)
-                call("dflash_gemm_bf16", *ga["out"], stream)
+                call(ga["out"][0], *ga["out"][1], stream)
                 self._residual("w_out", lw["ln_post"], stream)
                 gi += 1
             else:
                 prep, attn = self._attn_args[ai]
-                call("dflash_gemm_bf16", *ga["qkv"], stream)
+                call(ga["qkv"][0], *ga["qkv"][1], stream)
                 if self.splits["w_qkv"]:
                     call("dflash_splitk_reduce", self.part.data_ptr(), self.splits["w_qkv"], M,
                          cfg.attn_proj_rows, self.aproj.data_ptr(), cfg.attn_proj_rows, stream)
                 call("dflash_attn_prep", *prep, stream)
                 call("dflash_attn_verify", *attn, stream)
-                call("dflash_gemm_bf16", *ga["o"], stream)
+                call(ga["o"][0], *ga["o"][1], stream)
                 self._residual("w_o", lw["ln_post"], stream)
                 ai += 1
-            call("dflash_gemm_bf16_swiglu", *ga["gu"], stream)
-            call("dflash_gemm_bf16", *ga["down"], stream)
+            call(ga["gu"][0], *ga["gu"][1], stream)
+            call(ga["down"][0], *ga["down"][1], stream)
         self._residual("w_down", self.w.final_norm, stream)
         call("dflash_lm_head_greedy_accept", *self._lm_args, stream)
 

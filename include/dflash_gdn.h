@@ -382,6 +382,32 @@ int dflash_gemm_bf16_swiglu(const void* x, int64_t x_row_stride,
                             int K, int k_waves, void* stream);
 
 /*
+ * The same projections with the weight stored once, at load time, as MFMA
+ * fragments (the nn.Linear weight [N, K] of custom_qwen35_model.py:726-736
+ * and mlx-lm's attention / MLP Linears, re-laid out for streaming):
+ *   w_tiled[((rt * (K/64) + ks) * 2 + h) * 512 + l * 8 + e]
+ *     = w[16 rt + l % 16][64 ks + 16 (l / 16) + 8 h + e],
+ * so every 64-lane load is 1 KB of contiguous memory going straight into
+ * matrix-core registers.  dflash_weight_tile_bf16 builds it (N % 16 == 0,
+ * K % 64 == 0; dflash_weight_tile_bytes(N, K) bytes, 16-byte aligned); the
+ * _tiled GEMMs take it in place of (w, w_row_stride) and return the same sums
+ * bit for bit as their row-major counterparts.  rows_per_wave may also be 64
+ * here.  dflash_gemm_bf16_swiglu_tiled takes the tiled form of its w_pairs.
+ */
+size_t dflash_weight_tile_bytes(int N, int K);
+int dflash_weight_tile_bf16(const void* w, int64_t w_row_stride, void* w_tiled,
+                            int N, int K, void* stream);
+int dflash_gemm_bf16_tiled(const void* x, int64_t x_row_stride,
+                           const void* w_tiled, void* out,
+                           int64_t out_row_stride, int M, int N, int K,
+                           int nsplit, int rows_per_wave, int k_waves,
+                           void* stream);
+int dflash_gemm_bf16_swiglu_tiled(const void* x, int64_t x_row_stride,
+                                  const void* w_pairs_tiled, void* out,
+                                  int64_t out_row_stride, int M, int N, int K,
+                                  int k_waves, void* stream);
+
+/*
  * out[m, n] = bf16(sum_s partials[s, m, n]) for partials fp32 [nsplit, M, N]
  * (N % 4 == 0), out bf16 with row stride out_row_stride.
  */

@@ -126,3 +126,95 @@ def test_gemm_swiglu_fused(device, M, I, K, kw):
     err = ((out.float() - ref).abs() - 2 ** -7 * ref.abs()).max().item()
     print(f"[gemm swiglu] M={M} I={I} K={K} kw={kw}: excess {err:.3e} (rms {scale:.3e})", flush=True)
     assert err <= 1e-3 * scale
+
+
+def _tile(device, w):
+    N, K = w.shape
+    lib = _lib.load()
+    t = torch.empty(int(lib.dflash_weight_tile_bytes(N, K)) // 2, dtype=torch.bfloat16, device=device)
+    _lib.call("dflash_weight_tile_bf16", w.data_ptr(), w.stride(0), t.data_ptr(), N, K,
+              _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    return t
+
+
+def test_weight_tile_layout(device):
+    """The fragment layout entry by entry, from its defining formula."""
+    N, K = 48, 192
+    w = torch.arange(N * K, dtype=torch.float32).remainder(251).reshape(N, K).bfloat16().to(device)
+    t = _tile(device, w).cpu().float().numpy()
+    wn = w.cpu().float().numpy()
+    nks = K // 64
+    for rt in range(N // 16):
+        for ks in range(nks):
+            for h in range(2):
+                for lane in range(64):
+                    base = ((rt * nks + ks) * 2 + h) * 512 + lane * 8
+                    row = 16 * rt + lane % 16
+                    col = 64 * ks + 16 * (lane // 16) + 8 * h
+                    assert (t[base:base + 8] == wn[row, col:col + 8]).all(), (rt, ks, h, lane)
+
+
+@pytest.mark.parametrize("N,K,nsplit", C4_SHAPES)
+@pytest.mark.parametrize("rpw,kw", [(16, 4), (32, 4), (32, 1)])
+def test_gemm_tiled_bit_identical(device, N, K, nsplit, rpw, kw):
+    """Tiled weights give the row-major kernel's sums bit for bit (same k-slots)."""
+    M = 16
+    print(f"[gemm tiled] N={N} K={K} nsplit={nsplit} rpw={rpw} kw={kw}", flush=True)
+    x, w, out, used = _run(device, M, N, K, nsplit, rpw, seed=N * 3 + K, kw=kw)
+    t = _tile(device, w)
+    out_t = torch.full_like(out, float("nan"))
+    _lib.call("dflash_gemm_bf16_tiled", x.data_ptr(), K, t.data_ptr(), out_t.data_ptr(), N, M, N, K,
+              nsplit, rpw, kw, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    assert torch.equal(out_t, out)
+
+
+@pytest.mark.parametrize("M,N,K,nsplit,kw", [(16, 12352, 2560, 1, 4), (16, 5120, 2560, 1, 1),
+                                              (37, 1008, 640, 1, 4), (64, 784, 1024, 3, 1),
+                                              (1, 48, 64, 1, 4)])
+def test_gemm_tiled_64_rows_per_wave(device, M, N, K, nsplit, kw):
+    """rows_per_wave 64 (tiled only) against the fp32 reference, M and N tails."""
+    g = torch.Generator(device=device).manual_seed(M + N)
+    x = torch.randn(M, K, generator=g, device=device).bfloat16()
+    w = (0.02 * torch.randn(N, K, generator=g, device=device)).bfloat16()
+    t = _tile(device, w)
+    lib = _lib.load()
+    used = int(lib.dflash_gemm_splits(K, nsplit))
+    out = (torch.full((used, M, N), float("nan"), device=device) if nsplit > 1 else
+           torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=device))
+    _lib.call("dflash_gemm_bf16_tiled", x.data_ptr(), K, t.data_ptr(), out.data_ptr(), N, M, N, K,
+              nsplit, 64, kw, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    ref = _ref(x, w)
+    scale = ref.pow(2).mean().sqrt().item()
+    if nsplit > 1:
+        assert torch.isfinite(out).all()
+        assert (out.sum(0) - ref).abs().max().item() <= 1e-4 * scale + 1e-5
+    else:
+        assert ((out.float() - ref).abs() - (2 ** -8) * ref.abs()).max().item() <= 1e-3 * scale
+
+
+@pytest.mark.parametrize("M,I,K,kw", [(16, 9216, 2560, 4), (37, 64, 128, 1)])
+def test_gemm_swiglu_tiled_bit_identical(device, M, I, K, kw):
+    g = torch.Generator(device=device).manual_seed(I + M)
+    x = torch.randn(M, K, generator=g, device=device).bfloat16()
+    w = (0.02 * torch.randn(2 * I, K, generator=g, device=device)).bfloat16()
+    pairs = w.view(2, I // 16, 16, K).transpose(0, 1).reshape(2 * I, K).contiguous()
+    out = torch.full((M, I), float("nan"), dtype=torch.bfloat16, device=device)
+    _lib.call("dflash_gemm_bf16_swiglu", x.data_ptr(), K, pairs.data_ptr(), K, out.data_ptr(), I, M,
+              2 * I, K, kw, _lib.stream_handle(device))
+    t = _tile(device, pairs)
+    out_t = torch.full_like(out, float("nan"))
+    _lib.call("dflash_gemm_bf16_swiglu_tiled", x.data_ptr(), K, t.data_ptr(), out_t.data_ptr(), I,
+              M, 2 * I, K, kw, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    assert torch.equal(out_t, out)
+
+
+def test_gemm_tiled_rejects_bad_arguments(device):
+    lib = _lib.load()
+    assert lib.dflash_weight_tile_bytes(40, 64) == 0          # N % 16
+    assert lib.dflash_weight_tile_bf16(None, 64, None, 40, 64, None) == -2
+    assert lib.dflash_gemm_bf16_tiled(None, 64, None, None, 64, 16, 40, 64, 1, 32, 4, None) == -2
+    assert lib.dflash_gemm_bf16_tiled(None, 64, None, None, 64, 16, 48, 64, 1, 48, 4, None) == -3

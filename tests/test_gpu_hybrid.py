@@ -68,8 +68,8 @@ def _initial_state(cfg, B, lens, seed):
     return dict(lens=list(lens), conv=conv, rec=rec, k=k, v=v)
 
 
-def _runner(cfg, w, st, B, T, Smax, device):
-    r = HybridVerifyRunner(cfg, w, B, T, Smax, device)
+def _runner(cfg, w, st, B, T, Smax, device, weight_layout="tiled"):
+    r = HybridVerifyRunner(cfg, w, B, T, Smax, device, weight_layout=weight_layout)
     r.set_state(st["lens"], [c.to(device) for c in st["conv"]], [s.to(device) for s in st["rec"]],
                 [k.to(device) for k in st["k"]], [v.to(device) for v in st["v"]])
     return r
@@ -109,6 +109,27 @@ def test_small_hybrid_step_matches_oracle(device):
     clear = (srt[..., -1] - srt[..., -2]) > 0.1 * np.max(np.abs(ref["logits"]))
     assert np.array_equal(post[clear], ref["posterior"][clear])
     print(f"  posterior equal on {int(clear.sum())} clear-margin rows of {B * T}", flush=True)
+
+
+def test_tiled_and_rowmajor_weights_give_the_same_step(device):
+    """The fragment-tiled weight layout changes how the GEMMs stream, not what
+    they sum: the whole step's hidden states, tape and accept are bit-identical
+    to the row-major run."""
+    cfg, B, T, Smax = SMALL, 2, 16, 256
+    w = HybridWeights.random(cfg, device, seed=21, on_device=False)
+    st = _initial_state(cfg, B, [33, 90], seed=22)
+    tokens = torch.randint(0, cfg.vocab_size, (B, T), generator=torch.Generator().manual_seed(23),
+                           dtype=torch.int32)
+    outs = []
+    for layout in ("tiled", "rowmajor"):
+        print(f"[hybrid layout] {layout}", flush=True)
+        run = _runner(cfg, w, st, B, T, Smax, device, weight_layout=layout)
+        run.tokens.copy_(tokens)
+        run.forward_accept()
+        torch.cuda.synchronize()
+        outs.append((run.xn.clone(), run.tape[0].clone(), run.posterior.clone(), run.matched.clone()))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
 
 
 def _force_step(run, keep_minus_one):
