@@ -70,68 +70,79 @@ __device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); 
 // rsqrt(mean(h^2) + eps) * w), fp32 arithmetic.  The branch r is either bf16
 // [M, H] or (PART) the fp32 split-K partial sums of the projection that
 // produced it, rp[nsplit][M][H], rounded to bf16 after the sum (where the
-// projection's own output would be rounded).  One 256-thread workgroup per
-// row (verify steps have only B*T rows): thread t owns the 8-element chunks
-// t and t + 256 (H <= 4096), keeps them in registers, and issues all of its
-// loads (x, and every split of r) before using any.
-template <bool PART>
-__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const uint16_t* x, const uint16_t* r,
-                                                          const float* rp, int nsplit,
-                                                          const uint16_t* w, uint16_t* h_out,
-                                                          uint16_t* y, int M, int H, float eps) {
-  __shared__ float wsum[4];
+// projection's own output would be rounded).  One workgroup per row (verify
+// steps have only B*T rows) of one thread per 8-element chunk (H / 8 threads,
+// up to 1024): every thread issues all of its loads (x, and every split of
+// r: NS of them, a compile-time count for the common split factors) before
+// using any, so a row costs one memory round trip.  With tok != nullptr, x
+// is the embedding table and row m reads table row tok[m] (clamped to
+// [0, vocab)), stored to h_out as the residual stream's start.
+template <bool PART, int NS>
+__global__ __launch_bounds__(1024) void add_rmsnorm_kernel(const uint16_t* x, const int32_t* tok,
+                                                           int vocab, const uint16_t* r,
+                                                           const float* rp, int nsplit,
+                                                           const uint16_t* w, uint16_t* h_out,
+                                                           uint16_t* y, int M, int H, float eps) {
+  __shared__ float wsum[16];
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
-  const int nch = H >> 3;
-  const uint16_t* xr = x + (int64_t)row * H;
-  const uint16_t* rr = r != nullptr ? r + (int64_t)row * H : nullptr;
-  const bool has_r = PART || rr != nullptr;
-  float v[2][8];
-  float ss = 0.f;
+  const int ch = tid;
+  const bool live = ch < (H >> 3);
+  const int chc = live ? ch : 0;  // idle threads load chunk 0 and drop it
+  const int64_t xrow = tok != nullptr ? (int64_t)min(max(tok[row], 0), vocab - 1) : row;
+  float v[8];
+  unpack8(ld16(x + xrow * H + chc * 8), v);
+  if (PART) {
+    const float* src = rp + (int64_t)row * H + chc * 8;
+    const int64_t sstride = (int64_t)M * H;
+    f32x4 p0[NS > 0 ? NS : 1], p1[NS > 0 ? NS : 1];
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    if (NS > 0) {
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int ch = tid + 256 * c;
-    if (ch < nch) {
-      unpack8(ld16(xr + ch * 8), v[c]);
-      if (PART) {
-        f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-        const float* src = rp + (int64_t)row * H + ch * 8;
-        const int64_t sstride = (int64_t)M * H;
-#pragma unroll 8
-        for (int k = 0; k < nsplit; ++k) {
-          s0 += *reinterpret_cast<const f32x4*>(src + k * sstride);
-          s1 += *reinterpret_cast<const f32x4*>(src + k * sstride + 4);
-        }
-        const float rv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[c][e] = bf16_round(v[c][e] + bf16_round(rv[e]));
-      } else if (rr != nullptr) {
-        float rv[8];
-        unpack8(ld16(rr + ch * 8), rv);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[c][e] = bf16_round(v[c][e] + rv[e]);
+      for (int k = 0; k < NS; ++k) {
+        p0[k] = *reinterpret_cast<const f32x4*>(src + k * sstride);
+        p1[k] = *reinterpret_cast<const f32x4*>(src + k * sstride + 4);
       }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) ss = fmaf(v[c][e], v[c][e], ss);
+      for (int k = 0; k < NS; ++k) {
+        s0 += p0[k];
+        s1 += p1[k];
+      }
+    } else {
+#pragma unroll 8
+      for (int k = 0; k < nsplit; ++k) {
+        s0 += *reinterpret_cast<const f32x4*>(src + k * sstride);
+        s1 += *reinterpret_cast<const f32x4*>(src + k * sstride + 4);
+      }
     }
+    const float rv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = bf16_round(v[e] + bf16_round(rv[e]));
+  } else if (r != nullptr) {
+    float rv[8];
+    unpack8(ld16(r + (int64_t)row * H + chc * 8), rv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = bf16_round(v[e] + rv[e]);
+  }
+  float ss = 0.f;
+  if (live) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
   }
   ss = wave_sum(ss);
   if ((tid & 63) == 0) wsum[tid >> 6] = ss;
   __syncthreads();
-  ss = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
-  const float inv = 1.f / sqrtf(ss / (float)H + eps);
+  float tot = 0.f;
+  for (int i = 0; i < (int)(blockDim.x >> 6); ++i) tot += wsum[i];
+  const float inv = 1.f / sqrtf(tot / (float)H + eps);
+  if (live) {
+    if ((PART || r != nullptr || tok != nullptr) && h_out != nullptr)
+      *reinterpret_cast<u32x4*>(h_out + (int64_t)row * H + ch * 8) = pack8(v);
+    float wv[8], o[8];
+    unpack8(ld16(w + ch * 8), wv);
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int ch = tid + 256 * c;
-    if (ch < nch) {
-      if (has_r && h_out != nullptr)
-        *reinterpret_cast<u32x4*>(h_out + (int64_t)row * H + ch * 8) = pack8(v[c]);
-      float wv[8], o[8];
-      unpack8(ld16(w + ch * 8), wv);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = v[c][e] * inv * wv[e];
-      *reinterpret_cast<u32x4*>(y + (int64_t)row * H + ch * 8) = pack8(o);
-    }
+    for (int e = 0; e < 8; ++e) o[e] = v[e] * inv * wv[e];
+    *reinterpret_cast<u32x4*>(y + (int64_t)row * H + ch * 8) = pack8(o);
   }
 }
 
@@ -468,9 +479,10 @@ using namespace dflash;
 
 namespace dflash {
 namespace {
-int launch_add_rmsnorm(const void* x, const void* r, const float* rp, int nsplit, const void* weight,
-                       void* h_out, void* y, int M, int H, float eps, void* stream) {
-  if (M < 0 || H <= 0 || H % 8 != 0 || H > 512 * 8 || nsplit < 0) return DFLASH_ERR_SHAPE;
+int launch_add_rmsnorm(const void* x, const int32_t* tok, int vocab, const void* r, const float* rp,
+                       int nsplit, const void* weight, void* h_out, void* y, int M, int H,
+                       float eps, void* stream) {
+  if (M < 0 || H <= 0 || H % 8 != 0 || H > 1024 * 8 || nsplit < 0) return DFLASH_ERR_SHAPE;
   if (M == 0) return DFLASH_OK;
   if (x == nullptr || weight == nullptr || y == nullptr) return DFLASH_ERR_NULL;
   if (((uintptr_t)x & 15) || ((uintptr_t)r & 15) || ((uintptr_t)rp & 15) ||
@@ -478,17 +490,30 @@ int launch_add_rmsnorm(const void* x, const void* r, const float* rp, int nsplit
     return DFLASH_ERR_ALIGN;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)M);
+  const dim3 block((unsigned)ceil_div(H / 8, 64) * 64);
   const auto* xp = static_cast<const uint16_t*>(x);
   const auto* rpb = static_cast<const uint16_t*>(r);
   const auto* wp = static_cast<const uint16_t*>(weight);
   auto* hp = static_cast<uint16_t*>(h_out);
   auto* yp = static_cast<uint16_t*>(y);
-  if (rp != nullptr)
-    hipLaunchKernelGGL(add_rmsnorm_kernel<true>, grid, dim3(256), 0, s, xp, nullptr, rp, nsplit, wp,
-                       hp, yp, M, H, eps);
-  else
-    hipLaunchKernelGGL(add_rmsnorm_kernel<false>, grid, dim3(256), 0, s, xp, rpb, nullptr, 0, wp,
-                       hp, yp, M, H, eps);
+  if (rp != nullptr) {
+    switch (nsplit) {
+#define DFLASH_ARN(ns)                                                                           \
+  case ns:                                                                                       \
+    hipLaunchKernelGGL((add_rmsnorm_kernel<true, ns>), grid, block, 0, s, xp, tok, vocab, nullptr, \
+                       rp, nsplit, wp, hp, yp, M, H, eps);                                       \
+    break;
+      DFLASH_ARN(1) DFLASH_ARN(2) DFLASH_ARN(3) DFLASH_ARN(4) DFLASH_ARN(5) DFLASH_ARN(6)
+      DFLASH_ARN(7) DFLASH_ARN(8)
+#undef DFLASH_ARN
+      default:
+        hipLaunchKernelGGL((add_rmsnorm_kernel<true, 0>), grid, block, 0, s, xp, tok, vocab, nullptr,
+                           rp, nsplit, wp, hp, yp, M, H, eps);
+    }
+  } else {
+    hipLaunchKernelGGL((add_rmsnorm_kernel<false, 0>), grid, block, 0, s, xp, tok, vocab, rpb,
+                       nullptr, 0, wp, hp, yp, M, H, eps);
+  }
   return to_status(hipGetLastError());
 }
 }  // namespace
@@ -496,14 +521,24 @@ int launch_add_rmsnorm(const void* x, const void* r, const float* rp, int nsplit
 
 extern "C" int dflash_add_rmsnorm(const void* x, const void* r, const void* weight, void* h_out,
                                   void* y, int M, int H, float eps, void* stream) {
-  return launch_add_rmsnorm(x, r, nullptr, 0, weight, h_out, y, M, H, eps, stream);
+  return launch_add_rmsnorm(x, nullptr, 0, r, nullptr, 0, weight, h_out, y, M, H, eps, stream);
 }
 
 extern "C" int dflash_add_rmsnorm_splitk(const void* x, const float* r_partials, int nsplit,
                                          const void* weight, void* h_out, void* y, int M, int H,
                                          float eps, void* stream) {
   if (r_partials == nullptr || nsplit < 1) return DFLASH_ERR_NULL;
-  return launch_add_rmsnorm(x, nullptr, r_partials, nsplit, weight, h_out, y, M, H, eps, stream);
+  return launch_add_rmsnorm(x, nullptr, 0, nullptr, r_partials, nsplit, weight, h_out, y, M, H, eps,
+                            stream);
+}
+
+extern "C" int dflash_embed_rmsnorm(const void* table, const int32_t* tokens, int vocab,
+                                    const void* weight, void* h_out, void* y, int M, int H,
+                                    float eps, void* stream) {
+  if (vocab <= 0) return DFLASH_ERR_SHAPE;
+  if (tokens == nullptr || h_out == nullptr) return DFLASH_ERR_NULL;
+  return launch_add_rmsnorm(table, tokens, vocab, nullptr, nullptr, 0, weight, h_out, y, M, H, eps,
+                            stream);
 }
 
 extern "C" int dflash_swiglu(const void* gate_up, void* out, int M, int I, void* stream) {

@@ -50,6 +50,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dflash_add_rmsnorm": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, ctypes.c_float, _VP]),
     "dflash_add_rmsnorm_splitk": (
         _I, [_VP, _VP, _I, _VP, _VP, _VP, _I, _I, ctypes.c_float, _VP]),
+    "dflash_embed_rmsnorm": (_I, [_VP, _VP, _I, _VP, _VP, _VP, _I, _I, ctypes.c_float, _VP]),
     "dflash_gemm_bf16": (_I, [_VP, _I64, _VP, _I64, _VP, _I64, _I, _I, _I, _I, _I, _I, _VP]),
     "dflash_gemm_splits": (_I, [_I, _I]),
     "dflash_gemm_bf16_swiglu": (_I, [_VP, _I64, _VP, _I64, _VP, _I64, _I, _I, _I, _I, _VP]),

@@ -414,9 +414,9 @@ class HybridVerifyRunner:
         call = _lib.call
         M, H, I = B * T, cfg.hidden_size, cfg.intermediate_size
         eps = float(cfg.rms_norm_eps)
-        torch.index_select(self.w.embed, 0, self.tokens.view(-1), out=self.h)
-        call("dflash_add_rmsnorm", self.h.data_ptr(), None, self.w.layers[0]["ln_in"].data_ptr(),
-             self.h.data_ptr(), self.xn.data_ptr(), M, H, eps, stream)
+        call("dflash_embed_rmsnorm", self.w.embed.data_ptr(), self.tokens.data_ptr(),
+             cfg.vocab_size, self.w.layers[0]["ln_in"].data_ptr(), self.h.data_ptr(),
+             self.xn.data_ptr(), M, H, eps, stream)
         gi = ai = 0
         for i in range(cfg.num_hidden_layers):
             lw = self.w.layers[i]

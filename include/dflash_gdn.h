@@ -327,7 +327,7 @@ int dflash_conv_rollback(const void* const* conv_in, const void* const* qkv,
  *   h = bf16(x + r) -> h_out;  y = bf16(h * rsqrt(mean(h^2) + eps) * weight)
  * r may be NULL (then h = x and h_out is not written).  x, r, h_out, y are
  * bf16 [M, H] contiguous, weight bf16 [H]; h_out may alias x.  fp32
- * arithmetic.  Supported: H % 8 == 0, H <= 4096.
+ * arithmetic.  Supported: H % 8 == 0, H <= 8192.
  */
 int dflash_add_rmsnorm(const void* x, const void* r, const void* weight,
                        void* h_out, void* y, int M, int H, float eps,
@@ -342,6 +342,18 @@ int dflash_add_rmsnorm(const void* x, const void* r, const void* weight,
 int dflash_add_rmsnorm_splitk(const void* x, const float* r_partials,
                               int nsplit, const void* weight, void* h_out,
                               void* y, int M, int H, float eps, void* stream);
+
+/*
+ * The step's first norm with the embedding lookup folded in
+ * (Qwen3_5TextModel: embed_tokens(inputs) then layer 0's input_layernorm,
+ * custom_qwen35_model.py:866-869, :841):
+ *   h_out[m] = table[tokens[m]],  y = bf16(h * rsqrt(mean(h^2) + eps) * weight).
+ * table bf16 [vocab, H], tokens int32 [M] on the device (ids outside
+ * [0, vocab) are clamped: the kernel cannot raise, and must stay in bounds).
+ */
+int dflash_embed_rmsnorm(const void* table, const int32_t* tokens, int vocab,
+                         const void* weight, void* h_out, void* y, int M,
+                         int H, float eps, void* stream);
 
 /*
  * Verify-sized projection GEMM: out[M, N] = x[M, K] . w[N, K]^T, bf16 in,

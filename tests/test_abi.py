@@ -38,7 +38,7 @@ def test_header_declares_expected_entry_points():
         "dflash_gdn_chunked_prefill_workspace_bytes", "dflash_gdn_chunked_prefill",
         "dflash_add_rmsnorm", "dflash_swiglu", "dflash_attn_prep",
         "dflash_attn_verify_workspace_bytes", "dflash_attn_verify", "dflash_commit_accept",
-        "dflash_add_rmsnorm_splitk", "dflash_gemm_bf16", "dflash_gemm_splits",
+        "dflash_add_rmsnorm_splitk", "dflash_embed_rmsnorm", "dflash_gemm_bf16", "dflash_gemm_splits",
         "dflash_splitk_reduce", "dflash_gemm_bf16_swiglu", "dflash_weight_tile_bytes",
         "dflash_weight_tile_bf16", "dflash_gemm_bf16_tiled", "dflash_gemm_bf16_swiglu_tiled",
     ])

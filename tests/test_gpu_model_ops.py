@@ -168,3 +168,66 @@ def test_commit_accept(device):
     torch.cuda.synchronize()
     assert keep.cpu().tolist() == [1, 4, 16, 16, 1]
     assert lens.cpu().tolist() == [11, 14, 26, 26, 11]
+
+
+@pytest.mark.parametrize("nsplit", [1, 2, 3, 5, 8, 11])
+def test_add_rmsnorm_splitk_every_split_count(device, nsplit):
+    """The compile-time split counts (1..8) and the generic loop (11) sum the
+    partials in split order, as dflash_splitk_reduce does: bit-identical to
+    the bf16-branch kernel fed that reduce."""
+    M, H = 16, 2560
+    g = torch.Generator(device=device).manual_seed(nsplit)
+    part = torch.randn(nsplit, M, H, generator=g, device=device)
+    x = torch.randn(M, H, generator=g, device=device).bfloat16()
+    w = (1 + 0.1 * torch.randn(H, generator=g, device=device)).bfloat16()
+    r = torch.empty(M, H, dtype=torch.bfloat16, device=device)
+    st = _lib.stream_handle(device)
+    _lib.call("dflash_splitk_reduce", part.data_ptr(), nsplit, M, H, r.data_ptr(), H, st)
+    h1, y1 = x.clone(), torch.empty_like(x)
+    h2, y2 = x.clone(), torch.empty_like(x)
+    _lib.call("dflash_add_rmsnorm_splitk", h1.data_ptr(), part.data_ptr(), nsplit, w.data_ptr(),
+              h1.data_ptr(), y1.data_ptr(), M, H, 1e-6, st)
+    _lib.call("dflash_add_rmsnorm", h2.data_ptr(), r.data_ptr(), w.data_ptr(), h2.data_ptr(),
+              y2.data_ptr(), M, H, 1e-6, st)
+    torch.cuda.synchronize()
+    assert torch.equal(h1, h2) and torch.equal(y1, y2)
+
+
+def test_add_rmsnorm_widest_row(device):
+    M, H = 4, 8192
+    gen = torch.Generator().manual_seed(81)
+    x = torch.randn(M, H, generator=gen).bfloat16()
+    r = torch.randn(M, H, generator=gen).bfloat16()
+    w = (1 + 0.1 * torch.randn(H, generator=gen)).bfloat16()
+    xd, rd, wd = x.to(device), r.to(device), w.to(device)
+    h = torch.empty_like(xd)
+    y = torch.empty_like(xd)
+    _lib.call("dflash_add_rmsnorm", xd.data_ptr(), rd.data_ptr(), wd.data_ptr(), h.data_ptr(),
+              y.data_ptr(), M, H, 1e-6, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    h_ref, y_ref = ho.add_rmsnorm(_np(x), _np(r), _np(w), 1e-6)
+    assert _within_ulps(_np(h), h_ref, rel=2.0 ** -8) <= 0
+    assert _within_ulps(_np(y), y_ref) <= 0
+    lib = _lib.load()
+    assert lib.dflash_add_rmsnorm(None, None, None, None, None, 1, 8200, 1e-6, None) == -2
+
+
+def test_embed_rmsnorm(device):
+    """Embedding lookup folded into the first norm: h = table[tokens] exactly,
+    y as the oracle's RMSNorm of those rows; ids out of range clamp."""
+    V, H = 1000, 2560
+    gen = torch.Generator().manual_seed(5)
+    table = (0.02 * torch.randn(V, H, generator=gen)).bfloat16()
+    w = (1 + 0.1 * torch.randn(H, generator=gen)).bfloat16()
+    tokens = torch.tensor([0, 999, 17, 123, -5, 1000, 4242, 500], dtype=torch.int32)
+    td, wd, tokd = table.to(device), w.to(device), tokens.to(device)
+    M = tokens.numel()
+    h = torch.empty(M, H, dtype=torch.bfloat16, device=device)
+    y = torch.empty_like(h)
+    _lib.call("dflash_embed_rmsnorm", td.data_ptr(), tokd.data_ptr(), V, wd.data_ptr(), h.data_ptr(),
+              y.data_ptr(), M, H, 1e-6, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    ids = tokens.clamp(0, V - 1).long()
+    assert torch.equal(h.cpu(), table[ids])
+    _, y_ref = ho.add_rmsnorm(_np(table[ids]), None, _np(w), 1e-6)
+    assert _within_ulps(_np(y), y_ref) <= 0
