@@ -17,11 +17,12 @@
 //     holds elements 16g .. 16g+15 of the 64-wide step for both operands, so
 //     the contraction is exact whatever order the hardware gives the k-slots.
 //   - Tiled weights (dflash_weight_tile_bf16, once at load time): the weight
-//     stored as those A fragments, [N/16 row tiles][K/64 k-steps][2 halves]
+//     stored as those A fragments, [K/64 k-steps][N/16 row tiles][2 halves]
 //     [64 lanes][8], so every fragment is one contiguous 1 KB load straight
-//     into MFMA registers (no LDS step) and a workgroup's rows are one
-//     contiguous stretch of memory.  Same k-slots, so the same sums, bit for
-//     bit, as the row-major path.
+//     into MFMA registers (no LDS step), and the workgroups in flight, which
+//     walk their k-ranges in step, read within a narrow window of memory (a
+//     few pages) rather than each in its own region.  Same k-slots, so the
+//     same sums, bit for bit, as the row-major path.
 //   - Epilogue, nsplit == 1 requested: bf16 (round to nearest even) into
 //     out, or (dflash_gemm_bf16_swiglu) the MLP gating silu(gate) * up of a
 //     weight whose 32-row blocks are 16 gate rows then the 16 matching up
@@ -94,11 +95,11 @@ __global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams
   const int nks = min(part_len, split_begin + split_len - ks_begin);
 
   const uint16_t* wrow[2 * VT];
-  if (TILED) {  // fragment (row tile, k-step, half): 1 KB at ((rt * nks_all + ks) * 2 + h) KB
+  if (TILED) {  // fragment (k-step, row tile, half): 1 KB at ((ks * N/16 + rt) * 2 + h) KB
 #pragma unroll
     for (int vt = 0; vt < VT; ++vt) {
       const int rt = min(nwave / 16 + vt, p.N / 16 - 1);  // tail tiles re-read the last
-      wrow[2 * vt] = p.w + ((int64_t)rt * nks_all + ks_begin) * (2 * 512) + lane * 8;
+      wrow[2 * vt] = p.w + ((int64_t)ks_begin * (p.N / 16) + rt) * (2 * 512) + lane * 8;
       wrow[2 * vt + 1] = wrow[2 * vt] + 512;
     }
   } else {
@@ -115,7 +116,7 @@ __global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams
 
   auto load = [&](GStage<MT, VT>& st, int ks) {
     const int off = ks * kGKStep;
-    const int woff = TILED ? ks * 1024 : off;
+    const int64_t woff = TILED ? (int64_t)ks * (p.N / 16) * 1024 : off;
 #pragma unroll
     for (int i = 0; i < 2 * VT; ++i) st.a[i] = *reinterpret_cast<const u32x4*>(wrow[i] + woff);
 #pragma unroll
@@ -265,7 +266,7 @@ hipError_t launch_m(const GemmParams& p, hipStream_t s) {
        : mt == 3 ? launch_gemm<3, VT, KW, TILED>(p, s) : launch_gemm<4, VT, KW, TILED>(p, s);
 }
 
-// dst = src stored as A fragments: dst[((rt * (K/64) + ks) * 2 + h) * 512 + lane * 8 + e]
+// dst = src stored as A fragments: dst[((ks * (N/16) + rt) * 2 + h) * 512 + lane * 8 + e]
 //   = src[16 rt + lane % 16][64 ks + 16 (lane / 16) + 8 h + e].
 __global__ __launch_bounds__(256) void weight_tile_kernel(const uint16_t* src, int64_t ss,
                                                           uint16_t* dst, int N, int K) {
@@ -273,11 +274,11 @@ __global__ __launch_bounds__(256) void weight_tile_kernel(const uint16_t* src, i
   const int64_t nfrag = (int64_t)(N / 16) * nks * 2 * 64;  // 16-byte pieces
   for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < nfrag; e += (int64_t)gridDim.x * 256) {
     const int lane = (int)(e & 63);
-    const int64_t f = e >> 6;  // (rt * nks + ks) * 2 + h
+    const int64_t f = e >> 6;  // (ks * N/16 + rt) * 2 + h
     const int h = (int)(f & 1);
     const int64_t tk = f >> 1;
-    const int ks = (int)(tk % nks);
-    const int rt = (int)(tk / nks);
+    const int rt = (int)(tk % (N / 16));
+    const int ks = (int)(tk / (N / 16));
     const uint16_t* s = src + (int64_t)(16 * rt + (lane & 15)) * ss + 64 * ks + 16 * (lane >> 4) + 8 * h;
     *reinterpret_cast<u32x4*>(dst + e * 8) = *reinterpret_cast<const u32x4*>(s);
   }

@@ -221,7 +221,7 @@ class HybridVerifyRunner:
     GEMM_PLAN = {"w_in": (1, 32, 4), "w_out": (8, 16, 4), "w_qkv": (1, 32, 4),
                  "w_o": (8, 32, 4), "w_gu": (1, 32, 4), "w_down": (8, 32, 4)}
     # the same for fragment-tiled weights (rows_per_wave 64 exists only there)
-    TILED_PLAN = {"w_in": (1, 64, 4), "w_out": (8, 16, 4), "w_qkv": (1, 32, 4),
+    TILED_PLAN = {"w_in": (1, 64, 4), "w_out": (8, 32, 4), "w_qkv": (1, 32, 4),
                   "w_o": (8, 16, 4), "w_gu": (1, 32, 4), "w_down": (8, 32, 4)}
 
     def _build_gemms(self):

@@ -397,10 +397,10 @@ int dflash_gemm_bf16_swiglu(const void* x, int64_t x_row_stride,
  * The same projections with the weight stored once, at load time, as MFMA
  * fragments (the nn.Linear weight [N, K] of custom_qwen35_model.py:726-736
  * and mlx-lm's attention / MLP Linears, re-laid out for streaming):
- *   w_tiled[((rt * (K/64) + ks) * 2 + h) * 512 + l * 8 + e]
+ *   w_tiled[((ks * (N/16) + rt) * 2 + h) * 512 + l * 8 + e]
  *     = w[16 rt + l % 16][64 ks + 16 (l / 16) + 8 h + e],
  * so every 64-lane load is 1 KB of contiguous memory going straight into
- * matrix-core registers.  dflash_weight_tile_bf16 builds it (N % 16 == 0,
+ * matrix-core registers, and workgroups in flight read close together.  dflash_weight_tile_bf16 builds it (N % 16 == 0,
  * K % 64 == 0; dflash_weight_tile_bytes(N, K) bytes, 16-byte aligned); the
  * _tiled GEMMs take it in place of (w, w_row_stride) and return the same sums
  * bit for bit as their row-major counterparts.  rows_per_wave may also be 64

@@ -149,7 +149,7 @@ def test_weight_tile_layout(device):
         for ks in range(nks):
             for h in range(2):
                 for lane in range(64):
-                    base = ((rt * nks + ks) * 2 + h) * 512 + lane * 8
+                    base = ((ks * (N // 16) + rt) * 2 + h) * 512 + lane * 8
                     row = 16 * rt + lane % 16
                     col = 64 * ks + 16 * (lane // 16) + 8 * h
                     assert (t[base:base + 8] == wn[row, col:col + 8]).all(), (rt, ks, h, lane)
