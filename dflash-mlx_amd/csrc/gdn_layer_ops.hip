@@ -20,25 +20,11 @@
 
 #include "dflash_gdn.h"
 #include "device_common.h"
+#include "gdn_prologue_math.h"
 #include "host_common.h"
 
 namespace dflash {
 namespace {
-
-constexpr int kMaxConvTaps = 8;
-
-__device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); }
-__device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
-// softplus(x) = log(1 + exp(x)), evaluated without overflow.
-__device__ __forceinline__ float softplus(float x) {
-  return x > 20.f ? x : log1pf(__expf(x));
-}
-
-__device__ __forceinline__ float wave_sum(float x) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, 64);
-  return x;
-}
 
 struct ProParams {
   const uint16_t* qkv;  // [B, T, C] bf16, C contiguous
@@ -84,11 +70,10 @@ __device__ __forceinline__ void conv_silu(const ProParams& p, int b, int t, int 
       if (j < p.K) w[i][j] = ldbf(p.conv_w + (int64_t)(c0 + i) * p.K + j);
 #pragma unroll
   for (int i = 0; i < NC; ++i) {
-    float acc = 0.f;
+    float xi[kMaxConvTaps];
 #pragma unroll
-    for (int j = 0; j < kMaxConvTaps; ++j)
-      if (j < p.K) acc = fmaf(w[i][j], x[j][i], acc);
-    out[i] = silu(acc);
+    for (int j = 0; j < kMaxConvTaps; ++j) xi[j] = x[j][i];
+    out[i] = pro_conv_silu(w[i], xi, p.K);
   }
 }
 
@@ -116,8 +101,8 @@ __global__ __launch_bounds__(256) void gdn_prologue_kernel(const ProParams p) {
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < PER; ++i) ss = fmaf(vals[i], vals[i], ss);
-    ss = wave_sum(ss);
-    const float r = rsqrtf(ss / (float)p.Dk + p.eps) * (unit < p.Hk ? p.q_scale : p.k_scale);
+    ss = pro_wave_sum(ss);
+    const float r = pro_head_scale(ss, p.Dk, p.eps, unit < p.Hk ? p.q_scale : p.k_scale);
 #pragma unroll
     for (int i = 0; i < PER; ++i) act[c0 + i] = f32_to_bf16_rne(vals[i] * r);
   } else if (unit < n_qk + n_v) {
@@ -139,9 +124,8 @@ __global__ __launch_bounds__(256) void gdn_prologue_kernel(const ProParams p) {
     for (int h = lane; h < p.Hv; h += 64) {
       const float av = ldbf(p.a + b * p.a_sb + (int64_t)t * p.a_st + h);
       const float bv = ldbf(p.b + b * p.b_sb + (int64_t)t * p.b_st + h);
-      const float gv = __expf(-__expf(p.A_log[h]) * softplus(av + ldbf(p.dt_bias + h)));
-      p.g[(int64_t)bt * p.Hv + h] = gv;
-      p.beta[(int64_t)bt * p.Hv + h] = sigmoid(bv);
+      p.g[(int64_t)bt * p.Hv + h] = pro_decay(p.A_log[h], av, ldbf(p.dt_bias + h));
+      p.beta[(int64_t)bt * p.Hv + h] = pro_sigmoid(bv);
     }
   } else {
     // New conv window = the last K-1 rows of concat(conv_state, qkv): row r
@@ -196,11 +180,11 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const NormParams p) 
     xv[i] = ldbf(x + i * 64 + lane);
     ss = fmaf(xv[i], xv[i], ss);
   }
-  ss = wave_sum(ss);
+  ss = pro_wave_sum(ss);
   const float r = rsqrtf(ss / (float)p.D + p.eps);
   for (int i = 0; i < per; ++i) {
     const int c = i * 64 + lane;
-    p.y[(int64_t)row * p.D + c] = f32_to_bf16_rne(xv[i] * r * ldbf(p.w + c) * silu(ldbf(z + c)));
+    p.y[(int64_t)row * p.D + c] = f32_to_bf16_rne(xv[i] * r * ldbf(p.w + c) * pro_silu(ldbf(z + c)));
   }
 }
 

@@ -21,8 +21,11 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "dflash_gdn.h"
 #include "device_common.h"
+#include "gdn_prologue_math.h"
 #include "host_common.h"
 
 namespace dflash {
@@ -62,6 +65,33 @@ struct ScanParams {
   // that XCD walks the contiguous item range [x*items/8, (x+1)*items/8), which
   // keeps all row blocks of a head (and its k/q/v) in one XCD's L2.
   int xcd_items;  // items / 8, or 0 for the plain grid-stride walk
+  // Prologue on the fly (the PRO kernels): k, q, v, g and beta of an item
+  // are computed from the raw in_proj rows at the item's start instead of
+  // being read.  Channels of a row: q (Hk*Dk) | k (Hk*Dk) | v (Hv*Dv).
+  const uint16_t* pro_qkv;  // [B, T, *] with the strides below
+  int64_t pro_qkv_sb, pro_qkv_st;
+  const uint16_t* pro_conv_state;  // [B, K-1, C]
+  const uint16_t* pro_conv_w;      // [C, K]
+  const uint16_t* pro_a;           // [B, T, Hv] with strides
+  const uint16_t* pro_b;
+  int64_t pro_a_sb, pro_a_st, pro_b_sb, pro_b_st;
+  const float* pro_A_log;         // [Hv]
+  const uint16_t* pro_dt_bias;    // [Hv]
+  int pro_C, pro_K, pro_Hk;
+  float pro_eps, pro_q_scale, pro_k_scale;
+};
+
+// Tokens per block the on-the-fly prologue supports (its LDS is sized for it).
+constexpr int kProMaxT = 32;
+
+// The item's prologue outputs, rounded to bf16 as the standalone prologue
+// stores them.
+template <int DK, int ROWS>
+struct ProLds {
+  uint16_t qk[kProMaxT][2 * DK];  // q | k of the item's key head
+  uint16_t v[kProMaxT][ROWS];     // the item's value rows
+  float g[kProMaxT];
+  float beta[kProMaxT];
 };
 
 template <int VEC>
@@ -124,20 +154,165 @@ __device__ __forceinline__ void store_f32_stream(float* p, const float* f) {
   }
 }
 
+// PER consecutive bf16 channels (PER * 2 bytes, naturally aligned) as fp32.
+template <int PER>
+__device__ __forceinline__ void load_bf16_run(const uint16_t* p, float* f) {
+  if constexpr (PER == 2) {
+    const uint32_t r = *reinterpret_cast<const uint32_t*>(p);
+    f[0] = bf16_lo(r);
+    f[1] = bf16_hi(r);
+  } else if constexpr (PER == 4) {
+    const uint2 r = *reinterpret_cast<const uint2*>(p);
+    f[0] = bf16_lo(r.x); f[1] = bf16_hi(r.x); f[2] = bf16_lo(r.y); f[3] = bf16_hi(r.y);
+  } else {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) f[i] = bf16_bits_to_f32(p[i]);
+  }
+}
+
+// The layer prologue of one item (sequence b, value head hv, row block rb)
+// for its n tokens, into LDS.  Same arithmetic and lane layout as the
+// standalone prologue kernel (gdn_layer_ops.hip), so the values are the ones
+// it would store:
+//   - q and k of key head hk: one wavefront per (head, run of consecutive
+//     tokens), lane l owning channels l*PER .. l*PER+PER-1 with the head's
+//     rms-norm summed by pro_wave_sum; the conv window of the run is loaded
+//     once (rows t .. t+K-2 of the previous token are rows of the next);
+//   - the ROWS value channels of the row block: one (token, channel) per
+//     thread;
+//   - g and beta of head hv: one token per thread.
+// load() issues every load of the phase and consumes none; compute() does
+// the arithmetic and the LDS stores.  KT: conv taps when fixed at compile
+// time, 0 for the run-time K (<= kMaxConvTaps).
+template <int DK, int ROWS, int KT>
+struct ProPhase {
+  static constexpr int PER = DK / 64;
+  static constexpr int NT = KT > 0 ? KT : kMaxConvTaps;  // taps held in registers
+  static constexpr int RUN = kProMaxT / 2;              // tokens per q/k wavefront
+  static constexpr int XR = RUN + NT - 1;               // conv rows of a run
+  static constexpr int VT = (kProMaxT * ROWS + 255) / 256;  // value tasks per thread
+
+  float xq[XR][PER], wq[PER][NT];
+  float xv[VT][NT], wv[VT][NT];
+  float av, bv, A_log, dt_bias;
+  int sel, t_begin, t_end;
+
+  __device__ __forceinline__ int taps(const ScanParams& p) const { return KT > 0 ? KT : p.pro_K; }
+
+  __device__ __forceinline__ void load(const ScanParams& p, int b, int hv, int hk, int rb, int n) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int K = taps(p), K1 = K - 1;
+    const uint16_t* qkv = p.pro_qkv + b * p.pro_qkv_sb;
+    const uint16_t* cst = p.pro_conv_state + (int64_t)b * K1 * p.pro_C;
+    // Row s of concat(conv_state, qkv); s is clamped into [0, n - 1 + K1].
+    auto row_ptr = [&](int s) -> const uint16_t* {
+      s = min(s, n - 1 + K1);
+      return s < K1 ? cst + (int64_t)s * p.pro_C : qkv + (int64_t)(s - K1) * p.pro_qkv_st;
+    };
+    // q / k: wavefronts 0, 2 take q, 1, 3 take k; wavefronts 0, 1 the first
+    // half of the tokens, 2, 3 the second.
+    sel = w & 1;
+    const int half = (n + 1) >> 1;
+    t_begin = (w >> 1) * half;
+    t_end = min(n, t_begin + half);
+    const int c0 = sel * p.pro_Hk * DK + hk * DK + lane * PER;
+#pragma unroll
+    for (int r = 0; r < XR; ++r) load_bf16_run<PER>(row_ptr(t_begin + r) + c0, xq[r]);
+    // Taps j >= K (run-time K) are loaded from tap K-1 (a valid address, no
+    // branch around the load) and never used: the tap sum stops at K.
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        wq[i][j] = bf16_bits_to_f32(p.pro_conv_w[(int64_t)(c0 + i) * K + min(j, K1)]);
+    // Value channels.
+    const int vbase = 2 * p.pro_Hk * DK + hv * p.Dv + rb * ROWS;
+#pragma unroll
+    for (int k = 0; k < VT; ++k) {
+      const int task = min(tid + k * 256, n * ROWS - 1);
+      const int t = task / ROWS, ch = task - t * ROWS;
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        xv[k][j] = bf16_bits_to_f32(row_ptr(t + min(j, K1))[vbase + ch]);
+        wv[k][j] = bf16_bits_to_f32(p.pro_conv_w[(int64_t)(vbase + ch) * K + min(j, K1)]);
+      }
+    }
+    // Decay and write strength.
+    const int tg = min(tid, n - 1);
+    av = bf16_bits_to_f32(p.pro_a[b * p.pro_a_sb + (int64_t)tg * p.pro_a_st + hv]);
+    bv = bf16_bits_to_f32(p.pro_b[b * p.pro_b_sb + (int64_t)tg * p.pro_b_st + hv]);
+    A_log = p.pro_A_log[hv];
+    dt_bias = bf16_bits_to_f32(p.pro_dt_bias[hv]);
+  }
+
+  __device__ __forceinline__ void compute(const ScanParams& p, int n, ProLds<DK, ROWS>& L) {
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int K = taps(p);
+    if (tid < n) {
+      L.g[tid] = pro_decay(A_log, av, dt_bias);
+      L.beta[tid] = pro_sigmoid(bv);
+    }
+#pragma unroll
+    for (int k = 0; k < VT; ++k) {
+      const int task = tid + k * 256;
+      if (task < n * ROWS) {
+        const int t = task / ROWS, ch = task - t * ROWS;
+        L.v[t][ch] = f32_to_bf16_rne(pro_conv_silu_n<NT>(wv[k], xv[k], K));
+      }
+    }
+    // Tokens in chunks of 8 with no branch inside a chunk, so that the eight
+    // cross-lane reductions overlap (rows past the run are clamped copies).
+    const float scale = sel ? p.pro_k_scale : p.pro_q_scale;
+#pragma unroll
+    for (int u0 = 0; u0 < RUN; u0 += 8) {
+      if (t_begin + u0 < t_end) {  // uniform over the wavefront
+        float vals[8][PER], ss[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          ss[u] = 0.f;
+#pragma unroll
+          for (int i = 0; i < PER; ++i) {
+            float xi[NT];
+#pragma unroll
+            for (int j = 0; j < NT; ++j) xi[j] = xq[u0 + u + j][i];
+            vals[u][i] = pro_conv_silu_n<NT>(wq[i], xi, K);
+            ss[u] = fmaf(vals[u][i], vals[u][i], ss[u]);
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) ss[u] = pro_wave_sum(ss[u]);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int t = t_begin + u0 + u;
+          const float r = pro_head_scale(ss[u], DK, p.pro_eps, scale);
+          if (t < t_end) {
+#pragma unroll
+            for (int i = 0; i < PER; ++i)
+              L.qk[t][sel * DK + lane * PER + i] = f32_to_bf16_rne(vals[u][i] * r);
+          }
+        }
+      }
+    }
+  }
+};
+
 // PF: tokens of inputs in flight (register ring).  1 for launches that fill
 // the chip with workgroups; 4 when there are at most as many work items as
 // CUs (one layer of one sequence), where each step otherwise waits on its
 // own loads.
-template <int DK, int R, int PF>
+// PRO: the layer prologue runs at each item's start (pro_phase) and the
+// token loop reads its inputs from LDS.
+template <int DK, int R, int PF, bool PRO = false, int KT = 0>
 __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
   constexpr int VEC = (DK % 64 == 0) ? 4 : 2;
   constexpr int NCH = DK / (16 * VEC);
   constexpr int ROWS_WG = 16 * R;
   typedef BF16Vec<VEC> LD;
+  __shared__ std::conditional_t<PRO, ProLds<DK, ROWS_WG>, int> pro_lds;
 
   const int sub = threadIdx.x & 15;  // lane within the 16-lane row group
   const int gi = threadIdx.x >> 4;   // row group within the workgroup, 0..15
-  const bool has_q = p.q != nullptr;
+  const bool has_q = PRO || p.q != nullptr;
   const bool has_tape = p.tape != nullptr;
 
   int item_begin = blockIdx.x, item_end = p.items, item_step = gridDim.x;
@@ -154,7 +329,7 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
     const int hv = bh - b * p.Hv;
     const int hk = hv / p.rep;
     int n = p.T;
-    if (p.lengths != nullptr) n = min(max(p.lengths[b], 0), p.T);
+    if (!PRO && p.lengths != nullptr) n = min(max(p.lengths[b], 0), p.T);
 
     int row[R];
 #pragma unroll
@@ -165,18 +340,37 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
     const int64_t head_base = (int64_t)bh * p.Dv * DK;
     const float* s_src = p.state_in + head_base;
     bool writeback = false;
-    if (p.sel_tape != nullptr) {
-      const int a = min(max(p.sel_accepted[b % p.sel_period], 0), p.sel_T);
-      if (a >= 1) {
-        s_src = p.sel_tape + (int64_t)(a - 1) * p.tape_tstride + head_base;
-        writeback = true;
-      }
+    int a_sel = 0;
+    ProPhase<DK, ROWS_WG, KT> pro;
+    if constexpr (PRO) {
+      // The accepted count is loaded with no branch around it (from the state
+      // buffer, a valid address, when there is no selection; then unused), and
+      // the prologue's loads go out before it is waited on, ahead of the state
+      // loads that need it.
+      const bool has_sel = p.sel_tape != nullptr;
+      const int32_t* ap = has_sel ? p.sel_accepted + b % max(p.sel_period, 1)
+                                  : reinterpret_cast<const int32_t*>(p.state_in);
+      const int a_raw = *ap;
+      pro.load(p, b, hv, hk, rb, n);
+      a_sel = has_sel ? min(max(a_raw, 0), p.sel_T) : 0;
+    } else {
+      if (p.sel_tape != nullptr) a_sel = min(max(p.sel_accepted[b % p.sel_period], 0), p.sel_T);
+    }
+    if (a_sel >= 1) {
+      s_src = p.sel_tape + (int64_t)(a_sel - 1) * p.tape_tstride + head_base;
+      writeback = true;
     }
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
       for (int c = 0; c < NCH; ++c)
         load_f32<VEC>(s_src + (int64_t)row[r] * DK + c * 16 * VEC + sub * VEC, S[r][c]);
+    if constexpr (PRO) {
+      // The state loads stay in flight while the prologue computes.
+      __syncthreads();  // the previous item's token loop is done with pro_lds
+      pro.compute(p, n, pro_lds);
+      __syncthreads();
+    }
     if (writeback) {
 #pragma unroll
       for (int r = 0; r < R; ++r)
@@ -186,12 +380,12 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
                          S[r][c]);
     }
 
-    const uint16_t* kp = p.k + b * p.k_sb + hk * p.k_sh + sub * VEC;
+    const uint16_t* kp = PRO ? nullptr : p.k + b * p.k_sb + hk * p.k_sh + sub * VEC;
     const uint16_t* qp =
-        has_q ? p.q + b * p.q_sb + hk * p.q_sh + sub * VEC : nullptr;
-    const uint16_t* vp = p.v + b * p.v_sb + hv * p.v_sh;
-    const float* gp = p.g + b * p.g_sb + hv;
-    const float* bp = p.beta + b * p.b_sb + hv;
+        (has_q && !PRO) ? p.q + b * p.q_sb + hk * p.q_sh + sub * VEC : nullptr;
+    const uint16_t* vp = PRO ? nullptr : p.v + b * p.v_sb + hv * p.v_sh;
+    const float* gp = PRO ? nullptr : p.g + b * p.g_sb + hv;
+    const float* bp = PRO ? nullptr : p.beta + b * p.b_sb + hv;
     float* tp = has_tape ? p.tape + head_base + sub * VEC : nullptr;
 
     // Inputs of the next PF tokens stay in flight in a register ring (slot
@@ -200,16 +394,29 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
     uint16_t v_raw[PF][R];
     float g_r[PF], b_r[PF];
     auto fetch = [&](int slot, int t) {
+      if constexpr (PRO) {
+        const uint16_t* qk = pro_lds.qk[t];
 #pragma unroll
-      for (int c = 0; c < NCH; ++c) k_raw[slot][c] = LD::load(kp + t * p.k_st + c * 16 * VEC);
-      if (has_q) {
+        for (int c = 0; c < NCH; ++c) {
+          k_raw[slot][c] = LD::load(qk + DK + c * 16 * VEC + sub * VEC);
+          q_raw[slot][c] = LD::load(qk + c * 16 * VEC + sub * VEC);
+        }
 #pragma unroll
-        for (int c = 0; c < NCH; ++c) q_raw[slot][c] = LD::load(qp + t * p.q_st + c * 16 * VEC);
+        for (int r = 0; r < R; ++r) v_raw[slot][r] = pro_lds.v[t][r * 16 + gi];
+        g_r[slot] = pro_lds.g[t];
+        b_r[slot] = pro_lds.beta[t];
+      } else {
+#pragma unroll
+        for (int c = 0; c < NCH; ++c) k_raw[slot][c] = LD::load(kp + t * p.k_st + c * 16 * VEC);
+        if (has_q) {
+#pragma unroll
+          for (int c = 0; c < NCH; ++c) q_raw[slot][c] = LD::load(qp + t * p.q_st + c * 16 * VEC);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) v_raw[slot][r] = vp[t * p.v_st + row[r]];
+        g_r[slot] = gp[t * p.g_st];
+        b_r[slot] = bp[t * p.b_st];
       }
-#pragma unroll
-      for (int r = 0; r < R; ++r) v_raw[slot][r] = vp[t * p.v_st + row[r]];
-      g_r[slot] = gp[t * p.g_st];
-      b_r[slot] = bp[t * p.b_st];
     };
     if (n > 0) {
 #pragma unroll
@@ -301,7 +508,7 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
 int scan_grid(int items);
 int scan_cus();
 
-template <int DK>
+template <int DK, bool PRO = false>
 hipError_t launch_dk(const ScanParams& base, int R, int grid, int xcd, hipStream_t s) {
   ScanParams p = base;
   p.row_blocks = p.Dv / (16 * R);
@@ -312,6 +519,18 @@ hipError_t launch_dk(const ScanParams& base, int R, int grid, int xcd, hipStream
   const bool xcd_ok = blocks % 8 == 0 && p.items % 8 == 0 && blocks < p.items;
   p.xcd_items = (xcd != 0 && xcd_ok) ? p.items / 8 : 0;
   const bool deep = p.items <= scan_cus();
+  if constexpr (PRO) {
+    if (R != 1) return hipErrorInvalidValue;
+    const dim3 g(blocks), b(256);
+    if (p.pro_K == 4) {  // the Qwen3.5 conv width, taps fixed at compile time
+      if (deep) hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 4, true, 4>), g, b, 0, s, p);
+      else hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 1, true, 4>), g, b, 0, s, p);
+    } else {
+      if (deep) hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 4, true, 0>), g, b, 0, s, p);
+      else hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 1, true, 0>), g, b, 0, s, p);
+    }
+    return hipGetLastError();
+  }
   switch (R * (deep ? 10 : 1)) {
     case 1: hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 1>), dim3(blocks), dim3(256), 0, s, p); break;
     case 2: hipLaunchKernelGGL((gdn_scan_kernel<DK, 2, 1>), dim3(blocks), dim3(256), 0, s, p); break;
@@ -464,6 +683,85 @@ int scan_impl(const void* q, const void* k, const void* v, const float* g,
   return e == hipSuccess ? DFLASH_OK : (int)e;
 }
 
+// Verify scan with the layer prologue on the fly (Dk = 128, T <= kProMaxT).
+int scan_pro_impl(const void* qkv, int64_t qkv_sb, int64_t qkv_st, const void* conv_state,
+                  const void* conv_weight, const void* a, const void* b,
+                  const int64_t* ab_strides, const float* A_log, const void* dt_bias,
+                  const Select& sel, void* out, float* final_state, float* tape, int B, int T,
+                  int K, int Hk, int Hv, int Dk, int Dv, float eps, void* stream) {
+  if (B < 0 || T < 0 || K < 1 || K > kMaxConvTaps || Hk <= 0 || Hv <= 0 || Dk <= 0 || Dv <= 0)
+    return DFLASH_ERR_SHAPE;
+  if (Hv % Hk != 0) return DFLASH_ERR_SHAPE;
+  if (Dk != 128 || Dv % 16 != 0 || T > kProMaxT) return DFLASH_ERR_UNSUPPORTED;
+  if ((int64_t)B * Hv * (Dv / 16) > INT32_MAX) return DFLASH_ERR_SHAPE;
+  if (sel.prev_T < 0 || sel.period <= 0) return DFLASH_ERR_SHAPE;
+  if (sel.state == nullptr) return DFLASH_ERR_NULL;
+  if (final_state != nullptr && final_state == sel.state) return DFLASH_ERR_SHAPE;
+  if (sel.prev_T > 0 && (sel.prev_tape == nullptr || sel.prev_accepted == nullptr))
+    return DFLASH_ERR_NULL;
+  if (B == 0) return DFLASH_OK;
+  if (T == 0)  // nothing to run the prologue on: the rollback alone
+    return scan_impl(nullptr, nullptr, nullptr, nullptr, nullptr, sel.state, nullptr, final_state,
+                     tape, nullptr, B, 0, Hk, Hv, Dk, Dv, nullptr, &sel, stream);
+  if (qkv == nullptr || (K > 1 && conv_state == nullptr) || conv_weight == nullptr ||
+      a == nullptr || b == nullptr || A_log == nullptr || dt_bias == nullptr || out == nullptr)
+    return DFLASH_ERR_NULL;
+  const int64_t C = 2LL * Hk * Dk + (int64_t)Hv * Dv;
+  // q/k channel pairs are read as 4-byte words.
+  if (((uintptr_t)qkv & 3) || (qkv_sb & 1) || (qkv_st & 1) || ((uintptr_t)conv_state & 3))
+    return DFLASH_ERR_ALIGN;
+  if (((uintptr_t)conv_weight | (uintptr_t)a | (uintptr_t)b | (uintptr_t)dt_bias |
+       (uintptr_t)out) & 1)
+    return DFLASH_ERR_ALIGN;
+  if (((uintptr_t)sel.state & 15) || ((uintptr_t)final_state & 15) || ((uintptr_t)tape & 15) ||
+      ((uintptr_t)sel.prev_tape & 15))
+    return DFLASH_ERR_ALIGN;
+
+  ScanParams p{};
+  if (sel.prev_T > 0) {
+    p.sel_tape = sel.prev_tape;
+    p.sel_accepted = sel.prev_accepted;
+    p.state_wb = sel.state;
+    p.sel_period = sel.period;
+    p.sel_T = sel.prev_T;
+  }
+  p.state_in = sel.state;
+  p.out = static_cast<uint16_t*>(out);
+  p.final_state = final_state;
+  p.tape = tape;
+  p.B = B;
+  p.T = T;
+  p.Hv = Hv;
+  p.Dv = Dv;
+  p.rep = Hv / Hk;
+  p.tape_tstride = (int64_t)B * Hv * Dv * Dk;
+  p.pro_qkv = static_cast<const uint16_t*>(qkv);
+  p.pro_qkv_sb = qkv_sb;
+  p.pro_qkv_st = qkv_st;
+  p.pro_conv_state = static_cast<const uint16_t*>(conv_state);
+  p.pro_conv_w = static_cast<const uint16_t*>(conv_weight);
+  p.pro_a = static_cast<const uint16_t*>(a);
+  p.pro_b = static_cast<const uint16_t*>(b);
+  if (ab_strides != nullptr) {
+    p.pro_a_sb = ab_strides[0]; p.pro_a_st = ab_strides[1];
+    p.pro_b_sb = ab_strides[2]; p.pro_b_st = ab_strides[3];
+  } else {
+    p.pro_a_st = p.pro_b_st = Hv;
+    p.pro_a_sb = p.pro_b_sb = (int64_t)T * Hv;
+  }
+  p.pro_A_log = A_log;
+  p.pro_dt_bias = static_cast<const uint16_t*>(dt_bias);
+  p.pro_C = (int)C;
+  p.pro_K = K;
+  p.pro_Hk = Hk;
+  p.pro_eps = eps;
+  // The standalone prologue's scales: k by Dk^-1/2, q by Dk^-1.
+  p.pro_k_scale = 1.0f / sqrtf((float)Dk);
+  p.pro_q_scale = p.pro_k_scale * p.pro_k_scale;
+  const hipError_t e = launch_dk<128, true>(p, 1, -1, -1, static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? DFLASH_OK : (int)e;
+}
+
 }  // namespace
 }  // namespace dflash
 
@@ -498,4 +796,16 @@ extern "C" int dflash_gdn_replay(const void* k, const void* v, const float* g,
   if (state_out == nullptr) return DFLASH_ERR_NULL;
   return dflash::scan_impl(nullptr, k, v, g, beta, state_in, nullptr, state_out,
                            nullptr, lengths, B, T, Hk, Hv, Dk, Dv, strides, nullptr, stream);
+}
+
+extern "C" int dflash_gdn_prologue_scan_rollback(
+    const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_stride, const void* conv_state,
+    const void* conv_weight, const void* a, const void* b, const int64_t* ab_strides,
+    const float* A_log, const void* dt_bias, float* state, const float* prev_tape,
+    const int32_t* prev_accepted, int prev_T, int accepted_period, void* out, float* final_state,
+    float* tape, int B, int T, int K, int Hk, int Hv, int Dk, int Dv, float eps, void* stream) {
+  const dflash::Select sel{prev_tape, prev_accepted, state, prev_T, accepted_period};
+  return dflash::scan_pro_impl(qkv, qkv_batch_stride, qkv_row_stride, conv_state, conv_weight, a,
+                               b, ab_strides, A_log, dt_bias, sel, out, final_state, tape, B, T, K,
+                               Hk, Hv, Dk, Dv, eps, stream);
 }

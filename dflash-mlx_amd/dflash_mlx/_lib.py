@@ -82,6 +82,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_VP, _I64, _I64, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP,
          _I, _I, _I, _I, _I, _I, _I, ctypes.c_float, _VP],
     ),
+    "dflash_gdn_prologue_scan_rollback": (
+        _I,
+        [_VP, _I64, _I64, _VP, _VP, _VP, _VP, _VP, _VP, _VP,  # prologue inputs
+         _VP, _VP, _VP, _I, _I, _VP, _VP, _VP,  # state, selection, outputs
+         _I, _I, _I, _I, _I, _I, _I, ctypes.c_float, _VP],
+    ),
     "dflash_gdn_gated_rmsnorm": (
         _I, [_VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, ctypes.c_float, _VP]),
     "dflash_lm_head_accept_workspace_bytes": (_SZ, [_I, _I, _I]),

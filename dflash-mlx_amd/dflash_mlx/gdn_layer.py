@@ -163,3 +163,66 @@ def gdn_layer_verify(qkv, z, a, b, conv_state, state, weights: GatedDeltaWeights
     y = gated_rmsnorm(out, zz, weights.norm_weight, cfg.rms_norm_eps)
     record = make_rollback_record(conv_state, state, qkv, tape)
     return y.reshape(B, T, Hv * Dv), new_conv, final, tape, record
+
+
+def gdn_prologue_verify_rollback(qkv, conv_state, a, b, weights: GatedDeltaWeights,
+                                 cfg: GatedDeltaConfig, state, prev_tape, prev_accepted,
+                                 accepted_period: int | None = None, tape_out=None):
+    """gdn_prologue followed by gated_delta_verify_rollback, in one launch
+    (dflash_gdn_prologue_scan_rollback): the scan computes each head's q, k,
+    v, g and beta from the projection rows itself.  Same arguments as the two
+    calls (the prologue's, then the rollback scan's state / prev_tape /
+    prev_accepted / tape_out) and the same (out, tape), bit for bit; the new
+    conv window is not produced.  Supported: Dk == 128, T <= 32."""
+    from .gated_delta import _STATE_DTYPE
+
+    _require_device("qkv", qkv, None)
+    dev = qkv.device
+    B, T, C = qkv.shape
+    if C != cfg.conv_dim:
+        raise ValueError(f"qkv has {C} channels, the config needs {cfg.conv_dim}")
+    K = cfg.linear_conv_kernel_dim
+    Hk, Hv = cfg.linear_num_key_heads, cfg.linear_num_value_heads
+    Dk, Dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
+    for name, t in (("conv_state", conv_state), ("a", a), ("b", b), ("state", state),
+                    ("prev_tape", prev_tape), ("prev_accepted", prev_accepted)):
+        _require_device(name, t, dev)
+    if qkv.dtype != torch.bfloat16 or qkv.stride(-1) != 1:
+        raise ValueError("qkv must be bf16 with contiguous channels")
+    conv_state = conv_state.contiguous()
+    if tuple(conv_state.shape) != (B, K - 1, C) or conv_state.dtype != torch.bfloat16:
+        raise ValueError(f"conv_state must be bf16 [B, K-1, C] = {(B, K - 1, C)}")
+    a = a.to(torch.bfloat16)
+    b = b.to(torch.bfloat16)
+    if a.stride(-1) != 1:
+        a = a.contiguous()
+    if b.stride(-1) != 1:
+        b = b.contiguous()
+    if state.dtype != _STATE_DTYPE or not state.is_contiguous() or \
+            tuple(state.shape) != (B, Hv, Dv, Dk):
+        raise ValueError("state must be a contiguous float32 [B, Hv, Dv, Dk] buffer "
+                         "(it is updated in place)")
+    if prev_tape.dtype != _STATE_DTYPE or not prev_tape.is_contiguous() or \
+            tuple(prev_tape.shape[1:]) != (B, Hv, Dv, Dk):
+        raise ValueError("prev_tape must be a contiguous float32 [T', B, Hv, Dv, Dk] tape")
+    acc = prev_accepted.to(torch.int32).reshape(-1).contiguous()
+    period = acc.numel() if accepted_period is None else int(accepted_period)
+    if period <= 0 or acc.numel() < period or B % period != 0:
+        raise ValueError(f"accepted_period {period} must divide the batch {B} and fit prev_accepted")
+    out = torch.empty((B, T, Hv, Dv), dtype=torch.bfloat16, device=dev)
+    if tape_out is None:
+        tape_out = torch.empty((T, B, Hv, Dv, Dk), dtype=_STATE_DTYPE, device=dev)
+    elif tuple(tape_out.shape) != (T, B, Hv, Dv, Dk) or not tape_out.is_contiguous():
+        raise ValueError("tape_out must be a contiguous [T, B, Hv, Dv, Dk] float32 tensor")
+    w = weights
+    conv_w = w.conv_weight.contiguous()  # held until the launch is enqueued
+    strides = (ctypes.c_int64 * 4)(a.stride(0), a.stride(1), b.stride(0), b.stride(1))
+    _lib.call(
+        "dflash_gdn_prologue_scan_rollback",
+        qkv.data_ptr(), qkv.stride(0), qkv.stride(1), conv_state.data_ptr(), conv_w.data_ptr(),
+        a.data_ptr(), b.data_ptr(), strides, w.A_log.data_ptr(), w.dt_bias.data_ptr(),
+        state.data_ptr(), prev_tape.data_ptr(), acc.data_ptr(), prev_tape.shape[0], period,
+        out.data_ptr(), None, tape_out.data_ptr(), B, T, K, Hk, Hv, Dk, Dv,
+        float(cfg.rms_norm_eps), _lib.stream_handle(dev),
+    )
+    return out, tape_out

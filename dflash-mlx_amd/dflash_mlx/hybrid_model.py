@@ -145,7 +145,8 @@ class HybridVerifyRunner:
     for B sequences of T block tokens, with caches of Smax positions."""
 
     def __init__(self, cfg: HybridConfig, weights: HybridWeights, B: int, T: int, Smax: int,
-                 device: torch.device, gemm: str = "dflash", weight_layout: str = "tiled"):
+                 device: torch.device, gemm: str = "dflash", weight_layout: str = "tiled",
+                 fused_prologue: bool = True):
         """gemm: "dflash" runs every projection on this package's verify-sized
         GEMM (split-K partials summed by the consumer); "hipblaslt" runs them
         as torch.mm (for comparison).  weight_layout (dflash GEMMs): "tiled"
@@ -153,13 +154,16 @@ class HybridVerifyRunner:
         (dflash_weight_tile_bf16, cached in the layer dicts as "<name>_tiled";
         same sums bit for bit) wherever the row count is a multiple of 16 (the
         rest stay row-major), "rowmajor" streams the nn.Linear [N, K] weights
-        as they are."""
+        as they are.  fused_prologue (dflash GEMMs): each gated-delta layer's
+        scan computes its own prologue (dflash_gdn_prologue_scan_rollback, one
+        launch, same bits) instead of a prologue launch then the scan."""
         if gemm not in ("dflash", "hipblaslt"):
             raise ValueError(f"gemm must be 'dflash' or 'hipblaslt', got {gemm!r}")
         if weight_layout not in ("tiled", "rowmajor"):
             raise ValueError(f"weight_layout must be 'tiled' or 'rowmajor', got {weight_layout!r}")
         self.gemm = gemm
         self.tiled = weight_layout == "tiled"
+        self.fused_prologue = bool(fused_prologue) and cfg.linear.linear_key_head_dim == 128
         if T > 16 or B * T > 64:
             raise ValueError("the verify step takes T <= 16 block tokens and B*T <= 64 rows")
         if Smax % 64:
@@ -351,7 +355,8 @@ class HybridVerifyRunner:
                     self._scan_strides)
             gnorm = (self.scan_out.data_ptr(), base + 2 * C, self._z_strides,
                      gw.norm_weight.data_ptr(), self.gnorm.data_ptr(), B, T, Hv, Dv, eps)
-            self._gdn_args.append((prologue, scan, gnorm))
+            fused = prologue[:10] + scan[5:15] + (K, Hk, Hv, Dk, Dv, eps)
+            self._gdn_args.append((prologue, scan, gnorm, fused))
             gi += 1
         self._conv_ptrs = (_lib.ptr_array(self.conv), _lib.ptr_array(self.proj),
                            _lib.ptr_array(self.conv))
@@ -424,10 +429,13 @@ class HybridVerifyRunner:
             if i > 0:
                 self._residual("w_down", lw["ln_in"], stream)
             if cfg.is_linear(i):
-                prologue, scan, gnorm = self._gdn_args[gi]
+                prologue, scan, gnorm, fused = self._gdn_args[gi]
                 call(ga["in"][0], *ga["in"][1], stream)
-                call("dflash_gdn_prologue", *prologue, stream)
-                call("dflash_gdn_verify_scan_rollback", *scan, stream)
+                if self.fused_prologue:
+                    call("dflash_gdn_prologue_scan_rollback", *fused, stream)
+                else:
+                    call("dflash_gdn_prologue", *prologue, stream)
+                    call("dflash_gdn_verify_scan_rollback", *scan, stream)
                 call("dflash_gdn_gated_rmsnorm", *gnorm, stream)
                 call(ga["out"][0], *ga["out"][1], stream)
                 self._residual("w_out", lw["ln_post"], stream)
@@ -462,7 +470,7 @@ class HybridVerifyRunner:
             call("dflash_add_rmsnorm", self.h.data_ptr(), None if r is None else r.data_ptr(),
                  lw["ln_in"].data_ptr(), self.h.data_ptr(), self.xn.data_ptr(), M, H, eps, stream)
             if cfg.is_linear(i):
-                prologue, scan, gnorm = self._gdn_args[gi]
+                prologue, scan, gnorm, _ = self._gdn_args[gi]
                 self._mm(self.xn, lw["w_in"], self.proj[gi])
                 call("dflash_gdn_prologue", *prologue, stream)
                 call("dflash_gdn_verify_scan_rollback", *scan, stream)

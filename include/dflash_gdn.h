@@ -234,6 +234,36 @@ int dflash_gdn_prologue(const void* qkv, int64_t qkv_batch_stride,
                         int Hv, int Dk, int Dv, float eps, void* stream);
 
 /*
+ * dflash_gdn_prologue followed by dflash_gdn_verify_scan_rollback, in one
+ * launch: the scan's workgroups compute the prologue of their own head from
+ * the raw projection rows (into LDS) instead of reading act, g and beta.
+ *
+ * Replaces the same reference span as the pair: the layer body at
+ * dflash_mlx/custom_qwen35_model.py:431-466 (conv + silu, q/k rms-norm, g and
+ * beta, then the gated-delta kernel of :33-74 with its tape), with the
+ * rollback of the previous verify fused into the state load as in
+ * dflash_gdn_verify_scan_rollback.  The reference has no single call for it.
+ *
+ * Arguments as the two calls it stands for: the prologue's inputs (qkv,
+ * conv_state, conv_weight, a, b, A_log, dt_bias, K, eps), then the rollback
+ * scan's state / tape / selection and outputs (out is required).  q, k, v, g
+ * and beta are bit-identical to what dflash_gdn_prologue would store, so
+ * out, final_state and tape are bit-identical to the two-call path.  No new
+ * conv window is written (the pair's new_conv_state output is dropped; the
+ * verify path rebuilds the window at commit, dflash_conv_rollback).
+ * Supported: Dk == 128, Dv % 16 == 0, 1 <= K <= 8, T <= 32; qkv 4-byte
+ * aligned with even strides, conv_state 4-byte aligned.
+ */
+int dflash_gdn_prologue_scan_rollback(
+    const void* qkv, int64_t qkv_batch_stride, int64_t qkv_row_stride,
+    const void* conv_state, const void* conv_weight, const void* a,
+    const void* b, const int64_t* ab_strides, const float* A_log,
+    const void* dt_bias, float* state, const float* prev_tape,
+    const int32_t* prev_accepted, int prev_T, int accepted_period, void* out,
+    float* final_state, float* tape, int B, int T, int K, int Hk, int Hv,
+    int Dk, int Dv, float eps, void* stream);
+
+/*
  * Gated-delta layer epilogue: y = weight * x * rsqrt(mean(x^2) + eps) *
  * silu(z) over each (b, t, h) row of D channels.
  *

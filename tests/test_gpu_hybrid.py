@@ -68,8 +68,9 @@ def _initial_state(cfg, B, lens, seed):
     return dict(lens=list(lens), conv=conv, rec=rec, k=k, v=v)
 
 
-def _runner(cfg, w, st, B, T, Smax, device, weight_layout="tiled"):
-    r = HybridVerifyRunner(cfg, w, B, T, Smax, device, weight_layout=weight_layout)
+def _runner(cfg, w, st, B, T, Smax, device, weight_layout="tiled", fused_prologue=True):
+    r = HybridVerifyRunner(cfg, w, B, T, Smax, device, weight_layout=weight_layout,
+                           fused_prologue=fused_prologue)
     r.set_state(st["lens"], [c.to(device) for c in st["conv"]], [s.to(device) for s in st["rec"]],
                 [k.to(device) for k in st["k"]], [v.to(device) for v in st["v"]])
     return r
@@ -128,6 +129,35 @@ def test_tiled_and_rowmajor_weights_give_the_same_step(device):
         run.forward_accept()
         torch.cuda.synchronize()
         outs.append((run.xn.clone(), run.tape[0].clone(), run.posterior.clone(), run.matched.clone()))
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_fused_and_separate_prologue_give_the_same_steps(device):
+    """The scan that computes its own layer prologue (one launch) and the
+    prologue launch + scan give the same bits over two steps, the second
+    starting from the first one's rollback."""
+    cfg, B, T, Smax = SMALL, 2, 16, 256
+    w = HybridWeights.random(cfg, device, seed=31, on_device=False)
+    st = _initial_state(cfg, B, [17, 70], seed=32)
+    gen = torch.Generator().manual_seed(33)
+    toks = [torch.randint(0, cfg.vocab_size, (B, T), generator=gen, dtype=torch.int32)
+            for _ in range(2)]
+    outs = []
+    for fused in (True, False):
+        print(f"[hybrid prologue] fused={fused}", flush=True)
+        run = _runner(cfg, w, st, B, T, Smax, device, fused_prologue=fused)
+        assert run.fused_prologue == fused
+        got = []
+        for i, tk in enumerate(toks):
+            run.tokens.copy_(tk)
+            run.forward_accept()
+            run.matched.copy_(torch.tensor([5, 11][::1 if i == 0 else -1], dtype=torch.int32))
+            run.commit()
+            torch.cuda.synchronize()
+            got += [run.xn.clone(), run.posterior.clone(), run.state[0].clone(),
+                    run.tape[0].clone(), run.conv[0].clone()]
+        outs.append(got)
     for a, b in zip(*outs):
         assert torch.equal(a, b)
 

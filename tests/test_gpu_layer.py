@@ -152,3 +152,84 @@ def test_prologue_rejects_aliasing_and_bad_dims(device):
     with pytest.raises(_lib.DFlashError):
         gdn_prologue(x["qkv"].to(device), x["conv_state"].to(device), x["a"].to(device),
                      x["b"].to(device), _w_dev(w, device), cfg)
+
+
+FUSED_CFGS = [
+    (GatedDeltaConfig(), 2, 16),                                        # Qwen3.5-4B shape
+    (GatedDeltaConfig(), 1, 1),
+    (GatedDeltaConfig(), 3, 2),                                         # T < K-1
+    (GatedDeltaConfig(), 1, 32),                                        # the largest block
+    (GatedDeltaConfig(linear_num_key_heads=4, linear_num_value_heads=16,
+                      linear_conv_kernel_dim=2), 2, 7),                 # 4 value heads per key head
+    (GatedDeltaConfig(linear_num_key_heads=2, linear_num_value_heads=2,
+                      linear_value_head_dim=64, linear_conv_kernel_dim=8), 1, 9),
+]
+
+
+@pytest.mark.parametrize("inplace", [False, True], ids=["tape_out", "tape_in_place"])
+@pytest.mark.parametrize("cfg,B,T", FUSED_CFGS, ids=lambda x: str(x) if not isinstance(x, GatedDeltaConfig)
+                         else f"Hk{x.linear_num_key_heads}Hv{x.linear_num_value_heads}"
+                              f"Dv{x.linear_value_head_dim}K{x.linear_conv_kernel_dim}")
+def test_fused_prologue_scan_matches_two_calls(device, cfg, B, T, inplace):
+    """dflash_gdn_prologue_scan_rollback gives the bits of dflash_gdn_prologue
+    + dflash_gdn_verify_scan_rollback: out, tape and the rolled-back state,
+    with q/k/v/a/b read as strided views of projection rows."""
+    from dflash_mlx import gated_delta_verify_rollback
+    from dflash_mlx.gdn_layer import gdn_prologue_verify_rollback
+
+    print(f"[fused prologue+scan {cfg} B={B} T={T} inplace={inplace}]", flush=True)
+    x, w = _inputs(cfg, B, T, seed=B * 1000 + T)
+    C, Hv = cfg.conv_dim, cfg.linear_num_value_heads
+    Dk, Dv = cfg.linear_key_head_dim, cfg.linear_value_head_dim
+    gen = torch.Generator().manual_seed(T + 77)
+    rows = C + 2 * Hv + 6
+    proj = torch.randn(B, T, rows, generator=gen).bfloat16()
+    proj[..., :C] = x["qkv"]
+    proj[..., C:C + Hv] = x["b"]
+    proj[..., C + Hv:C + 2 * Hv] = x["a"]
+    proj = proj.to(device)
+    qkv, bb, aa = proj[..., :C], proj[..., C:C + Hv], proj[..., C + Hv:C + 2 * Hv]
+    conv_state = x["conv_state"].to(device)
+    wd = _w_dev(w, device)
+    prev_T = T if inplace else 5
+    state0 = (0.05 * torch.randn(B, Hv, Dv, Dk, generator=gen)).to(device)
+    tape0 = (0.05 * torch.randn(prev_T, B, Hv, Dv, Dk, generator=gen)).to(device)
+    acc = torch.tensor([0, 3, prev_T][:B], dtype=torch.int32, device=device)
+
+    st_a, tp_a = state0.clone(), tape0.clone()
+    q, k, v, g, beta, _ = gdn_prologue(qkv, conv_state, aa, bb, wd, cfg)
+    out_a, tape_a = gated_delta_verify_rollback(q, k, v, g, beta, st_a, tp_a, acc,
+                                                tape_out=tp_a if inplace else None)
+    st_b, tp_b = state0.clone(), tape0.clone()
+    out_b, tape_b = gdn_prologue_verify_rollback(qkv, conv_state, aa, bb, wd, cfg, st_b, tp_b, acc,
+                                                 tape_out=tp_b if inplace else None)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b)
+    assert torch.equal(tape_a, tape_b)
+    assert torch.equal(st_a, st_b)
+    assert torch.isfinite(out_b.float()).all()
+
+
+def test_fused_prologue_scan_rejects_unsupported(device):
+    from dflash_mlx.gdn_layer import gdn_prologue_verify_rollback
+
+    def run(cfg, T, offset=0):
+        x, w = _inputs(cfg, 1, T, seed=3)
+        Hv, Dv, Dk = cfg.linear_num_value_heads, cfg.linear_value_head_dim, cfg.linear_key_head_dim
+        flat = torch.cat([torch.zeros(offset, dtype=torch.bfloat16), x["qkv"].flatten()]).to(device)
+        qkv = flat[offset:].view(1, T, cfg.conv_dim)
+        st = torch.zeros(1, Hv, Dv, Dk, device=device)
+        tape = torch.zeros(1, 1, Hv, Dv, Dk, device=device)
+        acc = torch.zeros(1, dtype=torch.int32, device=device)
+        gdn_prologue_verify_rollback(qkv, x["conv_state"].to(device), x["a"].to(device),
+                                     x["b"].to(device), _w_dev(w, device), cfg, st, tape, acc)
+        torch.cuda.synchronize()
+
+    small = dict(linear_num_key_heads=1, linear_num_value_heads=1, linear_value_head_dim=64)
+    run(GatedDeltaConfig(**small), 4)                                   # supported: runs
+    with pytest.raises(_lib.DFlashError):                               # Dk != 128
+        run(GatedDeltaConfig(linear_key_head_dim=64, **small), 4)
+    with pytest.raises(_lib.DFlashError):                               # T > 32
+        run(GatedDeltaConfig(**small), 33)
+    with pytest.raises(_lib.DFlashError):                               # qkv not 4-byte aligned
+        run(GatedDeltaConfig(**small), 4, offset=1)
