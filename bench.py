@@ -119,24 +119,32 @@ def time_steps(torch, K: int, phases):
 
 def measure_lm_head(torch, dev, M=16, H=2560, V=151936, n=50):
     """Fused greedy LM head + accept (MFMA, no logits) at the
-    Qwen3.5-4B shape vs the unfused path (hipBLASLt bf16 logits via a 2-D
-    F.linear, then the greedy-accept kernel).  HBM-bound on the weight."""
-    from dflash_mlx.runtime import greedy_accept, lm_head_greedy_accept
+    Qwen3.5-4B shape, over the row-major [V, H] weight and over its
+    fragment-tiled copy (tile_weight, made once), vs the unfused path
+    (hipBLASLt bf16 logits via a 2-D F.linear, then the greedy-accept
+    kernel).  HBM-bound on the weight."""
+    from dflash_mlx.runtime import greedy_accept, lm_head_greedy_accept, tile_weight
 
     gen = torch.Generator(device=dev).manual_seed(0)
     hidden = (torch.randn(M, H, generator=gen, device=dev) / H ** 0.25).to(torch.bfloat16)
     weight = (torch.randn(V, H, generator=gen, device=dev) / H ** 0.25).to(torch.bfloat16)
     draft = torch.zeros(1, M, dtype=torch.int32, device=dev)
 
+    weight_tiled = tile_weight(weight)
+
     def fused():
         lm_head_greedy_accept(hidden[None], weight, draft, want_posterior=False)
+
+    def fused_tiled():
+        lm_head_greedy_accept(hidden[None], weight, draft, want_posterior=False,
+                              weight_tiled=weight_tiled)
 
     def unfused():
         logits = torch.nn.functional.linear(hidden, weight)
         greedy_accept(logits[None], draft, want_posterior=False)
 
     out = {}
-    for name, fn in (("fused", fused), ("unfused", unfused)):
+    for name, fn in (("fused", fused), ("fused_tiled", fused_tiled), ("unfused", unfused)):
         for _ in range(5):
             fn()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -147,17 +155,23 @@ def measure_lm_head(torch, dev, M=16, H=2560, V=151936, n=50):
         e1.record()
         torch.cuda.synchronize()
         out[name] = e0.elapsed_time(e1) * 1e3 / n
+    del weight_tiled
     bytes_alg = 2 * V * H + 2 * M * H
     gbps = bytes_alg / (out["fused"] / 1e6) / 1e9
+    gbps_t = bytes_alg / (out["fused_tiled"] / 1e6) / 1e9
     return {
         "shape": {"M": M, "H": H, "V": V},
         "fused_us": round(out["fused"], 2),
+        "fused_tiled_us": round(out["fused_tiled"], 2),
         "unfused_us": round(out["unfused"], 2),
         "bytes_alg": bytes_alg,
         "fused_gbps": round(gbps, 1),
         "fused_frac": round(gbps / PEAK_HBM_GBPS, 4),
-        "note": "per call, back-to-back launches incl. Python dispatch (fused: 2 kernels; "
-                "unfused: GEMM + 2 kernels)",
+        "fused_tiled_gbps": round(gbps_t, 1),
+        "fused_tiled_frac": round(gbps_t / PEAK_HBM_GBPS, 4),
+        "note": "per call, back-to-back launches incl. Python dispatch (fused: 2 kernels over the "
+                "row-major weight; fused_tiled: the same over its fragment-tiled copy; unfused: "
+                "GEMM + 2 kernels)",
     }
 
 

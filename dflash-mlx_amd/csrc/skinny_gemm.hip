@@ -84,6 +84,7 @@ __global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams
   const int r16 = lane & 15;
   const int g = lane >> 4;
   constexpr int kRowGroups = (kGThreads / 64) / KW;  // row groups per workgroup
+  static_assert(KW == 1 || kRowGroups == 1, "red[] holds the k-parts of one row group");
   const int kpart = wave % KW;                        // this wave's quarter of the k-range
   const int nwave = (blockIdx.x * kRowGroups + wave / KW) * VT * 16;
   const int split = blockIdx.y;

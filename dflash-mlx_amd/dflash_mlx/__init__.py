@@ -30,6 +30,7 @@ from .runtime import (
     lm_head_greedy_accept,
     longest_prefix_match,
     sample_tokens,
+    tile_weight,
     verify_block_parallel_replay,
 )
 
@@ -54,5 +55,6 @@ __all__ = [
     "rollback_linear_caches",
     "sample_tokens",
     "tape_select",
+    "tile_weight",
     "verify_block_parallel_replay",
 ]

@@ -95,6 +95,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_VP, _I64, _VP, _I64, _I, _I, _VP, _I64, _I, _VP, _VP, _VP, _I, _I, _VP, _SZ, _VP],
     ),
+    "dflash_lm_head_greedy_accept_tiled": (
+        _I,
+        [_VP, _I64, _VP, _I, _I, _VP, _I64, _I, _VP, _VP, _VP, _I, _I, _VP, _SZ, _VP],
+    ),
     "dflash_tape_select": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I64, _I64, _VP]),
     "dflash_conv_rollback": (
         _I,

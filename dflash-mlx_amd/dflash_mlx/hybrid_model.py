@@ -104,6 +104,9 @@ class HybridWeights:
     final_norm: torch.Tensor
     lm_head: torch.Tensor
     layers: list
+    # The LM head's fragment-tiled copy, made by the first runner that streams
+    # it (tile_weight; V % 16 == 0).
+    lm_head_tiled: torch.Tensor | None = None
 
     @staticmethod
     def random(cfg: HybridConfig, device, seed: int = 0, std: float = 0.02,
@@ -379,11 +382,21 @@ class HybridVerifyRunner:
             self._attn_args.append((prep, attn))
             ai += 1
         # draft = block[1:] of each sequence (row stride T)
-        self._lm_args = (self.xn.data_ptr(), cfg.hidden_size, self.w.lm_head.data_ptr(),
-                         cfg.hidden_size, cfg.hidden_size, cfg.vocab_size,
-                         self.tokens.data_ptr() + 4, T, T - 1, self.posterior.data_ptr(),
-                         self.matched.data_ptr(), self.bonus.data_ptr(), B, T,
-                         self.lm_ws.data_ptr(), self.lm_ws.numel())
+        tail = (self.tokens.data_ptr() + 4, T, T - 1, self.posterior.data_ptr(),
+                self.matched.data_ptr(), self.bonus.data_ptr(), B, T, self.lm_ws.data_ptr(),
+                self.lm_ws.numel())
+        if self.tiled and self.gemm == "dflash" and cfg.vocab_size % 16 == 0:
+            if self.w.lm_head_tiled is None:
+                from .runtime import tile_weight
+
+                self.w.lm_head_tiled = tile_weight(self.w.lm_head)
+            self._lm_fn = "dflash_lm_head_greedy_accept_tiled"
+            self._lm_args = (self.xn.data_ptr(), cfg.hidden_size, self.w.lm_head_tiled.data_ptr(),
+                             cfg.hidden_size, cfg.vocab_size) + tail
+        else:
+            self._lm_fn = "dflash_lm_head_greedy_accept"
+            self._lm_args = (self.xn.data_ptr(), cfg.hidden_size, self.w.lm_head.data_ptr(),
+                             cfg.hidden_size, cfg.hidden_size, cfg.vocab_size) + tail
 
     def set_state(self, lens, conv=None, rec=None, k=None, v=None):
         """Load cache contents: lens [B] (live KV length), per gated-delta layer
@@ -454,7 +467,7 @@ class HybridVerifyRunner:
             call(ga["gu"][0], *ga["gu"][1], stream)
             call(ga["down"][0], *ga["down"][1], stream)
         self._residual("w_down", self.w.final_norm, stream)
-        call("dflash_lm_head_greedy_accept", *self._lm_args, stream)
+        call(self._lm_fn, *self._lm_args, stream)
 
     def _forward_accept_hipblaslt(self):
         cfg, B, T = self.cfg, self.B, self.T
@@ -492,7 +505,7 @@ class HybridVerifyRunner:
             self._mm(self.mlp_act, lw["w_down"], self.r)
         call("dflash_add_rmsnorm", self.h.data_ptr(), self.r.data_ptr(), self.w.final_norm.data_ptr(),
              self.h.data_ptr(), self.xn.data_ptr(), M, H, eps, stream)
-        call("dflash_lm_head_greedy_accept", *self._lm_args, stream)
+        call(self._lm_fn, *self._lm_args, stream)
 
     def commit(self):
         """keep = matched + 1, lens += keep, and every conv window rolled to

@@ -96,12 +96,15 @@ def lm_head_greedy_accept(
     draft: torch.Tensor | Sequence[int] | Sequence[Sequence[int]] | None = None,
     *,
     want_posterior: bool = True,
+    weight_tiled: torch.Tensor | None = None,
 ) -> tuple[torch.Tensor | None, torch.Tensor, torch.Tensor]:
     """greedy_accept(hidden @ weight.T, draft) without materialising logits.
 
     hidden: [B,N,H] (or [N,H]) bf16; weight: [V,H] bf16 (LM head or tied
     embedding).  B*N <= 64 (verify-sized), H % 64 == 0.  Fuses the reference's
-    lm_head_argmax hook (dflash_mlx/adapters.py:267-271) with the accept."""
+    lm_head_argmax hook (dflash_mlx/adapters.py:267-271) with the accept.
+    weight_tiled: the head's fragment-tiled copy (tile_weight(weight), made
+    once; V % 16 == 0), streamed instead of weight when given."""
     _require_device("hidden", hidden, None)
     dev = hidden.device
     _require_device("weight", weight, dev)
@@ -137,6 +140,19 @@ def lm_head_greedy_accept(
     lib = _lib.load()
     ws = torch.empty((max(int(lib.dflash_lm_head_accept_workspace_bytes(B, N, V)), 8),),
                      dtype=torch.uint8, device=dev)
+    if weight_tiled is not None:
+        _require_device("weight_tiled", weight_tiled, dev)
+        if weight_tiled.numel() * weight_tiled.element_size() < \
+                int(lib.dflash_weight_tile_bytes(V, H)) or not weight_tiled.is_contiguous():
+            raise ValueError("weight_tiled must be the contiguous tile_weight(weight) copy")
+        _lib.call(
+            "dflash_lm_head_greedy_accept_tiled",
+            h2.data_ptr(), h2.stride(0), weight_tiled.data_ptr(), H, V,
+            _lib.ptr(d), d.stride(0) if d is not None else 0, n,
+            _lib.ptr(post), matched.data_ptr(), bonus.data_ptr(), B, N,
+            ws.data_ptr(), ws.numel(), _lib.stream_handle(dev),
+        )
+        return post, matched, bonus
     _lib.call(
         "dflash_lm_head_greedy_accept",
         h2.data_ptr(), h2.stride(0), w.data_ptr(), w.stride(0), H, V,
@@ -147,10 +163,29 @@ def lm_head_greedy_accept(
     return post, matched, bonus
 
 
-def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+def tile_weight(weight: torch.Tensor) -> torch.Tensor:
+    """The fragment-tiled copy of a bf16 [N, K] weight (dflash_weight_tile_bf16:
+    [K/64][N/16][2][64][8], the layout the tiled GEMMs and LM head stream);
+    N % 16 == 0, K % 64 == 0.  Made once per weight at load time."""
+    _require_device("weight", weight, None)
+    if weight.dim() != 2 or weight.dtype != torch.bfloat16 or weight.stride(-1) != 1:
+        raise ValueError("weight must be a bf16 [N, K] matrix with contiguous rows")
+    N, K = weight.shape
+    lib = _lib.load()
+    nbytes = int(lib.dflash_weight_tile_bytes(N, K))
+    if nbytes <= 0:
+        raise ValueError(f"[{N}, {K}] cannot be tiled (needs N % 16 == 0, K % 64 == 0)")
+    t = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=weight.device)
+    _lib.call("dflash_weight_tile_bf16", weight.data_ptr(), weight.stride(0), t.data_ptr(), N, K,
+              _lib.stream_handle(weight.device))
+    return t
+
+
+def lm_head_argmax(hidden: torch.Tensor, weight: torch.Tensor,
+                   weight_tiled: torch.Tensor | None = None) -> torch.Tensor:
     """The reference's lm_head_argmax hook (adapters.py:267-271):
     argmax(hidden @ weight.T, -1) as int32 [..., N], fused (no logits)."""
-    post, _, _ = lm_head_greedy_accept(hidden, weight, None)
+    post, _, _ = lm_head_greedy_accept(hidden, weight, None, weight_tiled=weight_tiled)
     return post.reshape(hidden.shape[:-1])
 
 

@@ -305,6 +305,25 @@ int dflash_lm_head_greedy_accept(const void* hidden, int64_t hidden_row_stride,
                                  void* stream);
 
 /*
+ * dflash_lm_head_greedy_accept over the head's fragment-tiled copy
+ * (dflash_weight_tile_bf16(weight, H, weight_tiled, V, H, stream), made once
+ * at load time): the same reference call replaced, the same outputs and
+ * workspace.  The contraction is split over two k-halves summed in fp32, so
+ * a logit may differ from the row-major kernel's in its last bits (ties
+ * within fp32 rounding may pick either token).  Supported: V % 16 == 0 and
+ * the limits above.
+ */
+int dflash_lm_head_greedy_accept_tiled(const void* hidden,
+                                       int64_t hidden_row_stride,
+                                       const void* weight_tiled, int H, int V,
+                                       const int32_t* draft,
+                                       int64_t draft_stride, int n_draft,
+                                       int32_t* posterior, int32_t* matched,
+                                       int32_t* bonus, int B, int N,
+                                       void* workspace, size_t workspace_bytes,
+                                       void* stream);
+
+/*
  * Recurrent-state rollback by tape gather, for L layers in one launch.
  *
  * Replaces the replay in Qwen3_5TextModel.rollback_linear_caches

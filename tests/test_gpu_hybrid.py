@@ -115,7 +115,8 @@ def test_small_hybrid_step_matches_oracle(device):
 def test_tiled_and_rowmajor_weights_give_the_same_step(device):
     """The fragment-tiled weight layout changes how the GEMMs stream, not what
     they sum: the whole step's hidden states, tape and accept are bit-identical
-    to the row-major run."""
+    to the row-major run.  (SMALL's vocab of 1000 is not a multiple of 16, so
+    both runs use the row-major LM head, whose tiled form splits the sum.)"""
     cfg, B, T, Smax = SMALL, 2, 16, 256
     w = HybridWeights.random(cfg, device, seed=21, on_device=False)
     st = _initial_state(cfg, B, [33, 90], seed=22)

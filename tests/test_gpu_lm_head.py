@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from dflash_mlx import _lib, greedy_accept, lm_head_argmax, lm_head_greedy_accept
+from dflash_mlx import _lib, greedy_accept, lm_head_argmax, lm_head_greedy_accept, tile_weight
 
 pytestmark = pytest.mark.gpu
 
@@ -106,3 +106,61 @@ def test_rejects_unsupported(device):
         lm_head_argmax(h, w)
     with pytest.raises(_lib.DFlashError):
         lm_head_argmax(h[:4, :48].contiguous(), w[:, :48].contiguous())  # H % 64 != 0
+
+
+@pytest.mark.parametrize("M,H,V", [(1, 64, 1008), (16, 2560, 20016), (17, 512, 4096),
+                                   (33, 256, 3008), (64, 2560, 8192)])
+def test_tiled_head_matches_fp64(device, M, H, V):
+    """The head over its fragment-tiled copy (tile_weight): same contract."""
+    hidden, weight = _inputs(M, H, V, seed=M * 11 + V)
+    print(f"[lm_head tiled M={M} H={H} V={V}]", flush=True)
+    w = weight.to(device)
+    post = lm_head_argmax(hidden.to(device), w, weight_tiled=tile_weight(w))
+    torch.cuda.synchronize()
+    assert tuple(post.shape) == (M,)
+    _check_rows(post.cpu().numpy(), _fp64_logits(hidden, weight))
+
+
+def test_tiled_head_planted_winners_and_row_major_agree(device):
+    """Planted winners: the tiled and row-major heads give the exact accept;
+    on random rows the two agree wherever the top-2 margin exceeds fp32
+    rounding of the split contraction."""
+    B, N, H, V = 2, 16, 2560, 50000
+    hidden, weight = _inputs(B * N, H, V, seed=13)
+    gen = torch.Generator().manual_seed(14)
+    targets = torch.randint(0, V, (B * N,), generator=gen)
+    w = weight.clone()
+    for m in range(B * N):
+        w[targets[m]] = (hidden[m].float() * 4.0).bfloat16()
+    accept = [7, 16]
+    draft = targets.reshape(B, N).clone().to(torch.int32)
+    draft[0, 7] = (draft[0, 7] + 1) % V
+    wd = w.to(device)
+    wt = tile_weight(wd)
+    post, matched, bonus = lm_head_greedy_accept(hidden.reshape(B, N, H).to(device), wd,
+                                                 draft.to(device), weight_tiled=wt)
+    torch.cuda.synchronize()
+    assert post.cpu().reshape(-1).tolist() == targets.tolist()
+    assert matched.cpu().tolist() == accept
+    assert bonus.cpu().tolist() == [int(targets[7]), -1]
+    h2, w2 = _inputs(B * N, H, V, seed=15)
+    hd, wd2 = h2.to(device), w2.to(device)
+    a = lm_head_argmax(hd, wd2)
+    b = lm_head_argmax(hd, wd2, weight_tiled=tile_weight(wd2))
+    torch.cuda.synchronize()
+    lg = _fp64_logits(h2, w2)
+    for m in range(B * N):
+        scale = np.max(np.abs(lg[m]))
+        top2 = np.partition(lg[m], -2)[-2:]
+        if (top2[1] - top2[0]) / scale > 1e-5:
+            assert int(a[m]) == int(b[m]), f"row {m}"
+
+
+def test_tiled_head_rejects_unsupported(device):
+    h = torch.zeros(4, 64, dtype=torch.bfloat16, device=device)
+    w = torch.zeros(100, 64, dtype=torch.bfloat16, device=device)      # V % 16 != 0
+    with pytest.raises(ValueError):
+        tile_weight(w)
+    w112 = torch.zeros(112, 64, dtype=torch.bfloat16, device=device)
+    with pytest.raises(ValueError):                                     # buffer too small
+        lm_head_argmax(h, w112, weight_tiled=torch.zeros(16, dtype=torch.bfloat16, device=device))
