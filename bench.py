@@ -16,7 +16,7 @@ inputs resident in HBM:
                        all 24 layers' states -> conv rollback.  4 launches.
 Prints one JSON line.
 
-python bench.py [--steps K] [--warmup W] [--config 1|2] [--cpu-seconds S]
+python bench.py [--steps K] [--warmup W] [--config 0|1|2] [--cpu-seconds S]
 """
 from __future__ import annotations
 
@@ -44,7 +44,9 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=1, choices=(1, 2))
+    ap.add_argument("--config", type=int, default=1, choices=(0, 1, 2),
+                    help="0: the reference's tiny CPU-runnable case (latency-bound); "
+                         "1: the headline (default); 2: batched serving, B=32")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="bounded CPU-baseline sample (0 disables it)")
     ap.add_argument("--no-extras", action="store_true",
