@@ -10,8 +10,9 @@ Two step forms are timed, both through the C ABI with preallocated buffers and
 inputs resident in HBM:
   fused    (headline)  scan whose state load performs the previous step's
                        rollback (state read from the previous tape at the
-                       device-side accepted count) -> greedy accept -> conv
-                       rollback.  4 kernels, no host sync.  Timed eagerly with
+                       device-side accepted count) -> greedy accept + conv
+                       rollback (argmax slices, then the accept's finalize
+                       inside the window copy).  3 kernels, no host sync.  Timed eagerly with
                        HIP events between phases (the breakdown) and as K
                        replays of the step captured as one HIP graph (the
                        value: how the device-driven serving loop launches it).
@@ -528,8 +529,8 @@ def main() -> int:
 
     K = args.steps
     print(f"[bench] timing {K} fused + {K} explicit steps", file=sys.stderr, flush=True)
-    tf = time_steps(torch, K, [("scan", fused.scan_rolled), ("accept", fused.accept),
-                               ("rollback", fused.conv_rollback)])
+    tf = time_steps(torch, K, [("scan", fused.scan_rolled),
+                               ("accept_rollback", fused.accept_conv_rollback)])
     te = time_steps(torch, K, [("scan", explicit.scan), ("accept", explicit.accept),
                                ("rollback", explicit.rollback)])
     # The same fused step as the device-driven serving loop launches it: captured
@@ -604,8 +605,9 @@ def main() -> int:
             "accepted": accepted,
             "io": "bf16 q/k/v/out, fp32 g/beta/state/tape, fp32 logits",
             "step": "fused: scan+tape with the previous step's state rollback in its load "
-                    "(1 launch) -> greedy accept (2) -> conv-window rollback (1), replayed "
-                    "as one HIP graph",
+                    "(1 launch) -> greedy accept + conv-window rollback (2 launches: argmax "
+                    "slices, then the accept's finalize inside the window copy), replayed as "
+                    "one HIP graph",
         },
         "roofline": roof,
         "graph_step_us": round(tg["gpu_step"], 2),

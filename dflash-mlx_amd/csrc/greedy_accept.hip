@@ -20,6 +20,7 @@
 #include <stdint.h>
 
 #include "accept_common.h"
+#include "conv_window.h"
 #include "dflash_gdn.h"
 #include "device_common.h"
 #include "host_common.h"
@@ -160,6 +161,72 @@ hipError_t launch_partial(const void* logits, int64_t bs, int64_t rs, int B, int
   return hipGetLastError();
 }
 
+// The accept's finalize and the conv-window rollback in one launch, grid
+// (column chunks, B, layers): every workgroup merges its sequence's argmax
+// keys (N rows x splits), prefix-compares
+// the draft as accept_finalize_kernel does, then copies its columns of the
+// window for a = matched + accepted_offset.  The workgroup (0, b, 0) of the
+// first launch (write_accept) also writes posterior / matched / bonus of b.
+// Dynamic LDS: N int32.
+template <typename U>
+__global__ __launch_bounds__(kConvThreads) void accept_conv_rollback_kernel(
+    const uint64_t* __restrict__ keys, int splits, int N, const int32_t* __restrict__ draft,
+    int64_t dstride, int n_draft, int32_t* __restrict__ posterior, int32_t* __restrict__ matched,
+    int32_t* __restrict__ bonus, int write_accept, int accepted_offset, const ConvTable tab, int T,
+    int K1, int64_t Cu, int64_t qkv_bs, int64_t qkv_rs) {
+  extern __shared__ int32_t post[];
+  __shared__ int s_first;
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  // 16 lanes per row, 16 rows per pass: every lane's key loads are issued
+  // together, then a max over its 16 lanes (exact, so order-free).
+  const int sub = threadIdx.x & 15;
+  for (int r0 = 0; r0 < N; r0 += kConvThreads / 16) {
+    const int r = r0 + (threadIdx.x >> 4);
+    uint64_t m = 0;
+    if (r < N) {
+      const uint64_t* kr = keys + ((int64_t)b * N + r) * splits;
+#pragma unroll 8
+      for (int s = sub; s < splits; s += 16) m = u64_max(m, kr[s]);
+    }
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) {
+      const uint32_t lo = __shfl_xor((unsigned)(m & 0xffffffffu), off, 16);
+      const uint32_t hi = __shfl_xor((unsigned)(m >> 32), off, 16);
+      m = u64_max(m, ((uint64_t)hi << 32) | lo);
+    }
+    if (sub == 0 && r < N) post[r] = argmax_key_index(m);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    const int mlen = min(n_draft, N);
+    int first = mlen;
+    for (int base0 = 0; base0 < mlen; base0 += 64) {
+      const int j = base0 + lane;
+      const bool mismatch = (j < mlen) && (draft[(int64_t)b * dstride + j] != post[j]);
+      const unsigned long long mask = __ballot(mismatch);
+      if (mask != 0ull) {
+        first = base0 + __ffsll(mask) - 1;
+        break;
+      }
+    }
+    if (lane == 0) s_first = first;
+  }
+  __syncthreads();
+  const int first = s_first;
+  if (write_accept && blockIdx.x == 0 && blockIdx.z == 0) {
+    if (posterior != nullptr)
+      for (int r = threadIdx.x; r < N; r += kConvThreads) posterior[(int64_t)b * N + r] = post[r];
+    if (threadIdx.x == 0) {
+      if (matched != nullptr) matched[b] = first;
+      if (bonus != nullptr) bonus[b] = first < N ? post[first] : -1;
+    }
+  }
+  conv_window_copy<U>(tab, blockIdx.z, b, min(max(first + accepted_offset, 0), T), K1, Cu,
+                      qkv_bs, qkv_rs);
+}
+
 }  // namespace
 }  // namespace dflash
 
@@ -202,4 +269,72 @@ extern "C" int dflash_greedy_accept(const void* logits, int logits_dtype,
   if (e != hipSuccess) return (int)e;
   return to_status(launch_accept_finalize(keys, sp.splits, B, N, draft, draft_stride, n_draft,
                                           posterior, matched, bonus, s));
+}
+
+extern "C" int dflash_greedy_accept_conv_rollback(
+    const void* logits, int logits_dtype, int64_t logits_batch_stride,
+    int64_t logits_row_stride, const int32_t* draft, int64_t draft_stride, int n_draft,
+    int32_t* posterior, int32_t* matched, int32_t* bonus, int B, int N, int V, void* workspace,
+    size_t workspace_bytes, const void* const* conv_in, const void* const* qkv,
+    void* const* conv_out, int accepted_offset, int L, int T, int K1, int64_t C,
+    int64_t qkv_batch_stride, int64_t qkv_row_stride, int elem_bytes, void* stream) {
+  using namespace dflash;
+  if (B < 0 || N <= 0 || V <= 0 || n_draft < 0) return DFLASH_ERR_SHAPE;
+  if (N > kMaxAcceptRows || (int64_t)B * N > INT32_MAX) return DFLASH_ERR_SHAPE;
+  if (L < 0 || T < 0 || K1 < 0 || C < 0 || B > 65535) return DFLASH_ERR_SHAPE;
+  if (K1 > kMaxConvRows) return DFLASH_ERR_UNSUPPORTED;
+  if (elem_bytes != 2 && elem_bytes != 4) return DFLASH_ERR_UNSUPPORTED;
+  if (B == 0) return DFLASH_OK;
+  if (logits == nullptr || workspace == nullptr) return DFLASH_ERR_NULL;
+  if (n_draft > 0 && draft == nullptr) return DFLASH_ERR_NULL;
+  if (logits_dtype != DFLASH_DTYPE_F32 && logits_dtype != DFLASH_DTYPE_BF16 &&
+      logits_dtype != DFLASH_DTYPE_F16)
+    return DFLASH_ERR_UNSUPPORTED;
+  if (workspace_bytes < dflash_greedy_accept_workspace_bytes(B, N, V)) return DFLASH_ERR_WORKSPACE;
+  if ((uintptr_t)workspace % 8 != 0) return DFLASH_ERR_ALIGN;
+  const bool conv = L > 0 && K1 > 0 && C > 0;
+  ConvPlan pl{2, 0, 0, 0};
+  if (conv) {
+    const int st = conv_plan(conv_in, qkv, conv_out, L, T, K1, C, qkv_batch_stride,
+                             qkv_row_stride, elem_bytes, &pl);
+    if (st != DFLASH_OK) return st;
+  }
+  const Split sp = plan_split(B, N, V);
+  uint64_t* keys = static_cast<uint64_t*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (logits_dtype == DFLASH_DTYPE_F32)
+    e = launch_partial<float>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, keys, s);
+  else if (logits_dtype == DFLASH_DTYPE_BF16)
+    e = launch_partial<uint16_t>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, keys, s);
+  else
+    e = launch_partial<F16Tag>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, keys, s);
+  if (e != hipSuccess) return (int)e;
+  if (!conv) {
+    if (posterior == nullptr && matched == nullptr && bonus == nullptr) return DFLASH_OK;
+    return to_status(launch_accept_finalize(keys, sp.splits, B, N, draft, draft_stride, n_draft,
+                                            posterior, matched, bonus, s));
+  }
+  const size_t lds = sizeof(int32_t) * (size_t)N;
+  for (int l0 = 0; l0 < L; l0 += kMaxLayersPerLaunch) {
+    const int nl = L - l0 < kMaxLayersPerLaunch ? L - l0 : kMaxLayersPerLaunch;
+    const ConvTable tab = conv_table(conv_in, qkv, conv_out, l0, nl);
+    const dim3 grid(copy_grid_chunks(pl.Cu, kConvThreads, B, nl), B, nl);
+    const int first = l0 == 0;
+    if (pl.unit == 16)
+      hipLaunchKernelGGL(accept_conv_rollback_kernel<u32x4>, grid, dim3(kConvThreads), lds, s,
+                         keys, sp.splits, N, draft, draft_stride, n_draft, posterior, matched,
+                         bonus, first, accepted_offset, tab, T, K1, pl.Cu, pl.qbs, pl.qrs);
+    else if (pl.unit == 4)
+      hipLaunchKernelGGL(accept_conv_rollback_kernel<uint32_t>, grid, dim3(kConvThreads), lds, s,
+                         keys, sp.splits, N, draft, draft_stride, n_draft, posterior, matched,
+                         bonus, first, accepted_offset, tab, T, K1, pl.Cu, pl.qbs, pl.qrs);
+    else
+      hipLaunchKernelGGL(accept_conv_rollback_kernel<uint16_t>, grid, dim3(kConvThreads), lds, s,
+                         keys, sp.splits, N, draft, draft_stride, n_draft, posterior, matched,
+                         bonus, first, accepted_offset, tab, T, K1, pl.Cu, pl.qbs, pl.qrs);
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+  }
+  return DFLASH_OK;
 }

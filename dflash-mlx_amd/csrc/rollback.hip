@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "conv_window.h"
 #include "dflash_gdn.h"
 #include "device_common.h"
 #include "host_common.h"
@@ -66,52 +67,15 @@ __global__ __launch_bounds__(kCopyThreads) void tape_select_kernel(
   }
 }
 
-struct ConvTable {
-  const char* cin[kMaxLayersPerLaunch];
-  const char* qkv[kMaxLayersPerLaunch];
-  char* cout[kMaxLayersPerLaunch];
-};
-
-constexpr int kMaxConvRows = 8;
-
-// grid: (column chunks, B, layers).  One lane owns one column unit of one
-// (layer, sequence) for all K1 rows: it reads every source row before it
-// writes, so conv_out may alias conv_in.
+// grid: (column chunks, B, layers).
 template <typename U>
-__global__ __launch_bounds__(kCopyThreads) void conv_rollback_kernel(
+__global__ __launch_bounds__(kConvThreads) void conv_rollback_kernel(
     const ConvTable tab, const int32_t* __restrict__ accepted, int T, int K1,
     int64_t Cu, int64_t qkv_bs, int64_t qkv_rs) {
-  const int l = blockIdx.z;
   const int b = blockIdx.y;
-  const int a = min(max(accepted[b], 0), T);
-  const U* cin = reinterpret_cast<const U*>(tab.cin[l]) + (int64_t)b * K1 * Cu;
-  const U* qkv = reinterpret_cast<const U*>(tab.qkv[l]) + (int64_t)b * qkv_bs;
-  U* cout = reinterpret_cast<U*>(tab.cout[l]) + (int64_t)b * K1 * Cu;
-  for (int64_t c = (int64_t)blockIdx.x * kCopyThreads + threadIdx.x; c < Cu;
-       c += (int64_t)gridDim.x * kCopyThreads) {
-    U vals[kMaxConvRows];
-#pragma unroll
-    for (int r = 0; r < kMaxConvRows; ++r) {
-      if (r < K1) {
-        const int j = a + r;
-        vals[r] = j < K1 ? cin[(int64_t)j * Cu + c] : qkv[(int64_t)(j - K1) * qkv_rs + c];
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < kMaxConvRows; ++r)
-      if (r < K1) cout[(int64_t)r * Cu + c] = vals[r];
-  }
+  conv_window_copy<U>(tab, blockIdx.z, b, min(max(accepted[b], 0), T), K1, Cu, qkv_bs, qkv_rs);
 }
 
-int grid_chunks(int64_t units, int per_block, int B, int L) {
-  // Aim for ~2048 workgroups in total; at least one per (sequence, layer).
-  int64_t want = ceil_div(2048, (int64_t)B * L);
-  const int64_t most = ceil_div(units, per_block);
-  if (want > most) want = most;
-  if (want < 1) want = 1;
-  if (want > 65535) want = 65535;
-  return (int)want;
-}
 
 }  // namespace
 }  // namespace dflash
@@ -149,7 +113,7 @@ extern "C" int dflash_tape_select(const float* const* tapes,
       tab.sin[j] = states_in[l0 + j];
       tab.sout[j] = states_out[l0 + j];
     }
-    dim3 grid(grid_chunks(units, kCopyThreads * kCopyUnroll, B, nl), B, nl);
+    dim3 grid(copy_grid_chunks(units, kCopyThreads * kCopyUnroll, B, nl), B, nl);
     if (vec)
       hipLaunchKernelGGL(tape_select_kernel<4>, grid, dim3(kCopyThreads), 0, s, tab, accepted, T,
                          state_elems, tstride);
@@ -173,41 +137,25 @@ extern "C" int dflash_conv_rollback(const void* const* conv_in, const void* cons
   if (elem_bytes != 2 && elem_bytes != 4) return DFLASH_ERR_UNSUPPORTED;
   if (L == 0 || B == 0 || K1 == 0 || C == 0) return DFLASH_OK;
   if (B > 65535) return DFLASH_ERR_SHAPE;
-  if (conv_in == nullptr || qkv == nullptr || conv_out == nullptr || accepted == nullptr)
-    return DFLASH_ERR_NULL;
-  const int64_t row_bytes = C * elem_bytes;
-  bool vec = (row_bytes % 16 == 0) && ((qkv_batch_stride * elem_bytes) % 16 == 0) &&
-             ((qkv_row_stride * elem_bytes) % 16 == 0);
-  for (int l = 0; l < L; ++l) {
-    if (conv_in[l] == nullptr || (T > 0 && qkv[l] == nullptr) || conv_out[l] == nullptr)
-      return DFLASH_ERR_NULL;
-    const uintptr_t any = (uintptr_t)conv_in[l] | (uintptr_t)qkv[l] | (uintptr_t)conv_out[l];
-    if (any & 15) vec = false;
-    if (any & (uintptr_t)(elem_bytes - 1)) return DFLASH_ERR_ALIGN;
-  }
+  if (accepted == nullptr) return DFLASH_ERR_NULL;
+  ConvPlan pl;
+  const int st = conv_plan(conv_in, qkv, conv_out, L, T, K1, C, qkv_batch_stride, qkv_row_stride,
+                           elem_bytes, &pl);
+  if (st != DFLASH_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const int unit = vec ? 16 : elem_bytes;
-  const int64_t Cu = row_bytes / unit;
-  const int64_t qbs = qkv_batch_stride * elem_bytes / unit;
-  const int64_t qrs = qkv_row_stride * elem_bytes / unit;
   for (int l0 = 0; l0 < L; l0 += kMaxLayersPerLaunch) {
     const int nl = L - l0 < kMaxLayersPerLaunch ? L - l0 : kMaxLayersPerLaunch;
-    ConvTable tab{};
-    for (int j = 0; j < nl; ++j) {
-      tab.cin[j] = static_cast<const char*>(conv_in[l0 + j]);
-      tab.qkv[j] = static_cast<const char*>(qkv[l0 + j]);
-      tab.cout[j] = static_cast<char*>(conv_out[l0 + j]);
-    }
-    dim3 grid(grid_chunks(Cu, kCopyThreads, B, nl), B, nl);
-    if (unit == 16)
-      hipLaunchKernelGGL(conv_rollback_kernel<u32x4>, grid, dim3(kCopyThreads), 0, s, tab,
-                         accepted, T, K1, Cu, qbs, qrs);
-    else if (unit == 4)
-      hipLaunchKernelGGL(conv_rollback_kernel<uint32_t>, grid, dim3(kCopyThreads), 0, s, tab,
-                         accepted, T, K1, Cu, qbs, qrs);
+    const ConvTable tab = conv_table(conv_in, qkv, conv_out, l0, nl);
+    dim3 grid(copy_grid_chunks(pl.Cu, kConvThreads, B, nl), B, nl);
+    if (pl.unit == 16)
+      hipLaunchKernelGGL(conv_rollback_kernel<u32x4>, grid, dim3(kConvThreads), 0, s, tab,
+                         accepted, T, K1, pl.Cu, pl.qbs, pl.qrs);
+    else if (pl.unit == 4)
+      hipLaunchKernelGGL(conv_rollback_kernel<uint32_t>, grid, dim3(kConvThreads), 0, s, tab,
+                         accepted, T, K1, pl.Cu, pl.qbs, pl.qrs);
     else
-      hipLaunchKernelGGL(conv_rollback_kernel<uint16_t>, grid, dim3(kCopyThreads), 0, s, tab,
-                         accepted, T, K1, Cu, qbs, qrs);
+      hipLaunchKernelGGL(conv_rollback_kernel<uint16_t>, grid, dim3(kConvThreads), 0, s, tab,
+                         accepted, T, K1, pl.Cu, pl.qbs, pl.qrs);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }

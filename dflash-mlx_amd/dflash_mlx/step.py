@@ -132,7 +132,11 @@ class VerifyStepRunner:
             couts = _lib.ptr_array(self.conv_out)
             self._conv_args = (cins, qkvs, couts, self.matched.data_ptr(), s.L, s.B, s.T, s.K1,
                                s.conv_dim, s.T * s.conv_dim, s.conv_dim, 2)
+            # accept + conv rollback in two launches (finalize inside the copy)
+            self._accept_conv_args = self._accept_args + (
+                cins, qkvs, couts, 0, s.L, s.T, s.K1, s.conv_dim, s.T * s.conv_dim, s.conv_dim, 2)
         lib = _lib.load()
+        self._accept_conv = lib.dflash_greedy_accept_conv_rollback
         self._scan = lib.dflash_gdn_verify_scan
         self._scan_rb = lib.dflash_gdn_verify_scan_rollback
         self._accept = lib.dflash_greedy_accept
@@ -162,6 +166,15 @@ class VerifyStepRunner:
         if self.shape.conv_dim:
             _lib.check("dflash_conv_rollback", self._conv(*self._conv_args, stream or self._stream()))
 
+    def accept_conv_rollback(self, stream: int | None = None) -> None:
+        """accept() then conv_rollback(), as two launches instead of three."""
+        st = stream or self._stream()
+        if not self.shape.conv_dim:
+            self.accept(st)
+            return
+        _lib.check("dflash_greedy_accept_conv_rollback",
+                   self._accept_conv(*self._accept_conv_args, st))
+
     def run(self) -> None:
         """Explicit form: scan (with final state) -> accept -> gather rollback."""
         st = self._stream()
@@ -177,8 +190,7 @@ class VerifyStepRunner:
         run_fused() picks up on the device.  Start with matched zeroed."""
         st = self._stream()
         self.scan_rolled(st)
-        self.accept(st)
-        self.conv_rollback(st)
+        self.accept_conv_rollback(st)
 
     def rolled_back_state(self) -> torch.Tensor:
         """Materialise the state the next fused step starts from (test helper;

@@ -364,6 +364,32 @@ int dflash_conv_rollback(const void* const* conv_in, const void* const* qkv,
                          int elem_bytes, void* stream);
 
 /*
+ * dflash_greedy_accept followed by dflash_conv_rollback with
+ * accepted[b] = matched[b] + accepted_offset, in two launches instead of
+ * three: the accept's finalize (key merge, prefix compare, bonus) runs inside
+ * the conv-window copy's workgroups, each of which needs its sequence's
+ * accepted count anyway.
+ *
+ * Replaces the accept of verify_block_parallel_replay (dflash_mlx/runtime.py:
+ * 134-147: argmax, longest_prefix_match, bonus) and the conv half of the
+ * rollback that follows it (custom_qwen35_model.py:1044-1051); the reference
+ * has no single call for the pair.  accepted_offset is 1 to roll back to
+ * accepted_inputs = matched + 1 (runtime.py:146), 0 to keep matched tokens.
+ * Arguments and outputs as the two calls (posterior and bonus may be NULL);
+ * the outputs are bit-identical to theirs.  With L, K1 or C zero only the
+ * accept runs.
+ */
+int dflash_greedy_accept_conv_rollback(
+    const void* logits, int logits_dtype, int64_t logits_batch_stride,
+    int64_t logits_row_stride, const int32_t* draft, int64_t draft_stride,
+    int n_draft, int32_t* posterior, int32_t* matched, int32_t* bonus, int B,
+    int N, int V, void* workspace, size_t workspace_bytes,
+    const void* const* conv_in, const void* const* qkv, void* const* conv_out,
+    int accepted_offset, int L, int T, int K1, int64_t C,
+    int64_t qkv_batch_stride, int64_t qkv_row_stride, int elem_bytes,
+    void* stream);
+
+/*
  * ---- The rest of the hybrid target's verify step (config c4) ----
  * Cache lengths `lens` are int32 [B] in device memory, so a whole verify step
  * (append, attend, accept, commit) needs no host round trip.

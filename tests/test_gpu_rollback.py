@@ -261,3 +261,50 @@ def test_step_runner_fused_matches_explicit(device):
     assert torch.equal(explicit.tape, fused.tape)
     assert torch.equal(explicit.out, fused.out)
     assert torch.equal(fused.rolled_back_state(), explicit.new_state)
+
+
+@pytest.mark.parametrize("B,N,V,L,K1,C,offset,dtype", [
+    (1, 16, 151936, 24, 3, 8192, 0, torch.float32),   # the c1 step: 24 layers, 16-byte units
+    (3, 16, 3000, 2, 3, 100, 1, torch.bfloat16),      # ragged C (2-byte units), keep = matched + 1
+    (2, 5, 1000, 40, 2, 64, 1, torch.float16),        # more layers than one launch holds
+])
+def test_accept_conv_rollback_matches_two_calls(device, B, N, V, L, K1, C, offset, dtype):
+    """dflash_greedy_accept_conv_rollback (finalize inside the window copy)
+    gives the bits of dflash_greedy_accept then dflash_conv_rollback with
+    accepted = matched + offset: posterior, matched, bonus and every window."""
+    import ctypes
+
+    from dflash_mlx import _lib, greedy_accept
+
+    print(f"[accept+conv B={B} N={N} V={V} L={L} K1={K1} C={C} offset={offset} {dtype}]", flush=True)
+    gen = torch.Generator().manual_seed(B * 131 + L)
+    logits = torch.randn(B, N, V, generator=gen).to(dtype)
+    am = logits.float().argmax(-1).to(torch.int32)
+    accept = torch.randint(0, N + 1, (B,), generator=gen, dtype=torch.int32)
+    pos = torch.arange(N, dtype=torch.int32)[None, :]
+    draft = torch.where(pos < accept[:, None], am, (am + 1) % V).to(torch.int32)
+    conv = [torch.randn(B, K1, C, generator=gen).bfloat16() for _ in range(L)]
+    qkv = [torch.randn(B, N, C, generator=gen).bfloat16() for _ in range(L)]
+    ld, dd = logits.to(device), draft.to(device)
+
+    post_a, m_a, b_a = greedy_accept(ld, dd)
+    conv_a = conv_rollback([c.to(device) for c in conv], [q.to(device) for q in qkv], m_a + offset)
+
+    lib = _lib.load()
+    ws = torch.empty(int(lib.dflash_greedy_accept_workspace_bytes(B, N, V)), dtype=torch.uint8,
+                     device=device)
+    post_b = torch.full((B, N), -7, dtype=torch.int32, device=device)
+    m_b = torch.full((B,), -7, dtype=torch.int32, device=device)
+    b_b = torch.full((B,), -7, dtype=torch.int32, device=device)
+    cin = [c.to(device) for c in conv]
+    qd = [q.to(device) for q in qkv]
+    cout = [torch.empty_like(c) for c in cin]
+    _lib.call("dflash_greedy_accept_conv_rollback", ld.data_ptr(), _lib.dtype_tag(dtype), N * V, V,
+              dd.data_ptr(), N, N, post_b.data_ptr(), m_b.data_ptr(), b_b.data_ptr(), B, N, V,
+              ws.data_ptr(), ws.numel(), _lib.ptr_array(cin), _lib.ptr_array(qd),
+              _lib.ptr_array(cout), offset, L, N, K1, C, N * C, C, 2, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    assert m_b.cpu().tolist() == accept.tolist()
+    assert torch.equal(post_a, post_b) and torch.equal(m_a, m_b) and torch.equal(b_a, b_b)
+    for l in range(L):
+        assert torch.equal(conv_a[l], cout[l]), f"layer {l}"
