@@ -58,6 +58,9 @@ constexpr int TPF = 68;  // fp32 row pitch of A / T in LDS
 //   P_HI / P_LO: bf16 fragments [4 it][2 s]: P[16it + r][32s+16t+4g+e]
 //   UT:          fp32 [8 rb][4 it][64 lane][4]: U~[16it + 4(lane/16) + e][16rb + lane%16]
 //   EG:          fp32 [64] exp(G_i);  ED: fp32 [64] exp(G_63 - G_i)  (decays)
+// Q and KT depend on the key head only: they are stored in the slots of the
+// first value head of each key head (hv % rep == 0) and read from there by
+// every value head of the group; the other heads' Q / KT slots stay unused.
 constexpr size_t kWHi = 0;
 constexpr size_t kWLo = kWHi + CH * D * 2;
 constexpr size_t kQ = kWLo + CH * D * 2;
@@ -216,8 +219,11 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   u32x4(*sKf)[64] = reinterpret_cast<u32x4(*)[64]>(&sT[0][0]);
 #pragma unroll
   for (int s = 0; s < 4; ++s) sKf[wave * 4 + s][lane] = kf[s];
+  // Q and K^T depend on the key head only: the first value head of each key
+  // head stores them, the others read that head's (phase 2, qk_base).
+  const bool own_qk = hv % p.rep == 0;
   // Q fragments go to the workspace as loaded.
-  {
+  if (own_qk) {
     u32x4* qw = reinterpret_cast<u32x4*>(ws + kQ);
 #pragma unroll
     for (int s = 0; s < 4; ++s) qw[(wave * 4 + s) * 64 + lane] = qf[s];
@@ -284,7 +290,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
     }
   }
   // K^T fragments [8 dt][2 s]: 16 bytes per (dk, s, g).
-  {
+  if (own_qk) {
     uint16_t* kt = reinterpret_cast<uint16_t*>(ws + kKT);
     for (int e = tid; e < D * 8; e += 256) {
       const int dk = e >> 3, s = (e >> 2) & 1, g = e & 3;
@@ -461,11 +467,14 @@ __device__ __forceinline__ void load_kt(const uint8_t* wsc, uint32_t lf, u32x4 (
   }
 }
 
-__device__ __forceinline__ void load_q(const uint8_t* wsc, uint32_t lf, uint32_t ld, QOps& o) {
+// wsq: the chunk slot holding Q (the key head's first value head), wsc: this
+// value head's slot (P, EG).
+__device__ __forceinline__ void load_q(const uint8_t* wsq, const uint8_t* wsc, uint32_t lf,
+                                       uint32_t ld, QOps& o) {
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) o.q[it][s] = ld16(wsc + kQ + lf + (it * 4 + s) * 1024);
+    for (int s = 0; s < 4; ++s) o.q[it][s] = ld16(wsq + kQ + lf + (it * 4 + s) * 1024);
 #pragma unroll
     for (int s = 0; s < (it < 2 ? 1 : 2); ++s) {
       o.ph[it][s] = ld16(wsc + kPHi + lf + (it * 2 + s) * 1024);
@@ -498,6 +507,13 @@ __device__ __forceinline__ void store_out(uint16_t* obase, int64_t row_stride, f
     if (!GUARD || row0 + e < nvalid) obase[(row0 + e) * row_stride] = v[e];
 }
 
+// Workspace of the first value head sharing bh's key head: its slots hold
+// the Q and K^T fragments of every value head of the group.
+__device__ __forceinline__ const uint8_t* qk_base(const ChunkParams& p, int bh) {
+  const int hv = bh % p.Hv;
+  return p.ws + (int64_t)(bh - hv % p.rep) * p.NC * kWsChunk;
+}
+
 __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb, int lane,
                                            Exchange* xb) {
   const int r16 = lane & 15;
@@ -506,6 +522,7 @@ __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb,
   const uint32_t lu = rb * 4096 + lane * 16;  // U~
   const uint32_t ld = g4 * 16;                // ED
   const uint8_t* ws0 = p.ws + (int64_t)bh * p.NC * kWsChunk;
+  const uint8_t* wk0 = qk_base(p, bh);
   const int last = p.NC - 1;
 
   f32x4 sT[8];
@@ -517,7 +534,7 @@ __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb,
   WOps w;
   u32x4 kt[8][2];
   load_w(ws0, lf, w);
-  load_kt(ws0, lf, kt);
+  load_kt(wk0, lf, kt);
   for (int c = 0; c < p.NC; ++c) {
     // Chunks past the last re-read the last one: the loads stay unconditional.
     const uint8_t* wsc = ws0 + (int64_t)c * kWsChunk;
@@ -582,7 +599,7 @@ __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb,
       sT[dt] = a;
     }
     __builtin_amdgcn_sched_barrier(0);
-    load_kt(wsn, lf, kt);
+    load_kt(wk0 + (int64_t)min(c + 1, last) * kWsChunk, lf, kt);
     __builtin_amdgcn_sched_barrier(0);
   }
   if (p.final_state != nullptr) {
@@ -601,6 +618,7 @@ __device__ __forceinline__ void output_wave(const ChunkParams& p, int bh, int rb
   const int b = bh / p.Hv;
   const int hv = bh - b * p.Hv;
   const uint8_t* ws0 = p.ws + (int64_t)bh * p.NC * kWsChunk;
+  const uint8_t* wk0 = qk_base(p, bh);
   const int last = p.NC - 1;
   const int64_t orow = (int64_t)p.Hv * D;  // out row stride (elements)
 
@@ -611,16 +629,19 @@ __device__ __forceinline__ void output_wave(const ChunkParams& p, int bh, int rb
   // that chunk's own loads, so in-order completion never holds them up.
   const uint32_t t0o = min((uint32_t)((rb * 113 + lane) * 128), (uint32_t)(kWsChunk - 4));
   const uint32_t t1o = min((uint32_t)((rb * 113 + min(lane + 64, 112)) * 128), (uint32_t)(kWsChunk - 4));
+  // Lines of the Q / K^T range are touched in the key head's slot.
+  const uint8_t* t0b = (t0o >= kQ && t0o < kPHi) ? wk0 : ws0;
+  const uint8_t* t1b = (t1o >= kQ && t1o < kPHi) ? wk0 : ws0;
   QOps qo;
-  load_q(ws0, lf, ld, qo);
+  load_q(wk0, ws0, lf, ld, qo);
   // The first touches (chunk 2) go after chunk 0's Q / P loads, as in the
   // loop, so the wait for Q / P at the loop head counts the same on entry.
   __builtin_amdgcn_sched_barrier(0);
   uint32_t ta, tb;
   {
-    const uint32_t* tq = reinterpret_cast<const uint32_t*>(ws0 + (int64_t)min(2, last) * kWsChunk);
-    ta = tq[t0o >> 2];
-    tb = tq[t1o >> 2];
+    const int64_t co = (int64_t)min(2, last) * kWsChunk;
+    ta = *reinterpret_cast<const uint32_t*>(t0b + co + t0o);
+    tb = *reinterpret_cast<const uint32_t*>(t1b + co + t1o);
   }
   __builtin_amdgcn_sched_barrier(0);
   for (int c = 0; c < p.NC; ++c) {
@@ -666,14 +687,16 @@ __device__ __forceinline__ void output_wave(const ChunkParams& p, int bh, int rb
     // Loads after the stores: waiting for them next chunk never depends on
     // how many stores the guarded path issued.
     __builtin_amdgcn_sched_barrier(0);
-    load_q(ws0 + (int64_t)min(c + 1, last) * kWsChunk, lf, ld, qo);  // this chunk's Q, P consumed
+    {  // this chunk's Q, P consumed
+      const int64_t cn = (int64_t)min(c + 1, last) * kWsChunk;
+      load_q(wk0 + cn, ws0 + cn, lf, ld, qo);
+    }
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::"v"(ta), "v"(tb));
     {
-      const uint32_t* tq =
-          reinterpret_cast<const uint32_t*>(ws0 + (int64_t)min(c + 3, last) * kWsChunk);
-      ta = tq[t0o >> 2];
-      tb = tq[t1o >> 2];
+      const int64_t co = (int64_t)min(c + 3, last) * kWsChunk;
+      ta = *reinterpret_cast<const uint32_t*>(t0b + co + t0o);
+      tb = *reinterpret_cast<const uint32_t*>(t1b + co + t1o);
     }
     __builtin_amdgcn_sched_barrier(0);
   }

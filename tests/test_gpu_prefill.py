@@ -47,6 +47,7 @@ SMALL = [
     _cfg(CONFIGS[3], B=2, T=64, Hk=2, Hv=2, state_std=0.05),  # one full chunk, B=2
     _cfg(CONFIGS[3], T=1, Hk=1, Hv=2, state_std=0.05),     # single token
     _cfg(CONFIGS[3], T=129, Hk=4, Hv=4),                   # zero state, 1 token past 2 chunks
+    _cfg(CONFIGS[3], B=2, T=130, Hk=1, Hv=4, state_std=0.05),  # 4 value heads share Q / K^T
 ]
 
 
