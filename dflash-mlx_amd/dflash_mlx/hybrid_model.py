@@ -227,9 +227,11 @@ class HybridVerifyRunner:
     # partials where the next add + RMSNorm sums them.
     GEMM_PLAN = {"w_in": (1, 32, 4), "w_out": (8, 16, 4), "w_qkv": (1, 32, 4),
                  "w_o": (8, 32, 4), "w_gu": (1, 32, 4), "w_down": (8, 32, 4)}
-    # the same for fragment-tiled weights (rows_per_wave 64 exists only there)
+    # the same for fragment-tiled weights (rows_per_wave 64 exists only
+    # there); down's 6 splits (24 of its 144 k-steps each, 6 per wave) beat 8
+    # by ~30 us per c4 step when timed inside the whole graph-captured step
     TILED_PLAN = {"w_in": (1, 64, 4), "w_out": (8, 32, 4), "w_qkv": (1, 32, 4),
-                  "w_o": (8, 16, 4), "w_gu": (1, 32, 4), "w_down": (8, 32, 4)}
+                  "w_o": (8, 16, 4), "w_gu": (1, 32, 4), "w_down": (6, 32, 4)}
 
     def _build_gemms(self):
         """Argument tuples of every projection GEMM, and the split-K partial
