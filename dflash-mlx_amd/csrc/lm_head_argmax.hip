@@ -228,8 +228,8 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_argmax_tiled_kernel(const 
     const int64_t woff = (int64_t)ks * tiles * 1024;
 #pragma unroll
     for (int vt = 0; vt < VT; ++vt) {
-      st.a[2 * vt] = *reinterpret_cast<const u32x4*>(wrow[vt] + woff);
-      st.a[2 * vt + 1] = *reinterpret_cast<const u32x4*>(wrow[vt] + woff + 512);
+      st.a[2 * vt] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[vt] + woff));
+      st.a[2 * vt + 1] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(wrow[vt] + woff + 512));
     }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {

@@ -19,7 +19,8 @@
 //   - Tiled weights (dflash_weight_tile_bf16, once at load time): the weight
 //     stored as those A fragments, [K/64 k-steps][N/16 row tiles][2 halves]
 //     [64 lanes][8], so every fragment is one contiguous 1 KB load straight
-//     into MFMA registers (no LDS step), and the workgroups in flight, which
+//     into MFMA registers (no LDS step; nontemporal loads, measured 2-7 %
+//     faster per projection than ordinary ones), and the workgroups in flight, which
 //     walk their k-ranges in step, read within a narrow window of memory (a
 //     few pages) rather than each in its own region.  Same k-slots, so the
 //     same sums, bit for bit, as the row-major path.
@@ -119,7 +120,10 @@ __global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams
     const int off = ks * kGKStep;
     const int64_t woff = TILED ? (int64_t)ks * (p.N / 16) * 1024 : off;
 #pragma unroll
-    for (int i = 0; i < 2 * VT; ++i) st.a[i] = *reinterpret_cast<const u32x4*>(wrow[i] + woff);
+    for (int i = 0; i < 2 * VT; ++i) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(wrow[i] + woff);
+      st.a[i] = TILED ? __builtin_nontemporal_load(src) : *src;
+    }
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       st.b[mt][0] = *reinterpret_cast<const u32x4*>(xrow[mt] + off);
