@@ -162,7 +162,11 @@ struct NormParams {
   float eps;
 };
 
-// One wavefront per (b, t, h) row of D channels; 4 rows per workgroup.
+// One wavefront per (b, t, h) row of D = 64 * PER channels; 4 rows per
+// workgroup.  Lane l holds channels l, l + 64, ...; its x, z and weight loads
+// all go out before the row's sum of squares (one round of memory latency in
+// a kernel that is nothing but latency at verify sizes).
+template <int PER>
 __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const NormParams p) {
   const int lane = threadIdx.x & 63;
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -173,19 +177,21 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const NormParams p) 
   const int b = bt / p.T;
   const uint16_t* x = p.x + (int64_t)row * p.D;
   const uint16_t* z = p.z + b * p.z_sb + (int64_t)t * p.z_st + (int64_t)h * p.z_sh;
-  const int per = p.D / 64;
-  float xv[4];
-  float ss = 0.f;
-  for (int i = 0; i < per; ++i) {
+  float xv[PER], zv[PER], wv[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
     xv[i] = ldbf(x + i * 64 + lane);
-    ss = fmaf(xv[i], xv[i], ss);
+    zv[i] = ldbf(z + i * 64 + lane);
+    wv[i] = ldbf(p.w + i * 64 + lane);
   }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) ss = fmaf(xv[i], xv[i], ss);
   ss = pro_wave_sum(ss);
   const float r = rsqrtf(ss / (float)p.D + p.eps);
-  for (int i = 0; i < per; ++i) {
-    const int c = i * 64 + lane;
-    p.y[(int64_t)row * p.D + c] = f32_to_bf16_rne(xv[i] * r * ldbf(p.w + c) * pro_silu(ldbf(z + c)));
-  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i)
+    p.y[(int64_t)row * p.D + i * 64 + lane] = f32_to_bf16_rne(xv[i] * r * wv[i] * pro_silu(zv[i]));
 }
 
 }  // namespace
@@ -278,7 +284,13 @@ extern "C" int dflash_gdn_gated_rmsnorm(const void* x, const void* z, const int6
   p.D = D;
   p.rows = B * T * H;
   p.eps = eps;
-  hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3((unsigned)ceil_div(p.rows, 4)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), p);
+  const dim3 grid((unsigned)ceil_div(p.rows, 4));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (D / 64) {
+    case 1: hipLaunchKernelGGL(gated_rmsnorm_kernel<1>, grid, dim3(256), 0, s, p); break;
+    case 2: hipLaunchKernelGGL(gated_rmsnorm_kernel<2>, grid, dim3(256), 0, s, p); break;
+    case 3: hipLaunchKernelGGL(gated_rmsnorm_kernel<3>, grid, dim3(256), 0, s, p); break;
+    default: hipLaunchKernelGGL(gated_rmsnorm_kernel<4>, grid, dim3(256), 0, s, p); break;
+  }
   return to_status(hipGetLastError());
 }

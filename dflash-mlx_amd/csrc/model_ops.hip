@@ -90,6 +90,7 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(const uint16_t* x, co
   const bool live = ch < (H >> 3);
   const int chc = live ? ch : 0;  // idle threads load chunk 0 and drop it
   const int64_t xrow = tok != nullptr ? (int64_t)min(max(tok[row], 0), vocab - 1) : row;
+  const u32x4 wraw = ld16(w + chc * 8);  // the norm weight, up front with the row's loads
   float v[8];
   unpack8(ld16(x + xrow * H + chc * 8), v);
   if (PART) {
@@ -139,7 +140,7 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(const uint16_t* x, co
     if ((PART || r != nullptr || tok != nullptr) && h_out != nullptr)
       *reinterpret_cast<u32x4*>(h_out + (int64_t)row * H + ch * 8) = pack8(v);
     float wv[8], o[8];
-    unpack8(ld16(w + ch * 8), wv);
+    unpack8(wraw, wv);
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = v[e] * inv * wv[e];
     *reinterpret_cast<u32x4*>(y + (int64_t)row * H + ch * 8) = pack8(o);
