@@ -221,10 +221,10 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const AttnPrepParams p) 
   const int h = is_q ? slot : slot - p.Hq;
   const uint16_t* src = is_q ? row + h * 2 * kHD : row + p.Hq * 2 * kHD + h * kHD;
   const uint32_t xv = *reinterpret_cast<const uint32_t*>(src + d0);
+  const uint32_t wv = *reinterpret_cast<const uint32_t*>((is_q ? p.q_norm_w : p.k_norm_w) + d0);
   float x0 = bf16_lo(xv), x1 = bf16_hi(xv);
   const float ss = wave_sum(x0 * x0 + x1 * x1);
   const float inv = 1.f / sqrtf(ss / (float)kHD + p.eps);
-  const uint32_t wv = *reinterpret_cast<const uint32_t*>((is_q ? p.q_norm_w : p.k_norm_w) + d0);
   x0 = x0 * inv * bf16_lo(wv);
   x1 = x1 * inv * bf16_hi(wv);
   if (p.rot > 0) {
