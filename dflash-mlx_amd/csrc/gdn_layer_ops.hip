@@ -209,6 +209,9 @@ extern "C" int dflash_gdn_prologue(const void* qkv, int64_t qkv_batch_stride,
     return DFLASH_ERR_SHAPE;
   if (Hv % Hk != 0) return DFLASH_ERR_SHAPE;
   if (Dk % 64 != 0 || Dk > 256) return DFLASH_ERR_UNSUPPORTED;
+  // grid.x = B * T; channel indices are int
+  if ((int64_t)B * T > INT32_MAX || 2LL * Hk * Dk + (int64_t)Hv * Dv > INT32_MAX)
+    return DFLASH_ERR_SHAPE;
   if (B == 0 || T == 0) return DFLASH_OK;
   if (qkv == nullptr || (K > 1 && conv_state == nullptr) || conv_weight == nullptr ||
       a == nullptr || b == nullptr || A_log == nullptr || dt_bias == nullptr || act == nullptr ||
@@ -266,6 +269,7 @@ extern "C" int dflash_gdn_gated_rmsnorm(const void* x, const void* z, const int6
   using namespace dflash;
   if (B < 0 || T < 0 || H <= 0 || D <= 0) return DFLASH_ERR_SHAPE;
   if (D % 64 != 0 || D > 256) return DFLASH_ERR_UNSUPPORTED;
+  if ((int64_t)B * T * H > INT32_MAX) return DFLASH_ERR_SHAPE;  // rows are int
   if (B == 0 || T == 0) return DFLASH_OK;
   if (x == nullptr || z == nullptr || weight == nullptr || y == nullptr) return DFLASH_ERR_NULL;
   if (((uintptr_t)x | (uintptr_t)z | (uintptr_t)weight | (uintptr_t)y) & 1) return DFLASH_ERR_ALIGN;

@@ -589,6 +589,7 @@ extern "C" int dflash_attn_prep(const void* proj, int64_t proj_row_stride, const
   if (!(rot_dims == 0 || rot_dims == 16 || rot_dims == 32 || rot_dims == 64 || rot_dims == 128))
     return DFLASH_ERR_UNSUPPORTED;
   if (proj_row_stride < (int64_t)(2 * Hq + 2 * Hkv) * D) return DFLASH_ERR_SHAPE;
+  if ((int64_t)B * T > INT32_MAX) return DFLASH_ERR_SHAPE;  // grid.x = B * T
   if (B == 0 || T == 0) return DFLASH_OK;
   if (proj == nullptr || q_norm_w == nullptr || k_norm_w == nullptr || lens == nullptr ||
       k_cache == nullptr || vt_cache == nullptr || q_out == nullptr)
@@ -629,6 +630,7 @@ extern "C" int dflash_attn_verify(const void* q, const void* k_cache, const void
     return DFLASH_ERR_SHAPE;
   if (D != kHD) return DFLASH_ERR_UNSUPPORTED;
   if (Smax <= 0 || Smax % KC != 0 || max_len <= 0 || max_len > Smax) return DFLASH_ERR_SHAPE;
+  if (B > 65535) return DFLASH_ERR_SHAPE;  // grid.z of the partials = B
   if (B == 0 || T == 0) return DFLASH_OK;
   if (q == nullptr || k_cache == nullptr || vt_cache == nullptr || lens == nullptr ||
       gate_src == nullptr || out == nullptr || workspace == nullptr)

@@ -37,7 +37,9 @@ extern "C" {
 /* Argument-validation codes (negative).  Positive values are hipError_t. */
 #define DFLASH_OK 0
 #define DFLASH_ERR_NULL (-1)        /* a required pointer is NULL              */
-#define DFLASH_ERR_SHAPE (-2)       /* a size is out of range or inconsistent  */
+#define DFLASH_ERR_SHAPE (-2)       /* a size is out of range or inconsistent
+                                       (also: a row or workgroup count that
+                                       would not fit in int)                 */
 #define DFLASH_ERR_UNSUPPORTED (-3) /* head dim / dtype not compiled in        */
 #define DFLASH_ERR_ALIGN (-4)       /* pointer or stride breaks vector access  */
 #define DFLASH_ERR_WORKSPACE (-5)   /* workspace smaller than required         */
@@ -542,7 +544,7 @@ int dflash_attn_prep(const void* proj, int64_t proj_row_stride,
  * positions past lens[b] + T are read and given zero weight, so the caches
  * must hold finite values there (allocate them zero-filled).  workspace: at
  * least dflash_attn_verify_workspace_bytes(B, Hq, Hkv, max_len) bytes.
- * Supported: D == 128, T <= 16, Hq / Hkv <= 4, Smax % 64 == 0.
+ * Supported: D == 128, T <= 16, Hq / Hkv <= 4, Smax % 64 == 0, B <= 65535.
  */
 size_t dflash_attn_verify_workspace_bytes(int B, int Hq, int Hkv, int max_len);
 int dflash_attn_verify(const void* q, const void* k_cache,

@@ -135,3 +135,20 @@ def test_ops_refuse_cpu_tensors():
         gated_delta_verify(q, q, v, g, g, s)
     with pytest.raises(ValueError, match="ROCm device"):
         greedy_accept(torch.zeros(1, 2, 8), None)
+
+
+def test_model_op_size_limits(lib):
+    """Shapes whose row or grid counts overflow int are refused before any launch."""
+    d = ctypes.c_void_p(0x1000)
+    big = 1 << 16
+    # gated RMSNorm: B*T*H rows > 2^31 - 1
+    assert lib.dflash_gdn_gated_rmsnorm(d, d, None, d, d, big, big, 32, 128, 1e-6, None) == -2
+    # prologue: B*T workgroup rows > 2^31 - 1
+    assert lib.dflash_gdn_prologue(d, 0, 0, d, d, d, d, None, d, d, d, d, d, d,
+                                   big, big, 4, 16, 32, 128, 128, 1e-6, None) == -2
+    # attention prep: B*T workgroups > 2^31 - 1
+    assert lib.dflash_attn_prep(d, 5120, d, d, d, d, d, d, big, big, 16, 4, 128, 4096,
+                                64, 1e7, 1e-6, None) == -2
+    # attention: B beyond the partial kernel's grid.z
+    assert lib.dflash_attn_verify(d, d, d, d, d, 4096, d, 70000, 16, 16, 4, 128, 4096, 4096,
+                                  0.0884, d, 1 << 40, None) == -2
