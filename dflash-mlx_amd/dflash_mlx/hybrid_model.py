@@ -228,10 +228,13 @@ class HybridVerifyRunner:
     GEMM_PLAN = {"w_in": (1, 32, 4), "w_out": (8, 16, 4), "w_qkv": (1, 32, 4),
                  "w_o": (8, 32, 4), "w_gu": (1, 32, 4), "w_down": (8, 32, 4)}
     # the same for fragment-tiled weights (rows_per_wave 64 exists only
-    # there); down's 6 splits (24 of its 144 k-steps each, 6 per wave) beat 8
-    # by ~30 us per c4 step when timed inside the whole graph-captured step
-    TILED_PLAN = {"w_in": (1, 64, 4), "w_out": (8, 32, 4), "w_qkv": (1, 32, 4),
-                  "w_o": (8, 16, 4), "w_gu": (1, 32, 4), "w_down": (6, 32, 4)}
+    # there), timed inside the whole graph-captured c4 step (which also counts
+    # the add + RMSNorm reading fewer partials): down in 6 splits (24 of its
+    # 144 k-steps each, 6 per wave) beat 8 by ~30 us per step; with
+    # nontemporal weight loads, out_proj in 6 splits and down at 64 rows per
+    # wave save another ~19 us
+    TILED_PLAN = {"w_in": (1, 64, 4), "w_out": (6, 32, 4), "w_qkv": (1, 32, 4),
+                  "w_o": (8, 16, 4), "w_gu": (1, 32, 4), "w_down": (6, 64, 4)}
 
     def _build_gemms(self):
         """Argument tuples of every projection GEMM, and the split-K partial

@@ -88,13 +88,17 @@ def test_prologue_matches_oracle(oracle, device, cfg, B, T):
     np.testing.assert_array_equal(new_conv.float().cpu().numpy(), rst)
 
 
-def test_gated_rmsnorm_matches_oracle(oracle, device):
-    gen = torch.Generator().manual_seed(7)
-    x = torch.randn(2, 16, 32, 128, generator=gen).bfloat16()
-    zfull = torch.randn(2, 16, 32 * 128 + 64, generator=gen).bfloat16()
-    z = zfull[..., :32 * 128].unflatten(-1, (32, 128))       # strided view, as out of a projection
-    wgt = (1 + 0.1 * torch.randn(128, generator=gen)).bfloat16()
-    y = gated_rmsnorm(x.to(device), zfull.to(device)[..., :32 * 128].unflatten(-1, (32, 128)),
+@pytest.mark.parametrize("B,T,H,D", [(2, 16, 32, 128), (1, 3, 5, 64), (1, 16, 7, 192), (2, 1, 3, 256)])
+def test_gated_rmsnorm_matches_oracle(oracle, device, B, T, H, D):
+    """Every compiled channel count (D / 64 = 1..4), rows not a multiple of the
+    4 per workgroup, the gate as a strided view of a wider projection row."""
+    gen = torch.Generator().manual_seed(7 + D)
+    print(f"[gated_rmsnorm B={B} T={T} H={H} D={D}]", flush=True)
+    x = torch.randn(B, T, H, D, generator=gen).bfloat16()
+    zfull = torch.randn(B, T, H * D + 64, generator=gen).bfloat16()
+    z = zfull[..., :H * D].unflatten(-1, (H, D))       # strided view, as out of a projection
+    wgt = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
+    y = gated_rmsnorm(x.to(device), zfull.to(device)[..., :H * D].unflatten(-1, (H, D)),
                       wgt.to(device), 1e-6)
     torch.cuda.synchronize()
     ref = oracle.gated_rmsnorm(x.float().numpy(), z.float().numpy(), wgt.float().numpy(), 1e-6)
