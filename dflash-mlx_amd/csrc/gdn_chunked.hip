@@ -134,13 +134,21 @@ __device__ __forceinline__ f32x4 ldf4(const void* ptr) { return *reinterpret_cas
 
 // ------------------------------------------------------------------ phase 1
 // grid (NC, B*Hv), 256 threads.
+// LDS is held to 53 KB so that three workgroups fit on a CU (the registers
+// allow three as well): A (read until T is formed) and V^T (read from the
+// U~ products on) share one buffer, V^T staying in registers until the
+// inverse is done, and g / beta live in the padding columns of the K^T tile
+// (64 .. 67, never read as K^T).
+static_assert(sizeof(float) * CH * TPF <= sizeof(uint16_t) * D * KTP, "A fits the V^T buffer");
+static_assert(KTP >= CH + 4 && CH <= D, "g and beta fit the K^T padding");
 __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
-  __shared__ __attribute__((aligned(16))) float sA[CH][TPF];
   __shared__ __attribute__((aligned(16))) float sT[CH][TPF];
   __shared__ __attribute__((aligned(16))) uint16_t sKT[D][KTP];
-  __shared__ __attribute__((aligned(16))) uint16_t sVT[D][KTP];
-  __shared__ float sG[CH];
-  __shared__ float sBeta[CH];
+  __shared__ __attribute__((aligned(16))) uint16_t sAV[D][KTP];
+  float(*sA)[TPF] = reinterpret_cast<float(*)[TPF]>(&sAV[0][0]);
+  uint16_t(*sVT)[KTP] = sAV;
+  auto sG = [&](int j) -> float& { return *reinterpret_cast<float*>(&sKT[j][CH]); };
+  auto sBeta = [&](int j) -> float& { return *reinterpret_cast<float*>(&sKT[j][CH + 2]); };
   const int c = blockIdx.x;
   const int bh = blockIdx.y;
   const int b = bh / p.Hv;
@@ -189,8 +197,9 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
     bt = p.beta[b * p.b_sb + (int64_t)(t0 + lane) * p.b_st + hv];
   }
 
-  // K^T and V^T tiles (padded tokens zero): a 4-token x 8-column block per
-  // thread, transposed in registers and written as 8-byte rows of 4 tokens.
+  // K^T tile (padded tokens zero; V's rows are zeroed here and written as
+  // V^T after the inverse): a 4-token x 8-column block per thread,
+  // transposed in registers and written as 8-byte rows of 4 tokens.
   {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
@@ -202,16 +211,11 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
 #pragma unroll
     for (int x = 0; x < 4; ++x) {
       const uint32_t k0 = kk[0][x], k1 = kk[1][x], k2 = kk[2][x], k3 = kk[3][x];
-      const uint32_t v0 = vv[0][x], v1 = vv[1][x], v2 = vv[2][x], v3 = vv[3][x];
       // column 2x: low halves of tokens 0..3; column 2x+1: high halves.
       *reinterpret_cast<u32x2*>(&sKT[piece * 8 + 2 * x][4 * jq]) =
           u32x2{__builtin_amdgcn_perm(k1, k0, 0x05040100u), __builtin_amdgcn_perm(k3, k2, 0x05040100u)};
       *reinterpret_cast<u32x2*>(&sKT[piece * 8 + 2 * x + 1][4 * jq]) =
           u32x2{__builtin_amdgcn_perm(k1, k0, 0x07060302u), __builtin_amdgcn_perm(k3, k2, 0x07060302u)};
-      *reinterpret_cast<u32x2*>(&sVT[piece * 8 + 2 * x][4 * jq]) =
-          u32x2{__builtin_amdgcn_perm(v1, v0, 0x05040100u), __builtin_amdgcn_perm(v3, v2, 0x05040100u)};
-      *reinterpret_cast<u32x2*>(&sVT[piece * 8 + 2 * x + 1][4 * jq]) =
-          u32x2{__builtin_amdgcn_perm(v1, v0, 0x07060302u), __builtin_amdgcn_perm(v3, v2, 0x07060302u)};
     }
   }
   // This wave's K fragments, shared (the A operand of the other waves' K K^T
@@ -235,8 +239,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
       const float o = __shfl_up(lg, off, 64);
       if (lane >= off) lg += o;
     }
-    sG[lane] = lg;
-    sBeta[lane] = bt;
+    sG(lane) = lg;
+    sBeta(lane) = bt;
     const float lg_end = __shfl(lg, CH - 1, 64);
     reinterpret_cast<float*>(ws + kEG)[lane] = __expf(lg);
     reinterpret_cast<float*>(ws + kED)[lane] = __expf(lg_end - lg);
@@ -252,7 +256,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
   // are zero (A's are never read).
   {
     const int i = wave * 16 + r16;
-    const float gi = sG[i], bi = sBeta[i];
+    const float gi = sG(i), bi = sBeta(i);
     uint32_t phw[4], plw[4];  // one fragment (8 slots) as hi / lo words
 #pragma unroll
     for (int jt = 0; jt < 4; ++jt) {
@@ -268,7 +272,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int j = jt * 16 + 4 * g4 + e;
-          const float dec = (j <= i) ? __expf(gi - sG[j]) : 0.f;
+          const float dec = (j <= i) ? __expf(gi - sG(j)) : 0.f;
           av[e] = (j < i) ? bi * dec * kq[e] : 0.f;
           pv[e] = dec * qq[e];
         }
@@ -353,6 +357,17 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
     for (int e = 0; e < 4; ++e) sT[16 * bi + 4 * g4 + e][16 * wave + r16] = -yv[e];
   }
   __syncthreads();
+  // V^T tile into the buffer A used (every wave is past its last read of A),
+  // transposed in registers as K^T was.
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    const uint32_t v0 = vv[0][x], v1 = vv[1][x], v2 = vv[2][x], v3 = vv[3][x];
+    *reinterpret_cast<u32x2*>(&sVT[piece * 8 + 2 * x][4 * jq]) =
+        u32x2{__builtin_amdgcn_perm(v1, v0, 0x05040100u), __builtin_amdgcn_perm(v3, v2, 0x05040100u)};
+    *reinterpret_cast<u32x2*>(&sVT[piece * 8 + 2 * x + 1][4 * jq]) =
+        u32x2{__builtin_amdgcn_perm(v1, v0, 0x07060302u), __builtin_amdgcn_perm(v3, v2, 0x07060302u)};
+  }
+  __syncthreads();
 
   // W^T[dk][i] = sum_j K^T[dk][j] T'[i][j],  T' = T diag(beta gamma)   (wave w: dk tiles 2w, 2w+1)
   // U~[i][dv]  = sum_j T_b[i][j] V^T[dv][j], T_b = T diag(beta)       (wave w: dv tiles 2w, 2w+1)
@@ -374,8 +389,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
         float tw[8], tb[8];
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
-          tb[x] = sT[i][j0 + x] * sBeta[j0 + x];
-          tw[x] = tb[x] * __expf(sG[j0 + x]);
+          tb[x] = sT[i][j0 + x] * sBeta(j0 + x);
+          tw[x] = tb[x] * __expf(sG(j0 + x));
         }
         u32x4 twh, twl, tbh, tbl;
         split8(tw, twh, twl);
