@@ -184,8 +184,10 @@ __global__ __launch_bounds__(kLmThreads) void lm_head_argmax_kernel(const LmPara
 // already in A-fragment layout, so no LDS transpose).  The 4 wavefronts are
 // kLmTiledKW k-parts of kLmTiledRG row groups of VT tiles: each k-part sums
 // its share of H, the parts merge through LDS, then the argmax epilogue is
-// the row-major kernel's.  On MI355X at V = 151936, H = 2560, 16 rows this
-// streams the 778 MB head at ~5.9 TB/s against ~5.2 row-major.
+// the row-major kernel's.  The fragment loads are nontemporal (whole 1 KB
+// runs, each read once): on MI355X at V = 151936, H = 2560, 16 rows this
+// streams the 778 MB head at ~6.9 TB/s (~6.1 with ordinary loads) against
+// ~5.3 row-major.
 constexpr int kLmTiledKW = 2;
 constexpr int kLmTiledRG = (kLmThreads / 64) / kLmTiledKW;
 constexpr int kLmTiledVT = 4;
