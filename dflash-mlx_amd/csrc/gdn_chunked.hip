@@ -128,6 +128,13 @@ __device__ __forceinline__ const uint16_t* vrow(const ChunkParams& p, int b, int
   return p.v + b * p.v_sb + (int64_t)t * p.v_st + hv * p.v_sh;
 }
 
+// Column of token `col` (< CH) in row `row` of the K^T / V^T tiles: the
+// 16-byte column chunks are XOR-swizzled by bits 3..5 of the row, so the
+// transposed writes (one lane per 8-row group, rows 8 apart) spread over the
+// LDS banks instead of meeting in one; readers use the same map, so the tile
+// holds the same values.  Padding columns (>= CH) are not swizzled.
+__device__ __forceinline__ int tcol(int row, int col) { return col ^ (((row >> 3) & 7) << 3); }
+
 __device__ __forceinline__ u32x4 ld16(const void* ptr) { return *reinterpret_cast<const u32x4*>(ptr); }
 __device__ __forceinline__ u32x2 ld8(const void* ptr) { return *reinterpret_cast<const u32x2*>(ptr); }
 __device__ __forceinline__ f32x4 ldf4(const void* ptr) { return *reinterpret_cast<const f32x4*>(ptr); }
@@ -212,9 +219,9 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
     for (int x = 0; x < 4; ++x) {
       const uint32_t k0 = kk[0][x], k1 = kk[1][x], k2 = kk[2][x], k3 = kk[3][x];
       // column 2x: low halves of tokens 0..3; column 2x+1: high halves.
-      *reinterpret_cast<u32x2*>(&sKT[piece * 8 + 2 * x][4 * jq]) =
+      *reinterpret_cast<u32x2*>(&sKT[piece * 8 + 2 * x][tcol(piece * 8 + 2 * x, 4 * jq)]) =
           u32x2{__builtin_amdgcn_perm(k1, k0, 0x05040100u), __builtin_amdgcn_perm(k3, k2, 0x05040100u)};
-      *reinterpret_cast<u32x2*>(&sKT[piece * 8 + 2 * x + 1][4 * jq]) =
+      *reinterpret_cast<u32x2*>(&sKT[piece * 8 + 2 * x + 1][tcol(piece * 8 + 2 * x + 1, 4 * jq)]) =
           u32x2{__builtin_amdgcn_perm(k1, k0, 0x07060302u), __builtin_amdgcn_perm(k3, k2, 0x07060302u)};
     }
   }
@@ -298,8 +305,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
     uint16_t* kt = reinterpret_cast<uint16_t*>(ws + kKT);
     for (int e = tid; e < D * 8; e += 256) {
       const int dk = e >> 3, s = (e >> 2) & 1, g = e & 3;
-      const u32x2 a = *reinterpret_cast<const u32x2*>(&sKT[dk][32 * s + 4 * g]);
-      const u32x2 z = *reinterpret_cast<const u32x2*>(&sKT[dk][32 * s + 16 + 4 * g]);
+      const u32x2 a = *reinterpret_cast<const u32x2*>(&sKT[dk][tcol(dk, 32 * s + 4 * g)]);
+      const u32x2 z = *reinterpret_cast<const u32x2*>(&sKT[dk][tcol(dk, 32 * s + 16 + 4 * g)]);
       *reinterpret_cast<u32x4*>(kt + (((dk >> 4) * 2 + s) * 64 + (dk & 15) + 16 * g) * 8) =
           u32x4{a.x, a.y, z.x, z.y};
     }
@@ -362,9 +369,9 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
 #pragma unroll
   for (int x = 0; x < 4; ++x) {
     const uint32_t v0 = vv[0][x], v1 = vv[1][x], v2 = vv[2][x], v3 = vv[3][x];
-    *reinterpret_cast<u32x2*>(&sVT[piece * 8 + 2 * x][4 * jq]) =
+    *reinterpret_cast<u32x2*>(&sVT[piece * 8 + 2 * x][tcol(piece * 8 + 2 * x, 4 * jq)]) =
         u32x2{__builtin_amdgcn_perm(v1, v0, 0x05040100u), __builtin_amdgcn_perm(v3, v2, 0x05040100u)};
-    *reinterpret_cast<u32x2*>(&sVT[piece * 8 + 2 * x + 1][4 * jq]) =
+    *reinterpret_cast<u32x2*>(&sVT[piece * 8 + 2 * x + 1][tcol(piece * 8 + 2 * x + 1, 4 * jq)]) =
         u32x2{__builtin_amdgcn_perm(v1, v0, 0x07060302u), __builtin_amdgcn_perm(v3, v2, 0x07060302u)};
   }
   __syncthreads();
@@ -398,10 +405,10 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
 #pragma unroll
         for (int x = 0; x < 2; ++x) {
           const int tile = 2 * wave + x;
-          const u32x4 ka = *reinterpret_cast<const u32x4*>(&sKT[tile * 16 + r16][j0]);
+          const u32x4 ka = *reinterpret_cast<const u32x4*>(&sKT[tile * 16 + r16][tcol(tile * 16 + r16, j0)]);
           aw[x] = mfma(ka, twh, aw[x]);
           aw[x] = mfma(ka, twl, aw[x]);
-          const u32x4 vb = *reinterpret_cast<const u32x4*>(&sVT[tile * 16 + r16][j0]);
+          const u32x4 vb = *reinterpret_cast<const u32x4*>(&sVT[tile * 16 + r16][tcol(tile * 16 + r16, j0)]);
           au[x] = mfma(tbh, vb, au[x]);
           au[x] = mfma(tbl, vb, au[x]);
         }
