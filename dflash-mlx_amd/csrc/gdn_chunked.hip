@@ -394,9 +394,11 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
       for (int s = 0; s < 2; ++s) {
         const int j0 = s * 32 + g4 * 8;
         float tw[8], tb[8];
+        const f32x4 ta = *reinterpret_cast<const f32x4*>(&sT[i][j0]);      // two 16-byte reads
+        const f32x4 tc = *reinterpret_cast<const f32x4*>(&sT[i][j0 + 4]);  // of T's row piece
 #pragma unroll
         for (int x = 0; x < 8; ++x) {
-          tb[x] = sT[i][j0 + x] * sBeta(j0 + x);
+          tb[x] = (x < 4 ? ta[x & 3] : tc[x & 3]) * sBeta(j0 + x);
           tw[x] = tb[x] * __expf(sG(j0 + x));
         }
         u32x4 twh, twl, tbh, tbl;
