@@ -338,3 +338,4 @@ extern "C" int dflash_greedy_accept_conv_rollback(
   }
   return DFLASH_OK;
 }
+

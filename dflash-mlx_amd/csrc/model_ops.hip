@@ -76,12 +76,15 @@ __device__ __forceinline__ float silu(float x) { return x / (1.f + __expf(-x)); 
 // r: NS of them, a compile-time count for the common split factors) before
 // using any, so a row costs one memory round trip.  With tok != nullptr, x
 // is the embedding table and row m reads table row tok[m] (clamped to
-// [0, vocab)), stored to h_out as the residual stream's start.
+// [0, vocab)), stored to h_out as the residual stream's start.  With hc !=
+// nullptr, h is also stored to row m of hc (row stride hc_stride elements):
+// the target hidden state a drafter reads at selected layers.
 template <bool PART, int NS>
 __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(const uint16_t* x, const int32_t* tok,
                                                            int vocab, const uint16_t* r,
                                                            const float* rp, int nsplit,
                                                            const uint16_t* w, uint16_t* h_out,
+                                                           uint16_t* hc, int64_t hc_stride,
                                                            uint16_t* y, int M, int H, float eps) {
   __shared__ float wsum[16];
   const int row = blockIdx.x;
@@ -139,6 +142,7 @@ __global__ __launch_bounds__(1024) void add_rmsnorm_kernel(const uint16_t* x, co
   if (live) {
     if ((PART || r != nullptr || tok != nullptr) && h_out != nullptr)
       *reinterpret_cast<u32x4*>(h_out + (int64_t)row * H + ch * 8) = pack8(v);
+    if (hc != nullptr) *reinterpret_cast<u32x4*>(hc + (int64_t)row * hc_stride + ch * 8) = pack8(v);
     float wv[8], o[8];
     unpack8(wraw, wv);
 #pragma unroll
@@ -182,6 +186,7 @@ struct AttnPrepParams {
   uint16_t* k_cache;   // [B, Hkv, Smax, D]
   uint16_t* vt_cache;  // [B, Hkv, D, Smax]
   uint16_t* q_out;     // [B, T, Hq, D]
+  int32_t* overflow;   // [B] or null: set to 1 when a block position falls outside [0, Smax)
   int B, T, Hq, Hkv, Smax, rot;
   double log2_base;
   float eps;
@@ -205,12 +210,16 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const AttnPrepParams p) 
   const int b = bt / p.T;
   const int t = bt - b * p.T;
   const int pos = p.lens[b] + t;
+  // A position outside the cache is never written; the sequence's overflow
+  // word records it so the host can refuse the step's output.
+  const bool in_cache = pos >= 0 && pos < p.Smax;
+  if (!in_cache && slot == 0 && lane == 0 && p.overflow != nullptr) p.overflow[b] = 1;
   const uint16_t* row = p.proj + (int64_t)bt * p.row_stride;
   const int d0 = 2 * lane;
   if (slot >= p.Hq + p.Hkv) {  // value head: V^T cache column
     const int h = slot - p.Hq - p.Hkv;
     const uint32_t vv = *reinterpret_cast<const uint32_t*>(row + p.Hq * 2 * kHD + p.Hkv * kHD + h * kHD + d0);
-    if (pos < p.Smax) {
+    if (in_cache) {
       uint16_t* col = p.vt_cache + (((int64_t)b * p.Hkv + h) * kHD + d0) * p.Smax + pos;
       col[0] = (uint16_t)vv;
       col[p.Smax] = (uint16_t)(vv >> 16);
@@ -252,7 +261,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const AttnPrepParams p) 
   const uint32_t packed = pack2(x0, x1);
   if (is_q) {
     *reinterpret_cast<uint32_t*>(p.q_out + ((int64_t)bt * p.Hq + h) * kHD + d0) = packed;
-  } else if (pos < p.Smax) {
+  } else if (in_cache) {
     *reinterpret_cast<uint32_t*>(p.k_cache + (((int64_t)b * p.Hkv + h) * p.Smax + pos) * kHD + d0) =
         packed;
   }
@@ -507,14 +516,17 @@ using namespace dflash;
 namespace dflash {
 namespace {
 int launch_add_rmsnorm(const void* x, const int32_t* tok, int vocab, const void* r, const float* rp,
-                       int nsplit, const void* weight, void* h_out, void* y, int M, int H,
-                       float eps, void* stream) {
+                       int nsplit, const void* weight, void* h_out, void* h_copy,
+                       int64_t h_copy_stride, void* y, int M, int H, float eps, void* stream) {
   if (M < 0 || H <= 0 || H % 8 != 0 || H > 1024 * 8 || nsplit < 0) return DFLASH_ERR_SHAPE;
+  if (h_copy != nullptr && h_copy_stride < H) return DFLASH_ERR_SHAPE;
   if (M == 0) return DFLASH_OK;
   if (x == nullptr || weight == nullptr || y == nullptr) return DFLASH_ERR_NULL;
   if (((uintptr_t)x & 15) || ((uintptr_t)r & 15) || ((uintptr_t)rp & 15) ||
-      ((uintptr_t)weight & 15) || ((uintptr_t)h_out & 15) || ((uintptr_t)y & 15))
+      ((uintptr_t)weight & 15) || ((uintptr_t)h_out & 15) || ((uintptr_t)y & 15) ||
+      ((uintptr_t)h_copy & 15) || (h_copy != nullptr && (h_copy_stride % 8)))
     return DFLASH_ERR_ALIGN;
+  auto* hcp = static_cast<uint16_t*>(h_copy);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)M);
   const dim3 block((unsigned)ceil_div(H / 8, 64) * 64);
@@ -528,18 +540,18 @@ int launch_add_rmsnorm(const void* x, const int32_t* tok, int vocab, const void*
 #define DFLASH_ARN(ns)                                                                           \
   case ns:                                                                                       \
     hipLaunchKernelGGL((add_rmsnorm_kernel<true, ns>), grid, block, 0, s, xp, tok, vocab, nullptr, \
-                       rp, nsplit, wp, hp, yp, M, H, eps);                                       \
+                       rp, nsplit, wp, hp, hcp, h_copy_stride, yp, M, H, eps);                   \
     break;
       DFLASH_ARN(1) DFLASH_ARN(2) DFLASH_ARN(3) DFLASH_ARN(4) DFLASH_ARN(5) DFLASH_ARN(6)
       DFLASH_ARN(7) DFLASH_ARN(8)
 #undef DFLASH_ARN
       default:
         hipLaunchKernelGGL((add_rmsnorm_kernel<true, 0>), grid, block, 0, s, xp, tok, vocab, nullptr,
-                           rp, nsplit, wp, hp, yp, M, H, eps);
+                           rp, nsplit, wp, hp, hcp, h_copy_stride, yp, M, H, eps);
     }
   } else {
     hipLaunchKernelGGL((add_rmsnorm_kernel<false, 0>), grid, block, 0, s, xp, tok, vocab, rpb,
-                       nullptr, 0, wp, hp, yp, M, H, eps);
+                       nullptr, 0, wp, hp, hcp, h_copy_stride, yp, M, H, eps);
   }
   return to_status(hipGetLastError());
 }
@@ -548,15 +560,26 @@ int launch_add_rmsnorm(const void* x, const int32_t* tok, int vocab, const void*
 
 extern "C" int dflash_add_rmsnorm(const void* x, const void* r, const void* weight, void* h_out,
                                   void* y, int M, int H, float eps, void* stream) {
-  return launch_add_rmsnorm(x, nullptr, 0, r, nullptr, 0, weight, h_out, y, M, H, eps, stream);
+  return launch_add_rmsnorm(x, nullptr, 0, r, nullptr, 0, weight, h_out, nullptr, 0, y, M, H, eps,
+                            stream);
 }
 
 extern "C" int dflash_add_rmsnorm_splitk(const void* x, const float* r_partials, int nsplit,
                                          const void* weight, void* h_out, void* y, int M, int H,
                                          float eps, void* stream) {
   if (r_partials == nullptr || nsplit < 1) return DFLASH_ERR_NULL;
-  return launch_add_rmsnorm(x, nullptr, 0, nullptr, r_partials, nsplit, weight, h_out, y, M, H, eps,
-                            stream);
+  return launch_add_rmsnorm(x, nullptr, 0, nullptr, r_partials, nsplit, weight, h_out, nullptr, 0,
+                            y, M, H, eps, stream);
+}
+
+extern "C" int dflash_add_rmsnorm_capture(const void* x, const void* r, const float* r_partials,
+                                          int nsplit, const void* weight, void* h_out,
+                                          void* h_copy, int64_t h_copy_row_stride, void* y, int M,
+                                          int H, float eps, void* stream) {
+  if (r_partials != nullptr && (r != nullptr || nsplit < 1)) return DFLASH_ERR_SHAPE;
+  if (h_copy == nullptr) return DFLASH_ERR_NULL;
+  return launch_add_rmsnorm(x, nullptr, 0, r, r_partials, r_partials ? nsplit : 0, weight, h_out,
+                            h_copy, h_copy_row_stride, y, M, H, eps, stream);
 }
 
 extern "C" int dflash_embed_rmsnorm(const void* table, const int32_t* tokens, int vocab,
@@ -564,8 +587,8 @@ extern "C" int dflash_embed_rmsnorm(const void* table, const int32_t* tokens, in
                                     float eps, void* stream) {
   if (vocab <= 0) return DFLASH_ERR_SHAPE;
   if (tokens == nullptr || h_out == nullptr) return DFLASH_ERR_NULL;
-  return launch_add_rmsnorm(table, tokens, vocab, nullptr, nullptr, 0, weight, h_out, y, M, H, eps,
-                            stream);
+  return launch_add_rmsnorm(table, tokens, vocab, nullptr, nullptr, 0, weight, h_out, nullptr, 0, y,
+                            M, H, eps, stream);
 }
 
 extern "C" int dflash_swiglu(const void* gate_up, void* out, int M, int I, void* stream) {
@@ -582,8 +605,9 @@ extern "C" int dflash_swiglu(const void* gate_up, void* out, int M, int I, void*
 
 extern "C" int dflash_attn_prep(const void* proj, int64_t proj_row_stride, const void* q_norm_w,
                                 const void* k_norm_w, const int32_t* lens, void* k_cache,
-                                void* vt_cache, void* q_out, int B, int T, int Hq, int Hkv, int D,
-                                int Smax, int rot_dims, float rope_base, float eps, void* stream) {
+                                void* vt_cache, void* q_out, int32_t* overflow, int B, int T,
+                                int Hq, int Hkv, int D, int Smax, int rot_dims, float rope_base,
+                                float eps, void* stream) {
   if (B < 0 || T < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || Smax <= 0) return DFLASH_ERR_SHAPE;
   if (D != kHD) return DFLASH_ERR_UNSUPPORTED;
   if (!(rot_dims == 0 || rot_dims == 16 || rot_dims == 32 || rot_dims == 64 || rot_dims == 128))
@@ -606,6 +630,7 @@ extern "C" int dflash_attn_prep(const void* proj, int64_t proj_row_stride, const
   p.k_cache = static_cast<uint16_t*>(k_cache);
   p.vt_cache = static_cast<uint16_t*>(vt_cache);
   p.q_out = static_cast<uint16_t*>(q_out);
+  p.overflow = overflow;
   p.B = B; p.T = T; p.Hq = Hq; p.Hkv = Hkv; p.Smax = Smax; p.rot = rot_dims;
   p.log2_base = log2((double)rope_base);
   p.eps = eps;

@@ -48,6 +48,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP, _VP, _SZ, _VP],
     ),
     "dflash_add_rmsnorm": (_I, [_VP, _VP, _VP, _VP, _VP, _I, _I, ctypes.c_float, _VP]),
+    "dflash_add_rmsnorm_capture": (
+        _I, [_VP, _VP, _VP, _I, _VP, _VP, _VP, _I64, _VP, _I, _I, ctypes.c_float, _VP]),
     "dflash_add_rmsnorm_splitk": (
         _I, [_VP, _VP, _I, _VP, _VP, _VP, _I, _I, ctypes.c_float, _VP]),
     "dflash_embed_rmsnorm": (_I, [_VP, _VP, _I, _VP, _VP, _VP, _I, _I, ctypes.c_float, _VP]),
@@ -62,8 +64,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dflash_swiglu": (_I, [_VP, _VP, _I, _I, _VP]),
     "dflash_attn_prep": (
         _I,
-        [_VP, _I64, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _I, ctypes.c_float,
-         ctypes.c_float, _VP],
+        [_VP, _I64, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _I,
+         ctypes.c_float, ctypes.c_float, _VP],
     ),
     "dflash_attn_verify_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "dflash_attn_verify": (
@@ -110,7 +112,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _I64, _I64, _I64, _I, _VP],
     ),
 }
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

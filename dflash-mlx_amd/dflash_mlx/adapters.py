@@ -18,6 +18,8 @@ gather:
 """
 from __future__ import annotations
 
+from dataclasses import dataclass, field
+from pathlib import Path
 from typing import Any
 
 import torch
@@ -73,24 +75,89 @@ def rollback_linear_caches(
 
 
 class Qwen35TargetAdapter:
-    """Rollback half of the reference's Qwen35TargetAdapter
-    (adapters.py:341-570).  Model loading, prompting and the LM head are
-    outside the verify hot path and are not provided here."""
+    """The reference's Qwen35TargetAdapter (adapters.py:341-570) over a model
+    object with the DFlash methods (``target.HybridTargetModel``).  Loading a
+    checkpoint and the chat template are outside the verify hot path: the
+    model is built by the caller and the tokenizer, when there is one, is
+    any object with the Hugging Face ``encode`` / ``decode`` /
+    ``apply_chat_template`` / ``eos_token_ids`` surface."""
 
     family = "qwen3_5"
 
-    def make_cache(self, num_layers: int, full_attention_interval: int = 4) -> list[Any]:
-        """custom_qwen35_model.py:818, :1153-1154: layer i is linear
-        attention unless (i + 1) % full_attention_interval == 0."""
+    def build_prompt(self, tokenizer, prompt_text: str) -> torch.Tensor:
+        """adapters.py:356-365: the chat template with thinking disabled."""
+        if tokenizer is None:
+            raise ValueError("building a prompt from text needs a tokenizer")
+        messages = [{"role": "user", "content": prompt_text}]
+        prompt = tokenizer.apply_chat_template(messages, tokenize=False,
+                                               add_generation_prompt=True, enable_thinking=False)
+        return torch.tensor(tokenizer.encode(prompt, add_special_tokens=False), dtype=torch.int32)
+
+    def stop_token_ids(self, tokenizer, model=None) -> set[int]:
+        """adapters.py:367-371 (the tokenizer's eos ids); without a tokenizer,
+        the model's configured eos ids."""
+        if tokenizer is None:
+            return set(getattr(model, "eos_token_ids", ()))
+        eos = tokenizer.eos_token_ids
+        return {eos} if isinstance(eos, int) else set(eos)
+
+    def make_cache(self, model=None, num_layers: int | None = None,
+                   full_attention_interval: int = 4) -> list[Any]:
+        """The model's cache list (custom_qwen35_model.py:1153-1154); without
+        a model, host-side cache objects for num_layers layers (layer i is
+        linear attention unless (i + 1) % full_attention_interval == 0, :818)."""
+        if model is not None and hasattr(model, "make_cache"):
+            return model.make_cache()
         return [
             ArraysCache(size=2) if (i + 1) % full_attention_interval != 0 else KVCache()
-            for i in range(num_layers)
+            for i in range(int(num_layers))
         ]
+
+    def embed_tokens(self, model, tokens):
+        return model.embed_tokens(tokens)
+
+    def lm_head_logits(self, model, hidden_states):
+        return model.lm_head_logits(hidden_states)
+
+    def lm_head_argmax(self, model, hidden_states):
+        """The hook of adapters.py:267-271, served by the fused LM-head
+        greedy kernel (no logits)."""
+        return model.lm_head_argmax(hidden_states)
+
+    def forward_with_hidden_states(self, model, inputs, cache, layer_ids,
+                                   return_rollback_records: bool = False):
+        """adapters.py:373-418 via the model's forward_dflash: (logits,
+        target_hidden[, records])."""
+        out = model.forward_dflash(inputs, cache, layer_ids,
+                                   return_rollback_records=return_rollback_records)
+        logits = model.lm_head_logits(out[0])
+        return (logits,) + tuple(out[1:])
+
+    def forward_verifier_states(self, model, inputs, cache, layer_ids):
+        """adapters.py:420-437: (norm_hidden, target_hidden, records)."""
+        return model.forward_dflash(inputs, cache, layer_ids, return_rollback_records=True)
+
+    def forward_accept_all_block(self, model, inputs, cache, layer_ids):
+        """adapters.py:439-456: logits of the last position only."""
+        norm_hidden, target_hidden = model.forward_dflash(inputs, cache, layer_ids,
+                                                          return_rollback_records=False)
+        return model.lm_head_logits(norm_hidden[:, -1:, :]), target_hidden
+
+    def snapshot_linear_caches(self, model, cache):
+        return model.snapshot_linear_caches(cache)
+
+    def restore_linear_caches(self, model, cache, snapshots) -> None:
+        model.restore_linear_caches(cache, snapshots)
 
     def rewind_kv_caches(self, cache: list[Any], num_tokens: int) -> None:
         rewind_kv_caches(cache, num_tokens)
 
     def rollback_linear_caches(self, model, cache, rollback_records, accepted_inputs) -> None:
+        """adapters.py:510-520: the model's own rollback when it has one, else
+        the generic tape gather."""
+        if model is not None and hasattr(model, "rollback_linear_caches"):
+            model.rollback_linear_caches(cache, rollback_records, accepted_inputs)
+            return
         rollback_linear_caches(cache, rollback_records, accepted_inputs)
 
     def cache_summary(self, cache: list[Any]) -> str:
@@ -109,3 +176,60 @@ ADAPTERS = {"qwen3_5": Qwen35TargetAdapter}
 
 def adapter_for_model_type(model_type: str):
     return ADAPTERS.get(model_type)
+
+
+@dataclass
+class LoadedTargetModel:
+    """The reference's LoadedTargetModel facade (adapters.py:729-826): the
+    decode runtime calls these methods, each delegating to the adapter with
+    the model.  ``model`` is a built model object (no checkpoint loading)."""
+
+    model: Any
+    adapter: Qwen35TargetAdapter = field(default_factory=Qwen35TargetAdapter)
+    tokenizer: Any = None
+    requested_model: str = "random-init"
+    resolved_model_path: Path | None = None
+
+    def build_prompt(self, prompt_text: str) -> torch.Tensor:
+        return self.adapter.build_prompt(self.tokenizer, prompt_text)
+
+    def stop_token_ids(self) -> set[int]:
+        return self.adapter.stop_token_ids(self.tokenizer, self.model)
+
+    def make_cache(self) -> list[Any]:
+        return self.adapter.make_cache(self.model)
+
+    def embed_tokens(self, tokens):
+        return self.adapter.embed_tokens(self.model, tokens)
+
+    def lm_head_logits(self, hidden_states):
+        return self.adapter.lm_head_logits(self.model, hidden_states)
+
+    def lm_head_argmax(self, hidden_states):
+        return self.adapter.lm_head_argmax(self.model, hidden_states)
+
+    def forward_with_hidden_states(self, inputs, cache, layer_ids,
+                                   return_rollback_records: bool = False):
+        return self.adapter.forward_with_hidden_states(
+            self.model, inputs, cache, layer_ids, return_rollback_records=return_rollback_records)
+
+    def forward_verifier_states(self, inputs, cache, layer_ids):
+        return self.adapter.forward_verifier_states(self.model, inputs, cache, layer_ids)
+
+    def forward_accept_all_block(self, inputs, cache, layer_ids):
+        return self.adapter.forward_accept_all_block(self.model, inputs, cache, layer_ids)
+
+    def snapshot_linear_caches(self, cache):
+        return self.adapter.snapshot_linear_caches(self.model, cache)
+
+    def restore_linear_caches(self, cache, snapshots) -> None:
+        self.adapter.restore_linear_caches(self.model, cache, snapshots)
+
+    def rewind_kv_caches(self, cache: list[Any], num_tokens: int) -> None:
+        self.adapter.rewind_kv_caches(cache, num_tokens)
+
+    def rollback_linear_caches(self, cache, rollback_records, accepted_inputs) -> None:
+        self.adapter.rollback_linear_caches(self.model, cache, rollback_records, accepted_inputs)
+
+    def cache_summary(self, cache: list[Any]) -> str:
+        return self.adapter.cache_summary(cache)

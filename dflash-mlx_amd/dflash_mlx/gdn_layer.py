@@ -27,6 +27,12 @@ from .adapters import make_rollback_record
 from .gated_delta import _require_device, gated_delta_verify
 
 
+# The q/k RMSNorm of the gated-delta layers uses a fixed eps of 1e-6
+# (custom_qwen35_model.py:355-356, :446-447, :787-788), independent of
+# rms_norm_eps, which sets only the layer norms and the gated norm.
+QK_NORM_EPS = 1e-6
+
+
 @dataclass(frozen=True)
 class GatedDeltaConfig:
     """The linear-attention fields of TextModelArgs
@@ -117,8 +123,7 @@ def gdn_prologue(qkv, conv_state, a, b, weights: GatedDeltaWeights, cfg: GatedDe
         qkv.data_ptr(), qkv.stride(0), qkv.stride(1), conv_state.data_ptr(),
         w.conv_weight.contiguous().data_ptr(), a.data_ptr(), b.data_ptr(), strides,
         w.A_log.data_ptr(), w.dt_bias.data_ptr(), act.data_ptr(), g.data_ptr(), beta.data_ptr(),
-        new_state.data_ptr(), B, T, K, Hk, Hv, Dk, Dv, float(cfg.rms_norm_eps),
-        _lib.stream_handle(dev),
+        new_state.data_ptr(), B, T, K, Hk, Hv, Dk, Dv, QK_NORM_EPS, _lib.stream_handle(dev),
     )
     kd = Hk * Dk
     q = act[..., :kd].unflatten(-1, (Hk, Dk))
@@ -222,7 +227,7 @@ def gdn_prologue_verify_rollback(qkv, conv_state, a, b, weights: GatedDeltaWeigh
         qkv.data_ptr(), qkv.stride(0), qkv.stride(1), conv_state.data_ptr(), conv_w.data_ptr(),
         a.data_ptr(), b.data_ptr(), strides, w.A_log.data_ptr(), w.dt_bias.data_ptr(),
         state.data_ptr(), prev_tape.data_ptr(), acc.data_ptr(), prev_tape.shape[0], period,
-        out.data_ptr(), None, tape_out.data_ptr(), B, T, K, Hk, Hv, Dk, Dv,
-        float(cfg.rms_norm_eps), _lib.stream_handle(dev),
+        out.data_ptr(), None, tape_out.data_ptr(), B, T, K, Hk, Hv, Dk, Dv, QK_NORM_EPS,
+        _lib.stream_handle(dev),
     )
     return out, tape_out

@@ -1,14 +1,28 @@
-"""Verify-step accept and rollback orchestration on MI355X.
+"""DFlash decode runtime on MI355X: the verify step, its accept and
+rollback, and the speculative decode loop.
 
-Mirrors the reference's decode-runtime pieces on the hot path
-(dflash_mlx/runtime.py):
+Mirrors the reference's dflash_mlx/runtime.py:
 
 * ``sample_tokens`` (:22-29) — greedy argmax runs in the gfx950 accept kernel;
 * ``longest_prefix_match`` (:41-47) — the host-list primitive, unchanged;
 * ``greedy_accept`` — argmax + prefix compare + bonus fused on the device, so
   only (matched, bonus) cross to the host;
-* ``verify_block_parallel_replay`` (:117-163) — same arguments and return
-  tuple; the rollback it triggers is a tape gather instead of a replay.
+* the verify modes ``verify_block_stream`` (:86-114),
+  ``verify_block_parallel_replay`` (:117-163),
+  ``verify_block_parallel_lazy_logits`` (:166-243),
+  ``verify_block_parallel_greedy_argmax`` (:246-292) and
+  ``verify_block_chunked`` (:295-357), same arguments and return tuples; the
+  rollback they trigger is a tape gather instead of a replay;
+* ``dflash_generate_stream`` / ``dflash_generate`` (:360-589): prefill,
+  draft a block, verify, accept, roll back, repeat, with the same events and
+  metrics.
+
+``target`` is the LoadedTargetModel facade (adapters.py) over the MI355X
+hybrid target; ``draft`` is any object with the DFlash drafter's interface
+(``block_size``, ``mask_token_id``, ``target_layer_ids``, ``make_cache()``,
+``__call__(noise_embedding=, target_hidden=, cache=)`` returning draft hidden
+states, dflash_mlx/draft.py:190-223).  The drafter network itself is not part
+of this package.
 
 Token ids are int32 on the device (the reference uses uint32; vocabularies
 here are far below 2**31).
@@ -16,6 +30,8 @@ here are far below 2**31).
 from __future__ import annotations
 
 import time
+from collections.abc import Iterator
+from dataclasses import dataclass
 from typing import Any, Sequence
 
 import torch
@@ -223,6 +239,90 @@ def add_profile_elapsed(profile: dict[str, float] | None, key: str, start: float
         profile[key] = profile.get(key, 0.0) + time.perf_counter() - start
 
 
+@dataclass
+class DFlashRuntimeEvent:
+    """runtime.py:14-19: tokens added since the last event, the whole output
+    so far, and the metrics on the final event."""
+
+    token_ids: list[int]
+    output_tokens: list[int]
+    metrics: dict[str, Any] | None = None
+    finished: bool = False
+
+
+def trim_draft_cache(cache: list[Any], num_tokens: int) -> None:
+    """runtime.py:32-34."""
+    for layer_cache in cache:
+        layer_cache.trim(num_tokens)
+
+
+def generated_token_count(output_tokens: list[int], prompt_len: int) -> int:
+    return max(len(output_tokens) - prompt_len, 0)
+
+
+def stop_position(tokens: list[int], start_idx: int, stop_token_ids: set[int]) -> int | None:
+    """runtime.py:50-54: index of the first stop token at or after start_idx."""
+    for idx in range(start_idx, len(tokens)):
+        if tokens[idx] in stop_token_ids:
+            return idx
+    return None
+
+
+def peak_memory_gb() -> float:
+    """runtime.py:57-58, as the device allocator's high-water mark."""
+    if not torch.cuda.is_available():
+        return 0.0
+    return torch.cuda.max_memory_allocated() / 1e9
+
+
+def _block_tensor(block_tokens: Sequence[int], device) -> torch.Tensor:
+    return torch.tensor([list(block_tokens)], dtype=torch.int32).to(device)
+
+
+def _target_device(target: Any):
+    model = getattr(target, "model", None)
+    return getattr(model, "device", None) or getattr(target, "device", None) or "cuda"
+
+
+def _posterior(logits: torch.Tensor, temperature: float) -> list[int]:
+    """Posterior tokens of row 0 of [1, N, V] logits on the host."""
+    return sample_tokens(logits[:1], temperature)[0].cpu().tolist()
+
+
+def _rollback(target, target_cache, rollback_records, draft_block_size, accepted_inputs,
+              profile) -> None:
+    """runtime.py:150-161: rewind the KV caches and roll the linear caches
+    back when only part of the block was accepted."""
+    if accepted_inputs < draft_block_size:
+        rollback_start = profile_start(profile)
+        target.rewind_kv_caches(target_cache, draft_block_size - accepted_inputs)
+        target.rollback_linear_caches(target_cache, rollback_records, accepted_inputs)
+        add_profile_elapsed(profile, "verify_rollback_time_s", rollback_start)
+
+
+def verify_block_stream(
+    target: Any,
+    target_cache: list[Any],
+    block_tokens: list[int],
+    temperature: float,
+    layer_ids: list[int],
+) -> tuple[int, int, torch.Tensor]:
+    """runtime.py:86-114: verify token by token, stopping at the first
+    mismatch (no rollback needed)."""
+    dev = _target_device(target)
+    verified_hidden_steps: list[torch.Tensor] = []
+    for idx, token in enumerate(block_tokens):
+        logits_step, hidden_step = target.forward_with_hidden_states(
+            _block_tensor([token], dev), target_cache, layer_ids)
+        next_token = _posterior(logits_step[:, -1:, :], temperature)[0]
+        verified_hidden_steps.append(hidden_step)
+        if idx == len(block_tokens) - 1:
+            return len(block_tokens), next_token, torch.cat(verified_hidden_steps, dim=1)
+        if next_token != block_tokens[idx + 1]:
+            return idx + 1, next_token, torch.cat(verified_hidden_steps, dim=1)
+    raise RuntimeError("Streaming verifier reached an impossible state.")
+
+
 def verify_block_parallel_replay(
     target: Any,
     target_cache: list[Any],
@@ -232,34 +332,331 @@ def verify_block_parallel_replay(
     layer_ids: list[int],
     profile: dict[str, float] | None = None,
 ) -> tuple[int, int, torch.Tensor]:
-    """One verify step (runtime.py:117-163).
+    """One verify step (runtime.py:117-163): the whole block in one forward
+    with rollback records, the posterior from its logits, the accept, and the
+    rollback of a partial accept.
 
-    ``target`` follows the reference's LoadedTargetModel facade:
-    forward_with_hidden_states(inputs, cache, layer_ids,
-    return_rollback_records=True) -> (logits, hidden, records),
-    rewind_kv_caches(cache, n) and rollback_linear_caches(cache, records, a).
-    Returns (accepted_inputs, bonus_token, verifier_hidden[:, :accepted_inputs]).
-    """
-    if temperature >= 1e-5:
-        raise NotImplementedError("the fused verify accepts greedy decoding only (temperature 0)")
+    Greedy (temperature 0): argmax, prefix compare and bonus run in one
+    device kernel pair and only (matched, bonus) cross to the host.  Else
+    the posterior is sampled (sample_tokens) and compared on the host.
+    Returns (accepted_inputs, bonus_token, verifier_hidden[:, :accepted_inputs])."""
     verifier_start = profile_start(profile)
-    dev = target.device
-    block = torch.tensor(block_tokens, dtype=torch.int32).to(dev)
+    block = _block_tensor(block_tokens, _target_device(target))
     logits, verifier_hidden, rollback_records = target.forward_with_hidden_states(
-        block[None], target_cache, layer_ids, return_rollback_records=True
+        block, target_cache, layer_ids, return_rollback_records=True
     )
-    # draft = block[1:] against posterior rows 0..T-2; the bonus may come from
-    # row `matched` <= T-1, so all T rows are argmax'ed (runtime.py:145-147).
-    _, matched_t, bonus_t = greedy_accept(logits[:1], block[None, 1:], want_posterior=False)
-    host = torch.stack([matched_t, bonus_t]).cpu()  # the one device->host sync
-    matched, bonus = int(host[0, 0]), int(host[1, 0])
+    if temperature < 1e-5:
+        # draft = block[1:] against posterior rows 0..T-2; the bonus may come
+        # from row `matched` <= T-1, so all T rows are argmax'ed (runtime.py:145-147).
+        _, matched_t, bonus_t = greedy_accept(logits[:1], block.to(logits.device)[:, 1:],
+                                              want_posterior=False)
+        host = torch.stack([matched_t, bonus_t]).cpu()  # the one device->host sync
+        matched, bonus = int(host[0, 0]), int(host[1, 0])
+    else:
+        posterior = _posterior(logits, temperature)
+        matched = longest_prefix_match(block_tokens[1:], posterior[:-1])
+        bonus = posterior[matched]
     accepted_inputs = matched + 1
     add_profile_elapsed(profile, "verify_forward_logits_time_s", verifier_start)
-
-    if accepted_inputs < draft_block_size:
-        rollback_start = profile_start(profile)
-        target.rewind_kv_caches(target_cache, draft_block_size - accepted_inputs)
-        target.rollback_linear_caches(target_cache, rollback_records, accepted_inputs)
-        add_profile_elapsed(profile, "verify_rollback_time_s", rollback_start)
-
+    _rollback(target, target_cache, rollback_records, draft_block_size, accepted_inputs, profile)
     return accepted_inputs, bonus, verifier_hidden[:, :accepted_inputs, :]
+
+
+def verify_block_parallel_lazy_logits(
+    target: Any,
+    target_cache: list[Any],
+    block_tokens: list[int],
+    draft_block_size: int,
+    temperature: float,
+    layer_ids: list[int],
+    logit_chunk_size: int,
+    profile: dict[str, float] | None = None,
+) -> tuple[int, int, torch.Tensor]:
+    """runtime.py:166-243: the verifier's normed hidden states first, then
+    the LM head chunk by chunk until the first mismatch."""
+    state_start = profile_start(profile)
+    norm_hidden_states, verifier_hidden, rollback_records = target.forward_verifier_states(
+        _block_tensor(block_tokens, _target_device(target)), target_cache, layer_ids)
+    add_profile_elapsed(profile, "verify_state_time_s", state_start)
+
+    matched = 0
+    accepted_inputs = draft_block_size
+    posterior_token: int | None = None
+    chunk_size = max(1, logit_chunk_size)
+    for chunk_start in range(0, draft_block_size, chunk_size):
+        chunk_end = min(chunk_start + chunk_size, draft_block_size)
+        logit_start = profile_start(profile)
+        logits_chunk = target.lm_head_logits(norm_hidden_states[:, chunk_start:chunk_end, :])
+        posterior_chunk = _posterior(logits_chunk, temperature)
+        add_profile_elapsed(profile, "verify_lazy_logits_time_s", logit_start)
+        prefix_start = profile_start(profile)
+        for local_idx, token in enumerate(posterior_chunk):
+            pos = chunk_start + local_idx
+            if pos == draft_block_size - 1:
+                posterior_token = token
+                accepted_inputs = draft_block_size
+                break
+            if token == block_tokens[pos + 1]:
+                matched += 1
+                continue
+            posterior_token = token
+            accepted_inputs = matched + 1
+            break
+        add_profile_elapsed(profile, "verify_prefix_time_s", prefix_start)
+        if posterior_token is not None:
+            break
+    if posterior_token is None:
+        raise RuntimeError("Lazy-logit verifier failed to produce a posterior token.")
+    _rollback(target, target_cache, rollback_records, draft_block_size, accepted_inputs, profile)
+    return accepted_inputs, posterior_token, verifier_hidden[:, :accepted_inputs, :]
+
+
+def verify_block_parallel_greedy_argmax(
+    target: Any,
+    target_cache: list[Any],
+    block_tokens: list[int],
+    draft_block_size: int,
+    temperature: float,
+    layer_ids: list[int],
+    profile: dict[str, float] | None = None,
+) -> tuple[int, int, torch.Tensor]:
+    """runtime.py:246-292: the verifier's normed hidden states, then the
+    target's lm_head_argmax hook (here the fused LM-head greedy kernel: no
+    logits are materialised), the prefix compare and the rollback."""
+    if temperature >= 1e-5:
+        raise ValueError("parallel-greedy-argmax only supports temperature=0.")
+    state_start = profile_start(profile)
+    norm_hidden_states, verifier_hidden, rollback_records = target.forward_verifier_states(
+        _block_tensor(block_tokens, _target_device(target)), target_cache, layer_ids)
+    add_profile_elapsed(profile, "verify_state_time_s", state_start)
+
+    argmax_start = profile_start(profile)
+    posterior = target.lm_head_argmax(norm_hidden_states)[0].cpu().tolist()
+    add_profile_elapsed(profile, "verify_argmax_time_s", argmax_start)
+
+    prefix_start = profile_start(profile)
+    matched = longest_prefix_match(block_tokens[1:], posterior[:-1])
+    accepted_inputs = matched + 1
+    add_profile_elapsed(profile, "verify_prefix_time_s", prefix_start)
+    _rollback(target, target_cache, rollback_records, draft_block_size, accepted_inputs, profile)
+    return accepted_inputs, posterior[matched], verifier_hidden[:, :accepted_inputs, :]
+
+
+def verify_block_chunked(
+    target: Any,
+    target_cache: list[Any],
+    block_tokens: list[int],
+    draft_block_size: int,
+    temperature: float,
+    layer_ids: list[int],
+    verify_chunk_size: int,
+) -> tuple[int, int, torch.Tensor]:
+    """runtime.py:295-357: verify in chunks; on a mismatch restore the
+    chunk's linear caches from a snapshot and re-run only its accepted
+    prefix."""
+    dev = _target_device(target)
+    verified_hidden_chunks: list[torch.Tensor] = []
+    cursor = 0
+    while cursor < draft_block_size:
+        chunk_end = min(cursor + verify_chunk_size, draft_block_size)
+        chunk_tokens = block_tokens[cursor:chunk_end]
+        linear_snapshots = target.snapshot_linear_caches(target_cache)
+        chunk_logits, chunk_hidden = target.forward_with_hidden_states(
+            _block_tensor(chunk_tokens, dev), target_cache, layer_ids)
+        posterior_chunk = _posterior(chunk_logits, temperature)
+
+        max_compare = min(len(chunk_tokens), draft_block_size - cursor - 1)
+        local_matches = 0
+        while local_matches < max_compare:
+            if posterior_chunk[local_matches] != block_tokens[cursor + local_matches + 1]:
+                break
+            local_matches += 1
+
+        if local_matches == max_compare and chunk_end < draft_block_size:
+            verified_hidden_chunks.append(chunk_hidden)
+            cursor = chunk_end
+            continue
+        if local_matches == max_compare and chunk_end == draft_block_size:
+            verified_hidden_chunks.append(chunk_hidden)
+            return (draft_block_size, posterior_chunk[-1],
+                    torch.cat(verified_hidden_chunks, dim=1))
+
+        accepted_local_inputs = local_matches + 1
+        target.rewind_kv_caches(target_cache, len(chunk_tokens))
+        target.restore_linear_caches(target_cache, linear_snapshots)
+        replay_hidden = target.forward_with_hidden_states(
+            _block_tensor(chunk_tokens[:accepted_local_inputs], dev), target_cache, layer_ids)[1]
+        verified_hidden_chunks.append(replay_hidden)
+        return (cursor + accepted_local_inputs, posterior_chunk[local_matches],
+                torch.cat(verified_hidden_chunks, dim=1))
+    raise RuntimeError("Chunked verifier reached an impossible state.")
+
+
+VERIFY_MODES = ("parallel-replay", "parallel-greedy-argmax", "parallel-lazy-logits", "stream",
+                "chunked")
+
+
+def dflash_generate_stream(
+    target: Any,
+    draft: Any,
+    prompt_tokens: torch.Tensor | Sequence[int],
+    max_new_tokens: int,
+    temperature: float,
+    stop_token_ids: set[int],
+    layer_ids: list[int],
+    speculative_tokens: int | None,
+    verify_mode: str,
+    verify_chunk_size: int,
+    profile: bool = False,
+) -> Iterator[DFlashRuntimeEvent]:
+    """The DFlash decode loop (runtime.py:360-555): prefill the prompt, then
+    repeatedly draft a block [last token, drafts...] from the target hidden
+    states, verify it, keep the accepted prefix plus the posterior's bonus
+    token, and stop at max_new_tokens or a stop token.  Yields the new tokens
+    after the prefill and after every block, then a final event with the
+    metrics."""
+    if verify_mode not in VERIFY_MODES:
+        raise ValueError(f"unknown verify_mode {verify_mode!r}; one of {VERIFY_MODES}")
+    prompt = torch.as_tensor(prompt_tokens).reshape(-1)
+    dev = _target_device(target)
+    target_cache = target.make_cache()
+    draft_cache = draft.make_cache()
+    profile_times: dict[str, float] | None = {} if profile else None
+    prompt_len = int(prompt.shape[0])
+    total_max_tokens = prompt_len + max_new_tokens
+    if speculative_tokens is None:
+        block_size = draft.block_size
+    else:
+        block_size = max(1, min(speculative_tokens, draft.block_size))
+
+    sync_start = time.perf_counter()
+    logits, target_hidden = target.forward_with_hidden_states(
+        prompt.to(device=dev, dtype=torch.int32)[None], target_cache, layer_ids)
+    first_token = _posterior(logits[:, -1:, :], temperature)[0]
+    prefill_time = time.perf_counter() - sync_start
+
+    output_tokens = prompt.tolist() + [first_token]
+    start = prompt_len
+    streamed_len = prompt_len
+    acceptance_lengths: list[int] = []
+
+    if max_new_tokens > 0:
+        yield DFlashRuntimeEvent(token_ids=output_tokens[streamed_len:],
+                                 output_tokens=list(output_tokens))
+        streamed_len = len(output_tokens)
+
+    decode_start = time.perf_counter()
+    while start < total_max_tokens:
+        draft_start = profile_start(profile_times)
+        block_tokens = [output_tokens[start]] + [draft.mask_token_id] * (block_size - 1)
+        noise_embedding = target.embed_tokens(_block_tensor(block_tokens, dev))
+        draft_hidden = draft(noise_embedding=noise_embedding, target_hidden=target_hidden,
+                             cache=draft_cache)
+        draft_logits = target.lm_head_logits(draft_hidden[:, 1:, :])
+        drafted_suffix = sample_tokens(draft_logits, temperature)[0].cpu().tolist()
+        trim_draft_cache(draft_cache, block_size)
+        block_tokens[1:] = drafted_suffix[: block_size - 1]
+        add_profile_elapsed(profile_times, "draft_time_s", draft_start)
+
+        verify_start = profile_start(profile_times)
+        if verify_mode == "stream":
+            accepted_inputs, posterior_token, verifier_hidden = verify_block_stream(
+                target, target_cache, block_tokens, temperature, layer_ids)
+        elif verify_mode == "chunked":
+            accepted_inputs, posterior_token, verifier_hidden = verify_block_chunked(
+                target, target_cache, block_tokens, block_size, temperature, layer_ids,
+                verify_chunk_size)
+        elif verify_mode == "parallel-lazy-logits":
+            accepted_inputs, posterior_token, verifier_hidden = verify_block_parallel_lazy_logits(
+                target, target_cache, block_tokens, block_size, temperature, layer_ids,
+                verify_chunk_size, profile=profile_times)
+        elif verify_mode == "parallel-greedy-argmax":
+            accepted_inputs, posterior_token, verifier_hidden = \
+                verify_block_parallel_greedy_argmax(target, target_cache, block_tokens, block_size,
+                                                    temperature, layer_ids, profile=profile_times)
+        else:
+            accepted_inputs, posterior_token, verifier_hidden = verify_block_parallel_replay(
+                target, target_cache, block_tokens, block_size, temperature, layer_ids,
+                profile=profile_times)
+        acceptance_lengths.append(accepted_inputs)
+        target_hidden = verifier_hidden[:, :accepted_inputs, :]
+        add_profile_elapsed(profile_times, "verify_time_s", verify_start)
+
+        bookkeeping_start = profile_start(profile_times)
+        output_tokens = output_tokens[:start]
+        output_tokens.extend(block_tokens[:accepted_inputs])
+        output_tokens.append(posterior_token)
+        start += accepted_inputs
+        add_profile_elapsed(profile_times, "bookkeeping_time_s", bookkeeping_start)
+
+        stop_idx = stop_position(output_tokens, prompt_len, stop_token_ids)
+        finished = False
+        if stop_idx is not None:
+            output_tokens = output_tokens[: stop_idx + 1]
+            finished = True
+        if len(output_tokens) > total_max_tokens:
+            output_tokens = output_tokens[:total_max_tokens]
+            finished = True
+
+        token_ids = output_tokens[streamed_len:]
+        if token_ids:
+            yield DFlashRuntimeEvent(token_ids=token_ids, output_tokens=list(output_tokens))
+            streamed_len = len(output_tokens)
+        if finished:
+            break
+
+    decode_time = time.perf_counter() - decode_start
+    output_tokens = output_tokens[:total_max_tokens]
+    generated_tokens = generated_token_count(output_tokens, prompt_len)
+    total_time = prefill_time + decode_time
+    metrics: dict[str, Any] = {
+        "num_input_tokens": prompt_len,
+        "num_output_tokens": generated_tokens,
+        "prefill_time_s": prefill_time,
+        "decode_time_s": decode_time,
+        "total_time_s": total_time,
+        "prompt_tps": prompt_len / max(prefill_time, 1e-9),
+        "generation_tps": generated_tokens / max(decode_time, 1e-9),
+        "end_to_end_tps": generated_tokens / max(total_time, 1e-9),
+        "avg_acceptance_length": sum(acceptance_lengths) / max(len(acceptance_lengths), 1),
+        "acceptance_lengths": acceptance_lengths,
+        "peak_memory_gb": peak_memory_gb(),
+        "target_cache_summary": target.cache_summary(target_cache),
+        "speculative_tokens": block_size,
+    }
+    if profile_times is not None:
+        profiled_time = sum(profile_times.get(key, 0.0)
+                            for key in ("draft_time_s", "verify_time_s", "bookkeeping_time_s"))
+        metrics["profile"] = {**profile_times,
+                              "unattributed_decode_time_s": decode_time - profiled_time,
+                              "steps": len(acceptance_lengths)}
+    yield DFlashRuntimeEvent(token_ids=[], output_tokens=list(output_tokens), metrics=metrics,
+                             finished=True)
+
+
+def dflash_generate(
+    target: Any,
+    draft: Any,
+    prompt_tokens: torch.Tensor | Sequence[int],
+    max_new_tokens: int,
+    temperature: float,
+    stop_token_ids: set[int],
+    layer_ids: list[int],
+    speculative_tokens: int | None,
+    verify_mode: str,
+    verify_chunk_size: int,
+    profile: bool = False,
+) -> tuple[list[int], dict[str, Any]]:
+    """runtime.py:558-589: run the stream to the end; (output_tokens, metrics)."""
+    final_event: DFlashRuntimeEvent | None = None
+    for event in dflash_generate_stream(
+        target=target, draft=draft, prompt_tokens=prompt_tokens, max_new_tokens=max_new_tokens,
+        temperature=temperature, stop_token_ids=stop_token_ids, layer_ids=layer_ids,
+        speculative_tokens=speculative_tokens, verify_mode=verify_mode,
+        verify_chunk_size=verify_chunk_size, profile=profile,
+    ):
+        if event.finished:
+            final_event = event
+    if final_event is None or final_event.metrics is None:
+        raise RuntimeError("DFlash generation did not produce a final event.")
+    return final_event.output_tokens, final_event.metrics

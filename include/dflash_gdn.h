@@ -32,7 +32,7 @@
 extern "C" {
 #endif
 
-#define DFLASH_ABI_VERSION 1
+#define DFLASH_ABI_VERSION 2
 
 /* Argument-validation codes (negative).  Positive values are hipError_t. */
 #define DFLASH_OK 0
@@ -421,6 +421,25 @@ int dflash_add_rmsnorm_splitk(const void* x, const float* r_partials,
                               void* y, int M, int H, float eps, void* stream);
 
 /*
+ * dflash_add_rmsnorm (r_partials NULL) or dflash_add_rmsnorm_splitk (r NULL)
+ * that also stores the new residual stream h to h_copy (row m at
+ * h_copy + m * h_copy_row_stride, bf16; stride % 8 == 0, >= H).
+ *
+ * Replaces the capture of the target hidden states the drafter reads:
+ * `selected_hidden_states.append(hidden_states)` after each layer in
+ * layer_ids and the concatenation along the feature axis
+ * (dflash_mlx/custom_qwen35_model.py:984-991, adapters.py:402-414).  The
+ * residual stream after layer i is complete in the add that opens layer
+ * i + 1 (or the final norm), so the caller points h_copy at that layer's
+ * column block of the [M, n_layers * H] capture buffer.
+ */
+int dflash_add_rmsnorm_capture(const void* x, const void* r,
+                               const float* r_partials, int nsplit,
+                               const void* weight, void* h_out, void* h_copy,
+                               int64_t h_copy_row_stride, void* y, int M,
+                               int H, float eps, void* stream);
+
+/*
  * The step's first norm with the embedding lookup folded in
  * (Qwen3_5TextModel: embed_tokens(inputs) then layer 0's input_layernorm,
  * custom_qwen35_model.py:866-869, :841):
@@ -523,15 +542,19 @@ int dflash_swiglu(const void* gate_up, void* out, int M, int I, void* stream);
  * value cache transposed, [B, Hkv, D, Smax] (keys contiguous per feature).
  * Rotary (nn.RoPE, traditional=False): feature i < rot_dims/2 pairs with
  * i + rot_dims/2 at angle pos * rope_base^(-2i/rot_dims); features past
- * rot_dims pass through.  Positions >= Smax are not written (the caller keeps
- * lens + T <= Smax).  Supported: D == 128, rot_dims in {0,16,32,64,128}.
+ * rot_dims pass through.  Positions outside [0, Smax) are never written: the
+ * caller keeps 0 <= lens[b] and lens[b] + T <= Smax, and when overflow is not
+ * NULL ([B] int32, cleared by the caller) the kernel sets overflow[b] = 1 for
+ * every sequence that had a position outside the cache, so the host can
+ * refuse that step's output at its next synchronisation.
+ * Supported: D == 128, rot_dims in {0,16,32,64,128}.
  */
 int dflash_attn_prep(const void* proj, int64_t proj_row_stride,
                      const void* q_norm_w, const void* k_norm_w,
                      const int32_t* lens, void* k_cache, void* vt_cache,
-                     void* q_out, int B, int T, int Hq, int Hkv, int D,
-                     int Smax, int rot_dims, float rope_base, float eps,
-                     void* stream);
+                     void* q_out, int32_t* overflow, int B, int T, int Hq,
+                     int Hkv, int D, int Smax, int rot_dims, float rope_base,
+                     float eps, void* stream);
 
 /*
  * Verify attention over the cache (custom_qwen35_model.py:524-534): causal

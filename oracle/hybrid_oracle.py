@@ -21,6 +21,9 @@ delta layers:
   (query t of the block sees keys 0 .. offset + t), output * sigmoid(gate);
 * ``model_step``: the whole verify step of a (small) hybrid model built from
   the above and the gated-delta oracle (oracle.py), for end-to-end parity.
+  Run over a whole generated sequence at once (teacher forcing), it checks
+  each greedy choice of a decode (the reference's exactness gate compares
+  DFlash output with plain greedy generation, ADDING_MODELS.md:76-137).
 """
 from __future__ import annotations
 
@@ -162,13 +165,17 @@ def model_step(cfg, weights, state, tokens, eps=1e-6):
     of the bf16 weights); state: dict with 'conv' [Lg][B,K-1,C], 'rec'
     [Lg][B,Hv,Dv,Dk], 'k'/'v' [La][B,Hkv,S,D], 'lens' [B]; tokens [B, T].
     Returns dict(hidden [B,T,H] (final normed), posterior, matched, bonus,
-    qkv [Lg][B,T,C], k_new/v_new [La][B,T,Hkv,D], tape [Lg][T,B,Hv,Dv,Dk])."""
+    qkv [Lg][B,T,C], k_new/v_new [La][B,T,Hkv,D], tape [Lg][T,B,Hv,Dv,Dk],
+    layer_hidden [L][B,T,H] (the residual stream after each layer, what
+    forward_dflash captures at layer_ids, custom_qwen35_model.py:984-991)).
+    The gated-delta q/k RMSNorm uses eps 1e-6 whatever ``eps`` is
+    (custom_qwen35_model.py:446-447); ``eps`` sets every other norm."""
     lc = cfg.linear
     B, T = tokens.shape
     H = cfg.hidden_size
     h = weights["embed"][tokens.reshape(-1)].reshape(B * T, H)
     r = None
-    res = dict(qkv=[], tape=[], k_new=[], v_new=[])
+    res = dict(qkv=[], tape=[], k_new=[], v_new=[], layer_hidden=[])
     gi = ai = 0
     for i in range(cfg.num_hidden_layers):
         lw = weights["layers"][i]
@@ -183,7 +190,7 @@ def model_step(cfg, weights, state, tokens, eps=1e-6):
             aa = proj[:, C + Hv * Dv + Hv:C + Hv * Dv + 2 * Hv].reshape(B, T, Hv)
             q, k, v, g, beta, _ = gdn.gdn_prologue(
                 qkv, state["conv"][gi], lw["conv_w"], aa, bb, lw["A_log"], lw["dt_bias"],
-                lc.linear_num_key_heads, Hv, lc.linear_key_head_dim, Dv, eps)
+                lc.linear_num_key_heads, Hv, lc.linear_key_head_dim, Dv, 1e-6)
             q, k, v = bf16(q), bf16(k), bf16(v)
             out, _, tape = gdn.scan_c(q, k, v, g, beta, state["rec"][gi], acc64=True)
             y = bf16(gdn.gated_rmsnorm(bf16(out), z, lw["norm_w"], eps))
@@ -216,6 +223,7 @@ def model_step(cfg, weights, state, tokens, eps=1e-6):
         x = bf16(x)
         act = bf16(swiglu(x @ lw["w_gu"].T))  # gating fused into the gate|up GEMM: one rounding
         r = bf16(act @ lw["w_down"].T)
+        res["layer_hidden"].append(bf16(h + r).reshape(B, T, H))
     h, x = add_rmsnorm(h, r, weights["final_norm"], eps)
     x = bf16(x)
     logits = x @ weights["lm_head"].T
@@ -225,3 +233,4 @@ def model_step(cfg, weights, state, tokens, eps=1e-6):
     res.update(hidden=x.reshape(B, T, H), logits=logits.reshape(B, T, -1), posterior=posterior,
                matched=matched, bonus=bonus)
     return res
+

@@ -40,7 +40,7 @@ def test_header_declares_expected_entry_points():
         "dflash_gdn_chunked_prefill_workspace_bytes", "dflash_gdn_chunked_prefill",
         "dflash_add_rmsnorm", "dflash_swiglu", "dflash_attn_prep",
         "dflash_attn_verify_workspace_bytes", "dflash_attn_verify", "dflash_commit_accept",
-        "dflash_add_rmsnorm_splitk", "dflash_embed_rmsnorm", "dflash_gemm_bf16", "dflash_gemm_splits",
+        "dflash_add_rmsnorm_splitk", "dflash_add_rmsnorm_capture", "dflash_embed_rmsnorm", "dflash_gemm_bf16", "dflash_gemm_splits",
         "dflash_splitk_reduce", "dflash_gemm_bf16_swiglu", "dflash_weight_tile_bytes",
         "dflash_weight_tile_bf16", "dflash_gemm_bf16_tiled", "dflash_gemm_bf16_swiglu_tiled",
     ])
@@ -64,7 +64,7 @@ def test_library_targets_gfx950_only():
 
 
 def test_abi_version_and_strerror(lib):
-    assert lib.dflash_abi_version() == 1
+    assert lib.dflash_abi_version() == 2
     assert lib.dflash_strerror(0) == b"ok"
     assert b"NULL" in lib.dflash_strerror(-1)
     assert lib.dflash_strerror(-999) == b"unknown dflash error"
@@ -147,7 +147,7 @@ def test_model_op_size_limits(lib):
     assert lib.dflash_gdn_prologue(d, 0, 0, d, d, d, d, None, d, d, d, d, d, d,
                                    big, big, 4, 16, 32, 128, 128, 1e-6, None) == -2
     # attention prep: B*T workgroups > 2^31 - 1
-    assert lib.dflash_attn_prep(d, 5120, d, d, d, d, d, d, big, big, 16, 4, 128, 4096,
+    assert lib.dflash_attn_prep(d, 5120, d, d, d, d, d, d, None, big, big, 16, 4, 128, 4096,
                                 64, 1e7, 1e-6, None) == -2
     # attention: B beyond the partial kernel's grid.z
     assert lib.dflash_attn_verify(d, d, d, d, d, 4096, d, 70000, 16, 16, 4, 128, 4096, 4096,

@@ -88,7 +88,7 @@ def _attn_prep(device, B, T, lens, Smax, seed):
     q = torch.empty(B, T, Hq, D, dtype=torch.bfloat16, device=device)
     _lib.call("dflash_attn_prep", pd.data_ptr(), rows, qnd.data_ptr(),
               knd.data_ptr(), lens_d.data_ptr(), kc.data_ptr(), vtc.data_ptr(),
-              q.data_ptr(), B, T, Hq, Hkv, D, Smax, C4["rot"], C4["base"], 1e-6,
+              q.data_ptr(), None, B, T, Hq, Hkv, D, Smax, C4["rot"], C4["base"], 1e-6,
               _lib.stream_handle(device))
     torch.cuda.synchronize()
     ref = ho.attn_prep(_np(proj), _np(qn), _np(kn), np.array(lens), B, T, Hq, Hkv, D, C4["rot"],

@@ -48,7 +48,7 @@ def test_kv_trim_is_offset_arithmetic():
 
 def test_make_cache_pattern_is_3_to_1():
     """custom_qwen35_model.py:818: layer i is linear unless (i+1) % 4 == 0."""
-    cache = Qwen35TargetAdapter().make_cache(32)
+    cache = Qwen35TargetAdapter().make_cache(num_layers=32)
     kinds = ["kv" if isinstance(c, KVCache) else "ssm" for c in cache]
     assert kinds.count("ssm") == 24 and kinds.count("kv") == 8
     assert [i for i, k in enumerate(kinds) if k == "kv"] == [3, 7, 11, 15, 19, 23, 27, 31]
@@ -81,3 +81,19 @@ def test_accept_inputs_have_the_drawn_accept_length(cfg_id):
     acc = make_accept_inputs(cfg)
     post, matched, _ = orc.greedy_accept(acc["logits"].numpy(), acc["draft"].numpy())
     np.testing.assert_array_equal(matched, acc["accept"].numpy())
+
+
+def test_cache_lengths_are_checked_on_the_host():
+    """The hybrid runner refuses cache lengths whose next block would fall
+    outside the KV cache before any launch (dflash_attn_prep never writes
+    there and flags such a sequence)."""
+    import pytest
+    from dflash_mlx.hybrid_model import check_cache_lengths
+
+    assert check_cache_lengths([0, 4080], 2, 16, 4096).tolist() == [0, 4080]
+    with pytest.raises(ValueError):
+        check_cache_lengths([4081], 1, 16, 4096)  # 4081 + 16 > 4096
+    with pytest.raises(ValueError):
+        check_cache_lengths([-1, 3], 2, 16, 4096)
+    with pytest.raises(ValueError):
+        check_cache_lengths([1, 2, 3], 2, 16, 4096)
