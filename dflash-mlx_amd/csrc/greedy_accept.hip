@@ -19,6 +19,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
+
 #include "accept_common.h"
 #include "conv_window.h"
 #include "dflash_gdn.h"
@@ -339,3 +342,79 @@ extern "C" int dflash_greedy_accept_conv_rollback(
   return DFLASH_OK;
 }
 
+// ------------------------------------------------ allocation-free variant
+// The argmax keys of dflash_greedy_accept_noalloc live in this file-scope
+// device array instead of a caller workspace.  Every device the library runs
+// on holds one copy for the life of the process; its device address comes
+// from hipGetSymbolAddress once per device (the array's name in host code is
+// only a host-side stand-in, never a device address).  Every key slot a call
+// uses is written by its argmax launch before the finalize reads it, so
+// nothing needs clearing; calls that overlap on one device share the array
+// and race.
+namespace dflash {
+namespace {
+constexpr size_t kNoAllocScratchBytes = size_t(1) << 20;
+constexpr int kMaxDevices = 64;
+}  // namespace
+}  // namespace dflash
+
+static __device__ __align__(256) uint64_t scratch[dflash::kNoAllocScratchBytes / sizeof(uint64_t)];
+
+namespace dflash {
+namespace {
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mutex;
+
+// Device address of `scratch` on the current device (resolved on the first
+// call made with that device current); nullptr with *status set on failure.
+uint64_t* scratch_for_current_device(int* status) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *status = (int)e;
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    *status = DFLASH_ERR_UNSUPPORTED;
+    return nullptr;
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p != nullptr) return static_cast<uint64_t*>(p);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+  if (p == nullptr) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr) {
+      *status = e != hipSuccess ? (int)e : DFLASH_ERR_NULL;
+      return nullptr;
+    }
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  return static_cast<uint64_t*>(p);
+}
+}  // namespace
+}  // namespace dflash
+
+extern "C" size_t dflash_greedy_accept_noalloc_max_bytes(void) {
+  return dflash::kNoAllocScratchBytes;
+}
+
+extern "C" int dflash_greedy_accept_noalloc(const void* logits, int logits_dtype,
+                                            int64_t logits_batch_stride,
+                                            int64_t logits_row_stride, const int32_t* draft,
+                                            int64_t draft_stride, int n_draft,
+                                            int32_t* posterior, int32_t* matched,
+                                            int32_t* bonus, int B, int N, int V, void* stream) {
+  using namespace dflash;
+  if (B < 0 || N <= 0 || V <= 0 || n_draft < 0) return DFLASH_ERR_SHAPE;
+  if (N > kMaxAcceptRows || (int64_t)B * N > INT32_MAX) return DFLASH_ERR_SHAPE;
+  if (B == 0) return DFLASH_OK;
+  const size_t need = dflash_greedy_accept_workspace_bytes(B, N, V);
+  if (need > kNoAllocScratchBytes) return DFLASH_ERR_WORKSPACE;
+  int status = DFLASH_OK;
+  uint64_t* keys = scratch_for_current_device(&status);
+  if (keys == nullptr) return status;
+  return dflash_greedy_accept(logits, logits_dtype, logits_batch_stride, logits_row_stride, draft,
+                              draft_stride, n_draft, posterior, matched, bonus, B, N, V, keys,
+                              kNoAllocScratchBytes, stream);
+}

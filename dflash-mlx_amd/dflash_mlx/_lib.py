@@ -75,6 +75,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "dflash_commit_accept": (_I, [_VP, _VP, _VP, _I, _I, _VP]),
     "dflash_greedy_accept_workspace_bytes": (_SZ, [_I, _I, _I]),
+    "dflash_greedy_accept_noalloc_max_bytes": (_SZ, []),
+    "dflash_greedy_accept_noalloc": (
+        _I, [_VP, _I, _I64, _I64, _VP, _I64, _I, _VP, _VP, _VP, _I, _I, _I, _VP]),
     "dflash_greedy_accept": (
         _I,
         [_VP, _I, _I64, _I64, _VP, _I64, _I, _VP, _VP, _VP, _I, _I, _I, _VP, _SZ, _VP],

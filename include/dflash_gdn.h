@@ -8,7 +8,9 @@
  *     rejected before any launch, or a positive hipError_t when the launch
  *     itself fails;
  *   - allocates nothing, synchronises nothing and keeps no state between calls
- *     (so it is reentrant and ordered only by the stream it is given);
+ *     (so it is reentrant and ordered only by the stream it is given), except
+ *     dflash_greedy_accept_noalloc, whose scratch is one static device array
+ *     per device;
  *   - enqueues its kernels on `stream` (a hipStream_t; NULL = the null stream).
  *
  * Tensor conventions (row-major, innermost index last):
@@ -205,6 +207,30 @@ int dflash_greedy_accept(const void* logits, int logits_dtype,
                          int n_draft, int32_t* posterior, int32_t* matched,
                          int32_t* bonus, int B, int N, int V, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/*
+ * dflash_greedy_accept without a workspace argument and without allocating:
+ * no reference counterpart; for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The argmax keys go to a static device array of
+ * dflash_greedy_accept_noalloc_max_bytes() bytes (1 MiB) that each device
+ * holds until the process ends; shapes whose
+ * dflash_greedy_accept_workspace_bytes(B, N, V) exceeds it are refused with
+ * DFLASH_ERR_WORKSPACE before any launch (that is B * N > 131072 logits
+ * rows, at any vocabulary size).  Calls on one device share the array, so
+ * calls that overlap in time on one device race.  The first call with a
+ * device current resolves the array's address on that device
+ * (hipGetSymbolAddress).  Arguments and outputs as dflash_greedy_accept,
+ * bit for bit.
+ */
+size_t dflash_greedy_accept_noalloc_max_bytes(void);
+int dflash_greedy_accept_noalloc(const void* logits, int logits_dtype,
+                                 int64_t logits_batch_stride,
+                                 int64_t logits_row_stride,
+                                 const int32_t* draft, int64_t draft_stride,
+                                 int n_draft, int32_t* posterior,
+                                 int32_t* matched, int32_t* bonus, int B, int N,
+                                 int V, void* stream);
 
 /*
  * Gated-delta layer prologue: everything between the input projections and

@@ -33,6 +33,7 @@ def test_header_declares_expected_entry_points():
         "dflash_abi_version", "dflash_strerror", "dflash_gdn_verify_scan",
         "dflash_gdn_verify_scan_rollback", "dflash_gdn_replay",
         "dflash_greedy_accept_workspace_bytes", "dflash_greedy_accept", "dflash_tape_select",
+        "dflash_greedy_accept_noalloc_max_bytes", "dflash_greedy_accept_noalloc",
         "dflash_conv_rollback", "dflash_lm_head_accept_workspace_bytes",
         "dflash_lm_head_greedy_accept", "dflash_gdn_prologue", "dflash_gdn_gated_rmsnorm",
         "dflash_gdn_prologue_scan_rollback", "dflash_lm_head_greedy_accept_tiled",
