@@ -3,24 +3,31 @@
 
 Workload (config c1): Qwen3.5-4B-shaped verify block, B=1, T=16, Hk=16, Hv=32,
 Dk=Dv=128, for all 24 gated-delta layers (stacked as batch entries of one scan
-launch), greedy accept over [16, 151936] fp32 logits, and the cache rollback
-to the accepted length (recurrent state + conv window, conv_dim 8192).
+launch), greedy accept over [16, 151936] fp32 logits with the reference's
+wiring (drafts block[1:] against posterior rows 0..14, bonus from the row of
+the first mismatch, accepted_inputs = matched + 1), and the cache rollback to
+the accepted length (recurrent state + conv window, conv_dim 8192).
 
 Two step forms are timed, both through the C ABI with preallocated buffers and
 inputs resident in HBM:
   fused    (headline)  scan whose state load performs the previous step's
                        rollback (state read from the previous tape at the
-                       device-side accepted count) -> greedy accept + conv
+                       device-side keep count) -> greedy accept + conv
                        rollback (argmax slices, then the accept's finalize
-                       inside the window copy).  3 kernels, no host sync.  Timed eagerly with
+                       inside the window copy, which also writes the keep
+                       count).  3 kernels, no host sync.  Timed eagerly with
                        HIP events between phases (the breakdown) and as K
                        replays of the step captured as one HIP graph (the
                        value: how the device-driven serving loop launches it).
-  explicit             scan (+ final state) -> greedy accept -> tape gather of
-                       all 24 layers' states -> conv rollback.  Eager.
-Prints one JSON line.
+  explicit             scan (+ final state) -> greedy accept + keep ->
+                       tape gather of all 24 layers' states -> conv rollback.
+                       Eager.
+The c1 line also carries configs c0 (the reference's tiny CPU-runnable case)
+and c2 (B = 32 serving batch) under "configs", each with its own roofline and
+CPU baseline.  Prints one JSON line.
 
 python bench.py [--steps K] [--warmup W] [--config 0|1|2] [--cpu-seconds S]
+                [--no-configs] [--no-extras] [--only lm_head|layer|prefill|hybrid]
 """
 from __future__ import annotations
 
@@ -52,7 +59,12 @@ def parse_args():
                     help="0: the reference's tiny CPU-runnable case (latency-bound); "
                          "1: the headline (default); 2: batched serving, B=32")
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
-                    help="bounded CPU-baseline sample (0 disables it)")
+                    help="bounded CPU-baseline sample of the headline config (0 disables it)")
+    ap.add_argument("--cpu-seconds-other", type=float, default=4.0,
+                    help="bounded CPU-baseline sample of each of c0 and c2")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="measure only --config (by default the c1 headline also carries c0 "
+                         "and c2 under 'configs')")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the measurements of the next-row kernels (fused LM head)")
     ap.add_argument("--only", choices=("lm_head", "layer", "prefill", "hybrid"), default=None,
@@ -424,7 +436,7 @@ def measure_layer(torch, dev, L=24, B=1, T=16):
     }
 
 
-def cpu_baseline(cfg, x, acc, conv, seconds: float):
+def cpu_baseline(cfg, x, acc, block, conv, seconds: float):
     """The CPU oracle (C restatement, OpenMP over heads) running the same step
     on a bounded sample: whole steps repeated for ~`seconds`."""
     import numpy as np
@@ -434,7 +446,7 @@ def cpu_baseline(cfg, x, acc, conv, seconds: float):
     cores = host_cores()
     ins = [x[n].float().numpy() for n in ("q", "k", "v", "g", "beta", "state")]
     logits = acc["logits"].numpy()
-    draft = acc["draft"].numpy()
+    drafts = block[:, 1:].numpy()
     conv_in, qkv = conv
     conv_in_np = [c.float().numpy() for c in conv_in]
     qkv_np = [q.float().numpy() for q in qkv]
@@ -443,10 +455,11 @@ def cpu_baseline(cfg, x, acc, conv, seconds: float):
     t0 = time.perf_counter()
     while True:
         _, _, tape = orc.scan_c(*ins, threads=cores)
-        _, matched, _ = orc.greedy_accept_c(logits, draft)
-        orc.tape_select(tape, ins[5], np.tile(matched, L))
+        _, matched, _ = orc.greedy_accept_c(logits, drafts)  # block[1:] vs posterior rows
+        keep = np.asarray(matched) + 1                        # accepted_inputs
+        orc.tape_select(tape, ins[5], np.tile(keep, L))
         for l in range(L):
-            orc.conv_rollback(conv_in_np[l], qkv_np[l], matched)
+            orc.conv_rollback(conv_in_np[l], qkv_np[l], keep)
         steps += 1
         el = time.perf_counter() - t0
         if el >= seconds:
@@ -458,9 +471,163 @@ def cpu_baseline(cfg, x, acc, conv, seconds: float):
         "cores": cores,
         "kind": "port",
         "sample": f"{steps} full steps of {cfg.name} (scan+tape over {L} layers, accept over "
-                  f"[{B},{cfg.T},{cfg.V}] fp32, state gather + conv rollback) in {el:.1f} s; "
-                  "oracle/gdn_oracle.c fp32, OpenMP over heads",
+                  f"[{B},{cfg.T},{cfg.V}] fp32, state gather + conv rollback to matched + 1) in "
+                  f"{el:.1f} s; oracle/gdn_oracle.c fp32, OpenMP over heads",
     }
+
+
+def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
+                   probe_only: bool = False):
+    """One config's verify step (scan + tape, greedy accept with the
+    reference's wiring: drafts block[1:] against the posterior rows, keep =
+    matched + 1; state and conv rollback to keep), fused and explicit forms.
+    Returns the config's result dict (value, roofline, cpu_baseline, ...)."""
+    from dflash_mlx.step import StepShape, VerifyStepRunner
+    from dflash_mlx.workloads import ScanConfig, make_accept_inputs, make_scan_inputs, make_verify_block
+
+    L, B, T = cfg.layers, cfg.B, cfg.T
+    shape = StepShape(L=L, B=B, T=T, Hk=cfg.Hk, Hv=cfg.Hv, Dk=cfg.Dk, Dv=cfg.Dv,
+                      V=cfg.V, conv_dim=CONV_DIM, K1=3)
+    print(f"[bench] {cfg.name}: building inputs", file=sys.stderr, flush=True)
+    x = make_scan_inputs(cfg)
+    acc = make_accept_inputs(ScanConfig(**{**cfg.__dict__, "layers": 1}), gen=x["_gen"])
+    block = make_verify_block(acc)
+    gen = x["_gen"]
+    conv_in = [torch.randn(B, 3, CONV_DIM, generator=gen).to(torch.bfloat16) for _ in range(L)]
+    qkv = [torch.randn(B, T, CONV_DIM, generator=gen).to(torch.bfloat16) for _ in range(L)]
+
+    runners = {}
+    for form in ("fused", "explicit"):
+        run = VerifyStepRunner(shape, dev)
+        for name in ("q", "k", "v", "g", "beta", "state"):
+            getattr(run, name).copy_(x[name])
+        run.logits.copy_(acc["logits"])
+        run.block.copy_(block)
+        for l in range(L):
+            run.conv_in[l].copy_(conv_in[l])
+            run.qkv[l].copy_(qkv[l])
+        runners[form] = run
+    torch.cuda.synchronize()
+
+    fused, explicit = runners["fused"], runners["explicit"]
+    print(f"[bench] {cfg.name}: warmup {warmup}", file=sys.stderr, flush=True)
+    for _ in range(max(warmup, 1)):
+        fused.run_fused()
+        explicit.run()
+    torch.cuda.synchronize()
+    # The drafts agree with the argmax on exactly the drawn accept length
+    # (capped at the T - 1 drafts a block holds).
+    want = [min(a, T - 1) for a in acc["accept"].tolist()]
+    for form, r in runners.items():
+        if r.matched.cpu().tolist() != want or r.keep.cpu().tolist() != [m + 1 for m in want]:
+            raise RuntimeError(f"{cfg.name} {form}: accept mismatch")
+    keep = [m + 1 for m in want]
+    if probe_only:
+        return {"probe": probe(torch, fused, explicit)}
+
+    K = steps
+    print(f"[bench] {cfg.name}: timing {K} fused + {K} explicit steps", file=sys.stderr, flush=True)
+    tf = time_steps(torch, K, [("scan", fused.scan_rolled),
+                               ("accept_rollback", fused.accept_conv_rollback)])
+    te = time_steps(torch, K, [("scan", explicit.scan), ("accept", explicit.accept),
+                               ("rollback", explicit.rollback)])
+    # The same fused step as the device-driven serving loop launches it: captured
+    # once as a HIP graph (no host work inside), W replays untimed, then K replays
+    # between synchronizes.  The eager per-phase timing above is the breakdown.
+    print(f"[bench] {cfg.name}: timing {K} graph replays of the fused step", file=sys.stderr,
+          flush=True)
+    cap = torch.cuda.Stream(device=dev)
+    cap.wait_stream(torch.cuda.current_stream(dev))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        fused.run_fused()
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    g0.record()
+    for _ in range(K):
+        graph.replay()
+    g1.record()
+    torch.cuda.synchronize()
+    tg = {"ms_per_step": (time.perf_counter() - t0) * 1e3 / K,
+          "gpu_step": g0.elapsed_time(g1) * 1e3 / K}
+    del graph
+
+    # Algorithmic HBM bytes.  Scan: bf16 q,k,v,out + fp32 g,beta + fp32 state
+    # read + tape (T states per head).  The fused scan also writes the
+    # rolled-back state for sequences that kept >= 1 token (every sequence:
+    # keep = matched + 1); the explicit scan writes the final state instead.
+    S_bytes = 4 * cfg.Hv * cfg.Dv * cfg.Dk
+    io = 2 * L * B * T * (2 * cfg.Hk * cfg.Dk + 2 * cfg.Hv * cfg.Dv) + 8 * L * B * T * cfg.Hv
+    n_wb = L * sum(1 for a in keep if a >= 1)
+    scan_fused_bytes = io + S_bytes * (L * B * (1 + T) + n_wb)
+    scan_expl_bytes = shape.scan_bytes()
+    accept_bytes = shape.accept_bytes()
+    conv_bytes = 2 * 2 * L * B * 3 * CONV_DIM
+    gather_bytes = 2 * S_bytes * L * B
+    tokens = B * T
+
+    achieved = scan_fused_bytes / (tf["scan"] / 1e6) / 1e9
+    roof = {
+        "bound": "hbm",
+        "kernel": "gdn_scan_kernel<DK,R> via dflash_gdn_verify_scan_rollback",
+        "achieved": round(achieved, 1),
+        "peak": PEAK_HBM_GBPS,
+        "unit": "GB/s",
+        "frac": round(achieved / PEAK_HBM_GBPS, 4),
+        "traffic": traffic_from_profiles(cfg.name),
+        "bytes_alg_per_launch": scan_fused_bytes,
+        "avg_launch_us": round(tf["scan"], 2),
+    }
+    r2 = lambda d: {k: round(v, 2) for k, v in d.items() if k != "ms_per_step"}
+    expl_scan_gbps = scan_expl_bytes / (te["scan"] / 1e6) / 1e9
+    res = {
+        "value": round(tokens / (tg["ms_per_step"] / 1e3), 1),
+        "unit": "tokens/s",
+        "ms_per_step": round(tg["ms_per_step"], 4),
+        "config": {
+            "workload": cfg.name, "B": B, "T": T, "Hk": cfg.Hk, "Hv": cfg.Hv,
+            "Dk": cfg.Dk, "Dv": cfg.Dv, "layers": L, "vocab": cfg.V, "conv_dim": CONV_DIM,
+            "accepted_inputs": keep,
+            "io": "bf16 q/k/v/out, fp32 g/beta/state/tape, fp32 logits",
+            "accept": "drafts block[1:] vs posterior rows 0..T-2, bonus = posterior[matched], "
+                      "keep = matched + 1 (runtime.py:145-147)",
+            "step": "fused: scan+tape with the previous step's state rollback in its load "
+                    "(1 launch) -> greedy accept + conv-window rollback (2 launches: argmax "
+                    "slices, then the accept's finalize inside the window copy, which also "
+                    "writes keep), replayed as one HIP graph",
+        },
+        "roofline": roof,
+        "graph_step_us": round(tg["gpu_step"], 2),
+        "eager_step": {"value": round(tokens / (tf["ms_per_step"] / 1e3), 1),
+                       "ms_per_step": round(tf["ms_per_step"], 4)},
+        "breakdown_us": r2(tf),
+        "step_hbm_gbps": round((scan_fused_bytes + accept_bytes + conv_bytes)
+                               / (tf["gpu_step"] / 1e6) / 1e9, 1),
+        "explicit_step": {
+            "value": round(tokens / (te["ms_per_step"] / 1e3), 1),
+            "ms_per_step": round(te["ms_per_step"], 4),
+            "breakdown_us": r2(te),
+            "scan_gbps": round(expl_scan_gbps, 1),
+            "scan_frac": round(expl_scan_gbps / PEAK_HBM_GBPS, 4),
+            "scan_bytes_alg": scan_expl_bytes,
+            "step_hbm_gbps": round((scan_expl_bytes + accept_bytes + gather_bytes + conv_bytes)
+                                   / (te["gpu_step"] / 1e6) / 1e9, 1),
+        },
+    }
+    del runners, fused, explicit
+    torch.cuda.empty_cache()
+    if cpu_seconds > 0:
+        print(f"[bench] {cfg.name}: cpu baseline (~{cpu_seconds:.0f} s)", file=sys.stderr,
+              flush=True)
+        res["cpu_baseline"] = cpu_baseline(cfg, x, acc, block, (conv_in, qkv), cpu_seconds)
+    else:
+        res["cpu_baseline"] = None
+    return res
 
 
 def main() -> int:
@@ -481,155 +648,42 @@ def main() -> int:
         print(json.dumps({args.only: fn[args.only](torch, dev)}), flush=True)
         return 0
 
-    from dflash_mlx.step import StepShape, VerifyStepRunner
-    from dflash_mlx.workloads import CONFIGS, ScanConfig, make_accept_inputs, make_scan_inputs
+    from dflash_mlx.workloads import CONFIGS
 
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
     dev = torch.device("cuda", 0)
     cfg = CONFIGS[args.config]
-    L, B, T = cfg.layers, cfg.B, cfg.T
-    shape = StepShape(L=L, B=B, T=T, Hk=cfg.Hk, Hv=cfg.Hv, Dk=cfg.Dk, Dv=cfg.Dv,
-                      V=cfg.V, conv_dim=CONV_DIM, K1=3)
-    print(f"[bench] {cfg.name}: building inputs", file=sys.stderr, flush=True)
-    x = make_scan_inputs(cfg)
-    acc = make_accept_inputs(ScanConfig(**{**cfg.__dict__, "layers": 1}), gen=x["_gen"])
-    gen = x["_gen"]
-    conv_in = [torch.randn(B, 3, CONV_DIM, generator=gen).to(torch.bfloat16) for _ in range(L)]
-    qkv = [torch.randn(B, T, CONV_DIM, generator=gen).to(torch.bfloat16) for _ in range(L)]
-
-    runners = {}
-    for form in ("fused", "explicit"):
-        run = VerifyStepRunner(shape, dev)
-        for name in ("q", "k", "v", "g", "beta", "state"):
-            getattr(run, name).copy_(x[name])
-        run.logits.copy_(acc["logits"])
-        run.draft.copy_(acc["draft"])
-        for l in range(L):
-            run.conv_in[l].copy_(conv_in[l])
-            run.qkv[l].copy_(qkv[l])
-        runners[form] = run
-    torch.cuda.synchronize()
-
-    fused, explicit = runners["fused"], runners["explicit"]
-    print(f"[bench] warmup {args.warmup}", file=sys.stderr, flush=True)
-    for _ in range(args.warmup):
-        fused.run_fused()
-        explicit.run()
-    torch.cuda.synchronize()
-    for form, r in runners.items():
-        # The draft agrees with the argmax on exactly the drawn accept length.
-        if r.matched.cpu().tolist() != acc["accept"].tolist():
-            print(f"[bench] {form}: accept mismatch", file=sys.stderr)
-            return 1
-    accepted = acc["accept"].tolist()
     if args.probe:
-        return probe(torch, fused, explicit)
-
-    K = args.steps
-    print(f"[bench] timing {K} fused + {K} explicit steps", file=sys.stderr, flush=True)
-    tf = time_steps(torch, K, [("scan", fused.scan_rolled),
-                               ("accept_rollback", fused.accept_conv_rollback)])
-    te = time_steps(torch, K, [("scan", explicit.scan), ("accept", explicit.accept),
-                               ("rollback", explicit.rollback)])
-    # The same fused step as the device-driven serving loop launches it: captured
-    # once as a HIP graph (no host work inside), W replays untimed, then K replays
-    # between synchronizes.  The eager per-phase timing above is the breakdown.
-    print(f"[bench] timing {K} graph replays of the fused step", file=sys.stderr, flush=True)
-    cap = torch.cuda.Stream(device=dev)
-    cap.wait_stream(torch.cuda.current_stream(dev))
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=cap):
-        fused.run_fused()
-    torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    g0.record()
-    for _ in range(K):
-        graph.replay()
-    g1.record()
-    torch.cuda.synchronize()
-    tg = {"ms_per_step": (time.perf_counter() - t0) * 1e3 / K,
-          "gpu_step": g0.elapsed_time(g1) * 1e3 / K}
-    del graph
-
-    # Algorithmic HBM bytes.  Scan: bf16 q,k,v,out + fp32 g,beta + fp32 state
-    # read + tape (16 states per head).  The fused scan also writes the
-    # rolled-back state for sequences that accepted >= 1 token; the explicit
-    # scan writes the final state instead.
-    S_bytes = 4 * cfg.Hv * cfg.Dv * cfg.Dk
-    io = 2 * L * B * T * (2 * cfg.Hk * cfg.Dk + 2 * cfg.Hv * cfg.Dv) + 8 * L * B * T * cfg.Hv
-    n_wb = L * sum(1 for a in accepted if a >= 1)
-    scan_fused_bytes = io + S_bytes * (L * B * (1 + T) + n_wb)
-    scan_expl_bytes = shape.scan_bytes()
-    accept_bytes = shape.accept_bytes()
-    conv_bytes = 2 * 2 * L * B * 3 * CONV_DIM
-    gather_bytes = 2 * S_bytes * L * B
-    tokens = B * T
-
-    achieved = scan_fused_bytes / (tf["scan"] / 1e6) / 1e9
-    roof = {
-        "bound": "hbm",
-        "kernel": "gdn_scan_kernel<128,R> via dflash_gdn_verify_scan_rollback",
-        "achieved": round(achieved, 1),
-        "peak": PEAK_HBM_GBPS,
-        "unit": "GB/s",
-        "frac": round(achieved / PEAK_HBM_GBPS, 4),
-        "traffic": traffic_from_profiles(cfg.name),
-        "bytes_alg_per_launch": scan_fused_bytes,
-        "avg_launch_us": round(tf["scan"], 2),
-    }
-    r2 = lambda d: {k: round(v, 2) for k, v in d.items() if k != "ms_per_step"}
-    expl_scan_gbps = scan_expl_bytes / (te["scan"] / 1e6) / 1e9
+        return measure_verify(torch, dev, cfg, args.steps, args.warmup, 0, probe_only=True)["probe"]
+    head = measure_verify(torch, dev, cfg, args.steps, args.warmup, args.cpu_seconds)
     line = {
         "metric": METRIC,
-        "value": round(tokens / (tg["ms_per_step"] / 1e3), 1),
-        "unit": "tokens/s",
+        "value": head.pop("value"),
+        "unit": head.pop("unit"),
         "n_gpus": 1,
-        "steps": K,
+        "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(tg["ms_per_step"], 4),
+        "ms_per_step": head.pop("ms_per_step"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": {
-            "workload": cfg.name, "B": B, "T": T, "Hk": cfg.Hk, "Hv": cfg.Hv,
-            "Dk": cfg.Dk, "Dv": cfg.Dv, "layers": L, "vocab": cfg.V, "conv_dim": CONV_DIM,
-            "accepted": accepted,
-            "io": "bf16 q/k/v/out, fp32 g/beta/state/tape, fp32 logits",
-            "step": "fused: scan+tape with the previous step's state rollback in its load "
-                    "(1 launch) -> greedy accept + conv-window rollback (2 launches: argmax "
-                    "slices, then the accept's finalize inside the window copy), replayed as "
-                    "one HIP graph",
-        },
-        "roofline": roof,
-        "graph_step_us": round(tg["gpu_step"], 2),
-        "eager_step": {"value": round(tokens / (tf["ms_per_step"] / 1e3), 1),
-                       "ms_per_step": round(tf["ms_per_step"], 4)},
-        "breakdown_us": r2(tf),
-        "step_hbm_gbps": round((scan_fused_bytes + accept_bytes + conv_bytes)
-                               / (tf["gpu_step"] / 1e6) / 1e9, 1),
-        "explicit_step": {
-            "value": round(tokens / (te["ms_per_step"] / 1e3), 1),
-            "ms_per_step": round(te["ms_per_step"], 4),
-            "breakdown_us": r2(te),
-            "scan_gbps": round(expl_scan_gbps, 1),
-            "scan_frac": round(expl_scan_gbps / PEAK_HBM_GBPS, 4),
-            "scan_bytes_alg": scan_expl_bytes,
-            "step_hbm_gbps": round((scan_expl_bytes + accept_bytes + gather_bytes + conv_bytes)
-                                   / (te["gpu_step"] / 1e6) / 1e9, 1),
-        },
+        "config": head.pop("config"),
+        "roofline": head.pop("roofline"),
+        "cpu_baseline": head.pop("cpu_baseline"),
     }
+    line.update(head)
+    if not args.no_configs and args.config == 1:
+        line["configs"] = {}
+        for ci in (0, 2):
+            c = CONFIGS[ci]
+            line["configs"][c.name] = measure_verify(torch, dev, c, args.steps, args.warmup,
+                                                     args.cpu_seconds_other)
     if not args.no_extras:
         print("[bench] next rows: fused LM head", file=sys.stderr, flush=True)
-        del runners, fused, explicit
         line["next_rows"] = {"lm_head_greedy_accept": measure_lm_head(torch, dev)}
         print("[bench] next rows: gated-delta layer prologue/epilogue", file=sys.stderr, flush=True)
         line["next_rows"]["gdn_layer"] = measure_layer(torch, dev)
@@ -637,11 +691,6 @@ def main() -> int:
         line["next_rows"]["chunked_prefill"] = measure_prefill(torch, dev)
         print("[bench] next rows: hybrid verify step (config c4)", file=sys.stderr, flush=True)
         line["next_rows"]["hybrid_verify_step"] = measure_hybrid(torch, dev)
-    if args.cpu_seconds > 0:
-        print(f"[bench] cpu baseline (~{args.cpu_seconds:.0f} s)", file=sys.stderr, flush=True)
-        line["cpu_baseline"] = cpu_baseline(cfg, x, acc, (conv_in, qkv), args.cpu_seconds)
-    else:
-        line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)
     return 0
 

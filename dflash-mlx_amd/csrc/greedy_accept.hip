@@ -169,13 +169,16 @@ hipError_t launch_partial(const void* logits, int64_t bs, int64_t rs, int B, int
 // keys (N rows x splits), prefix-compares
 // the draft as accept_finalize_kernel does, then copies its columns of the
 // window for a = matched + accepted_offset.  The workgroup (0, b, 0) of the
-// first launch (write_accept) also writes posterior / matched / bonus of b.
+// first launch (write_accept) also writes posterior / matched / bonus of b
+// and, when accepted_out is given, the clamped a (the keep count the next
+// step's rolled-back state load reads).
 // Dynamic LDS: N int32.
 template <typename U>
 __global__ __launch_bounds__(kConvThreads) void accept_conv_rollback_kernel(
     const uint64_t* __restrict__ keys, int splits, int N, const int32_t* __restrict__ draft,
     int64_t dstride, int n_draft, int32_t* __restrict__ posterior, int32_t* __restrict__ matched,
-    int32_t* __restrict__ bonus, int write_accept, int accepted_offset, const ConvTable tab, int T,
+    int32_t* __restrict__ bonus, int write_accept, int accepted_offset,
+    int32_t* __restrict__ accepted_out, const ConvTable tab, int T,
     int K1, int64_t Cu, int64_t qkv_bs, int64_t qkv_rs) {
   extern __shared__ int32_t post[];
   __shared__ int s_first;
@@ -224,6 +227,7 @@ __global__ __launch_bounds__(kConvThreads) void accept_conv_rollback_kernel(
     if (threadIdx.x == 0) {
       if (matched != nullptr) matched[b] = first;
       if (bonus != nullptr) bonus[b] = first < N ? post[first] : -1;
+      if (accepted_out != nullptr) accepted_out[b] = min(max(first + accepted_offset, 0), T);
     }
   }
   conv_window_copy<U>(tab, blockIdx.z, b, min(max(first + accepted_offset, 0), T), K1, Cu,
@@ -279,7 +283,8 @@ extern "C" int dflash_greedy_accept_conv_rollback(
     int64_t logits_row_stride, const int32_t* draft, int64_t draft_stride, int n_draft,
     int32_t* posterior, int32_t* matched, int32_t* bonus, int B, int N, int V, void* workspace,
     size_t workspace_bytes, const void* const* conv_in, const void* const* qkv,
-    void* const* conv_out, int accepted_offset, int L, int T, int K1, int64_t C,
+    void* const* conv_out, int accepted_offset, int32_t* accepted_out, int L, int T, int K1,
+    int64_t C,
     int64_t qkv_batch_stride, int64_t qkv_row_stride, int elem_bytes, void* stream) {
   using namespace dflash;
   if (B < 0 || N <= 0 || V <= 0 || n_draft < 0) return DFLASH_ERR_SHAPE;
@@ -296,6 +301,7 @@ extern "C" int dflash_greedy_accept_conv_rollback(
   if (workspace_bytes < dflash_greedy_accept_workspace_bytes(B, N, V)) return DFLASH_ERR_WORKSPACE;
   if ((uintptr_t)workspace % 8 != 0) return DFLASH_ERR_ALIGN;
   const bool conv = L > 0 && K1 > 0 && C > 0;
+  if (!conv && accepted_out != nullptr) return DFLASH_ERR_UNSUPPORTED;  // written by the copy
   ConvPlan pl{2, 0, 0, 0};
   if (conv) {
     const int st = conv_plan(conv_in, qkv, conv_out, L, T, K1, C, qkv_batch_stride,
@@ -327,15 +333,18 @@ extern "C" int dflash_greedy_accept_conv_rollback(
     if (pl.unit == 16)
       hipLaunchKernelGGL(accept_conv_rollback_kernel<u32x4>, grid, dim3(kConvThreads), lds, s,
                          keys, sp.splits, N, draft, draft_stride, n_draft, posterior, matched,
-                         bonus, first, accepted_offset, tab, T, K1, pl.Cu, pl.qbs, pl.qrs);
+                         bonus, first, accepted_offset, accepted_out, tab, T, K1, pl.Cu, pl.qbs,
+                         pl.qrs);
     else if (pl.unit == 4)
       hipLaunchKernelGGL(accept_conv_rollback_kernel<uint32_t>, grid, dim3(kConvThreads), lds, s,
                          keys, sp.splits, N, draft, draft_stride, n_draft, posterior, matched,
-                         bonus, first, accepted_offset, tab, T, K1, pl.Cu, pl.qbs, pl.qrs);
+                         bonus, first, accepted_offset, accepted_out, tab, T, K1, pl.Cu, pl.qbs,
+                         pl.qrs);
     else
       hipLaunchKernelGGL(accept_conv_rollback_kernel<uint16_t>, grid, dim3(kConvThreads), lds, s,
                          keys, sp.splits, N, draft, draft_stride, n_draft, posterior, matched,
-                         bonus, first, accepted_offset, tab, T, K1, pl.Cu, pl.qbs, pl.qrs);
+                         bonus, first, accepted_offset, accepted_out, tab, T, K1, pl.Cu, pl.qbs,
+                         pl.qrs);
     e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }

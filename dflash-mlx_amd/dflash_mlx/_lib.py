@@ -107,7 +107,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dflash_greedy_accept_conv_rollback": (
         _I,
         [_VP, _I, _I64, _I64, _VP, _I64, _I, _VP, _VP, _VP, _I, _I, _I, _VP, _SZ,  # accept
-         _VP, _VP, _VP, _I, _I, _I, _I, _I64, _I64, _I64, _I, _VP],  # conv rollback
+         _VP, _VP, _VP, _I, _VP, _I, _I, _I, _I64, _I64, _I64, _I, _VP],  # conv rollback
     ),
     "dflash_tape_select": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I64, _I64, _VP]),
     "dflash_conv_rollback": (

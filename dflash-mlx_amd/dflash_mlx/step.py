@@ -7,12 +7,15 @@ allocation), in the order of the reference's verify_block_parallel_replay
 
   1. gated-delta scan of all linear layers' inputs, writing out, the final
      state and the per-token state tape       (dflash_gdn_verify_scan)
-  2. greedy accept on the verify logits       (dflash_greedy_accept)
-  3. recurrent-state rollback by tape gather  (dflash_tape_select)
-  4. conv-window rollback                     (dflash_conv_rollback)
+  2. greedy accept on the verify logits       (dflash_greedy_accept): the
+     block's drafts block[1:] against the posterior rows 0..T-2, bonus =
+     posterior[matched] (runtime.py:145-147), then keep = matched + 1
+     (accepted_inputs, :146; dflash_commit_accept)
+  3. recurrent-state rollback by tape gather  (dflash_tape_select, keep)
+  4. conv-window rollback                     (dflash_conv_rollback, keep)
 
-The accepted count produced by step 2 feeds steps 3-4 on the device, so a
-step needs no host synchronisation.  Layers are stacked as batch entries of
+The keep count produced by step 2 feeds steps 3-4 on the device, so a step
+needs no host synchronisation.  Layers are stacked as batch entries of
 one scan launch (batch index = layer * B + b); layer l's tape is the view
 tape[:, l*B:(l+1)*B] whose token stride is L*B*S.
 """
@@ -59,7 +62,8 @@ class StepShape:
 class VerifyStepRunner:
     """Holds the step's device buffers; ``run()`` enqueues one verify step on
     torch's current stream.  Inputs are written into the ``q, k, v, g, beta,
-    state, logits, draft, conv_in, qkv`` buffers by the caller."""
+    state, logits, block, conv_in, qkv`` buffers by the caller (``block``:
+    the verify block, the last accepted token then T-1 drafts)."""
 
     def __init__(self, shape: StepShape, device: torch.device):
         s = shape
@@ -68,7 +72,7 @@ class VerifyStepRunner:
         Bt = s.L * s.B
         bf, f32, i32 = torch.bfloat16, torch.float32, torch.int32
         # Inputs are written by the caller and outputs by the kernels, so the
-        # buffers start uninitialised; only `matched` must start at zero (the
+        # buffers start uninitialised; only `keep` must start at zero (the
         # first fused step then starts every sequence from `state`).
         z = lambda *shp, dt: torch.empty(shp, dtype=dt, device=device)
         self.q = z(Bt, s.T, s.Hk, s.Dk, dt=bf)
@@ -82,9 +86,10 @@ class VerifyStepRunner:
         self.tape = z(s.T, Bt, s.Hv, s.Dv, s.Dk, dt=f32)
         self.new_state = z(Bt, s.Hv, s.Dv, s.Dk, dt=f32)
         self.logits = z(s.B, s.T, s.V, dt=f32)
-        self.draft = z(s.B, s.T, dt=i32)
+        self.block = z(s.B, s.T, dt=i32)  # the verify block: last token, then T-1 drafts
         self.posterior = z(s.B, s.T, dt=i32)
         self.matched = torch.zeros(s.B, dtype=i32, device=device)
+        self.keep = torch.zeros(s.B, dtype=i32, device=device)  # accepted_inputs = matched + 1
         self.bonus = z(s.B, dt=i32)
         lib = _lib.load()
         ws = int(lib.dflash_greedy_accept_workspace_bytes(s.B, s.T, s.V))
@@ -106,35 +111,40 @@ class VerifyStepRunner:
             Bt, s.T, s.Hk, s.Hv, s.Dk, s.Dv, None,
         )
         # Fused form: the scan starts each sequence from the previous step's
-        # tape at its accepted count (self.matched), updating self.state in
-        # place, and rewrites the same tape buffer; the final state is tape[T-1].
+        # tape at its keep count (self.keep), updating self.state in place, and
+        # rewrites the same tape buffer; the final state is tape[T-1].
         self._scan_rb_args = (
             self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.g.data_ptr(),
             self.beta.data_ptr(), self.state.data_ptr(), self.tape.data_ptr(),
-            self.matched.data_ptr(), s.T, s.B, self.out.data_ptr(), None,
+            self.keep.data_ptr(), s.T, s.B, self.out.data_ptr(), None,
             self.tape.data_ptr(), Bt, s.T, s.Hk, s.Hv, s.Dk, s.Dv, None,
         )
+        # drafts = block[1:] (row stride T, T-1 of them) against all T
+        # posterior rows: the bonus may come from row T-1
         self._accept_args = (
             self.logits.data_ptr(), _lib.DFLASH_DTYPE_F32, s.T * s.V, s.V,
-            self.draft.data_ptr(), s.T, s.T, self.posterior.data_ptr(),
+            self.block.data_ptr() + 4, s.T, s.T - 1, self.posterior.data_ptr(),
             self.matched.data_ptr(), self.bonus.data_ptr(), s.B, s.T, s.V,
             self.workspace.data_ptr(), self.workspace.numel(),
         )
+        self._commit_args = (self.matched.data_ptr(), self.keep.data_ptr(), None, s.B, s.T)
         esz = 4
         tapes = (ctypes.c_void_p * s.L)(*[self.tape.data_ptr() + l * s.B * S * esz for l in range(s.L)])
         sins = (ctypes.c_void_p * s.L)(*[self.state.data_ptr() + l * s.B * S * esz for l in range(s.L)])
         souts = (ctypes.c_void_p * s.L)(*[self.new_state.data_ptr() + l * s.B * S * esz
                                           for l in range(s.L)])
-        self._tape_args = (tapes, sins, souts, self.matched.data_ptr(), s.L, s.B, s.T, S, Bt * S)
+        self._tape_args = (tapes, sins, souts, self.keep.data_ptr(), s.L, s.B, s.T, S, Bt * S)
         if s.conv_dim:
             cins = _lib.ptr_array(self.conv_in)
             qkvs = _lib.ptr_array(self.qkv)
             couts = _lib.ptr_array(self.conv_out)
-            self._conv_args = (cins, qkvs, couts, self.matched.data_ptr(), s.L, s.B, s.T, s.K1,
+            self._conv_args = (cins, qkvs, couts, self.keep.data_ptr(), s.L, s.B, s.T, s.K1,
                                s.conv_dim, s.T * s.conv_dim, s.conv_dim, 2)
-            # accept + conv rollback in two launches (finalize inside the copy)
+            # accept + conv rollback in two launches (finalize inside the copy),
+            # which also writes keep = matched + 1 for the next scan
             self._accept_conv_args = self._accept_args + (
-                cins, qkvs, couts, 0, s.L, s.T, s.K1, s.conv_dim, s.T * s.conv_dim, s.conv_dim, 2)
+                cins, qkvs, couts, 1, self.keep.data_ptr(), s.L, s.T, s.K1, s.conv_dim,
+                s.T * s.conv_dim, s.conv_dim, 2)
         lib = _lib.load()
         self._accept_conv = lib.dflash_greedy_accept_conv_rollback
         self._scan = lib.dflash_gdn_verify_scan
@@ -142,6 +152,7 @@ class VerifyStepRunner:
         self._accept = lib.dflash_greedy_accept
         self._tsel = lib.dflash_tape_select
         self._conv = lib.dflash_conv_rollback
+        self._commit = lib.dflash_commit_accept
 
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
@@ -150,7 +161,10 @@ class VerifyStepRunner:
         _lib.check("dflash_gdn_verify_scan", self._scan(*self._scan_args, stream or self._stream()))
 
     def accept(self, stream: int | None = None) -> None:
-        _lib.check("dflash_greedy_accept", self._accept(*self._accept_args, stream or self._stream()))
+        """Greedy accept, then keep = matched + 1 (two launches)."""
+        st = stream or self._stream()
+        _lib.check("dflash_greedy_accept", self._accept(*self._accept_args, st))
+        _lib.check("dflash_commit_accept", self._commit(*self._commit_args, st))
 
     def rollback(self, stream: int | None = None) -> None:
         st = stream or self._stream()
@@ -167,7 +181,8 @@ class VerifyStepRunner:
             _lib.check("dflash_conv_rollback", self._conv(*self._conv_args, stream or self._stream()))
 
     def accept_conv_rollback(self, stream: int | None = None) -> None:
-        """accept() then conv_rollback(), as two launches instead of three."""
+        """accept() then conv_rollback(), as two launches instead of four (the
+        window copy also writes keep)."""
         st = stream or self._stream()
         if not self.shape.conv_dim:
             self.accept(st)
@@ -185,9 +200,10 @@ class VerifyStepRunner:
     def run_fused(self) -> None:
         """Steady-state serving form: scan with the previous step's state
         rollback fused into its load -> accept -> conv-window rollback.  After
-        the call, the state after accepting matched[b] tokens of this block is
-        tape[matched[b]-1, b] (or state[b] when matched[b] == 0), which the next
-        run_fused() picks up on the device.  Start with matched zeroed."""
+        the call, the state after keeping keep[b] = matched[b] + 1 tokens of
+        this block is tape[keep[b]-1, b], which the next run_fused() picks up
+        on the device.  Start with keep zeroed (the first scan then starts
+        from state)."""
         st = self._stream()
         self.scan_rolled(st)
         self.accept_conv_rollback(st)
@@ -196,6 +212,6 @@ class VerifyStepRunner:
         """Materialise the state the next fused step starts from (test helper;
         reads matched on the host)."""
         s = self.shape
-        a = self.matched.cpu().repeat(s.L).tolist()
+        a = self.keep.cpu().repeat(s.L).tolist()
         outs = [self.tape[ai - 1, i] if ai >= 1 else self.state[i] for i, ai in enumerate(a)]
         return torch.stack(outs)

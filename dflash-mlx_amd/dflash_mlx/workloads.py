@@ -95,3 +95,16 @@ def make_accept_inputs(cfg: ScanConfig, gen: torch.Generator | None = None,
     pos = torch.arange(cfg.T, dtype=torch.int32)[None, :]
     draft = torch.where(pos < accept[:, None], am, (am + 1) % cfg.V).to(torch.int32)
     return {"logits": logits, "draft": draft, "accept": accept}
+
+
+def make_verify_block(acc: dict[str, torch.Tensor], first_token: int = 0) -> torch.Tensor:
+    """The verify block [B, T] of the reference's wiring (runtime.py:145-147):
+    block[0] is the last accepted token, block[1:] the drafts, compared with
+    posterior rows 0..T-2.  Here block[1+i] = draft[i], so an accept length
+    a drawn by make_accept_inputs gives matched = min(a, T-1) and
+    accepted_inputs = matched + 1."""
+    draft = acc["draft"]
+    block = torch.empty_like(draft)
+    block[:, 0] = first_token
+    block[:, 1:] = draft[:, :-1]
+    return block

@@ -404,8 +404,10 @@ int dflash_conv_rollback(const void* const* conv_in, const void* const* qkv,
  * has no single call for the pair.  accepted_offset is 1 to roll back to
  * accepted_inputs = matched + 1 (runtime.py:146), 0 to keep matched tokens.
  * Arguments and outputs as the two calls (posterior and bonus may be NULL);
- * the outputs are bit-identical to theirs.  With L, K1 or C zero only the
- * accept runs.
+ * the outputs are bit-identical to theirs.  accepted_out ([B] int32, or
+ * NULL) receives clamp(matched + accepted_offset, 0, T), the keep count that
+ * dflash_gdn_verify_scan_rollback of the next step reads as prev_accepted.
+ * With L, K1 or C zero only the accept runs (accepted_out must be NULL).
  */
 int dflash_greedy_accept_conv_rollback(
     const void* logits, int logits_dtype, int64_t logits_batch_stride,
@@ -413,7 +415,7 @@ int dflash_greedy_accept_conv_rollback(
     int n_draft, int32_t* posterior, int32_t* matched, int32_t* bonus, int B,
     int N, int V, void* workspace, size_t workspace_bytes,
     const void* const* conv_in, const void* const* qkv, void* const* conv_out,
-    int accepted_offset, int L, int T, int K1, int64_t C,
+    int accepted_offset, int32_t* accepted_out, int L, int T, int K1, int64_t C,
     int64_t qkv_batch_stride, int64_t qkv_row_stride, int elem_bytes,
     void* stream);
 

@@ -13,7 +13,8 @@ import torch
 from dflash_mlx import greedy_accept
 from dflash_mlx.gdn_layer import GatedDeltaConfig, GatedDeltaWeights, gdn_layer_verify
 from dflash_mlx.step import StepShape, VerifyStepRunner
-from dflash_mlx.workloads import CONFIGS, ScanConfig, make_accept_inputs, make_scan_inputs
+from dflash_mlx.workloads import (CONFIGS, ScanConfig, make_accept_inputs, make_scan_inputs,
+                                  make_verify_block)
 
 pytestmark = pytest.mark.gpu
 
@@ -80,7 +81,7 @@ def test_fused_step_runner_graph_replays(device):
         for n in ("q", "k", "v", "g", "beta", "state"):
             getattr(r, n).copy_(x[n])
         r.logits.copy_(acc["logits"])
-        r.draft.copy_(acc["draft"])
+        r.block.copy_(make_verify_block(acc))
         for t in r.conv_in + r.qkv:
             t.zero_()
         runners.append(r)
@@ -94,7 +95,7 @@ def test_fused_step_runner_graph_replays(device):
         graphed.run_fused()
     # Capture does not execute: reset the graphed runner's carried state.
     graphed.state.copy_(x["state"])
-    graphed.matched.zero_()
+    graphed.keep.zero_()
     torch.cuda.synchronize()
     for step in range(4):
         eager.run_fused()
@@ -103,6 +104,7 @@ def test_fused_step_runner_graph_replays(device):
         torch.cuda.synchronize()
         print(f"[graph step {step}] matched {graphed.matched.cpu().tolist()}", flush=True)
         assert torch.equal(graphed.matched, eager.matched)
+        assert torch.equal(graphed.keep, eager.keep)
         assert torch.equal(graphed.tape, eager.tape)
         assert torch.equal(graphed.state, eager.state)
         assert torch.equal(graphed.out, eager.out)

@@ -240,7 +240,8 @@ def test_step_runner_fused_matches_explicit(device):
     """VerifyStepRunner: run_fused (rollback folded into the next scan) and run
     (explicit gather) leave the same rolled-back state and the same tape."""
     from dflash_mlx.step import StepShape, VerifyStepRunner
-    from dflash_mlx.workloads import CONFIGS, ScanConfig, make_accept_inputs, make_scan_inputs
+    from dflash_mlx.workloads import (CONFIGS, ScanConfig, make_accept_inputs, make_scan_inputs,
+                                      make_verify_block)
 
     cfg = ScanConfig(**{**CONFIGS[2].__dict__, "B": 4, "V": 5000})
     x = make_scan_inputs(cfg)
@@ -252,10 +253,13 @@ def test_step_runner_fused_matches_explicit(device):
         for n in ("q", "k", "v", "g", "beta", "state"):
             getattr(r, n).copy_(x[n])
         r.logits.copy_(acc["logits"])
-        r.draft.copy_(acc["draft"])
+        r.block.copy_(make_verify_block(acc))
         (r.run_fused if fused else r.run)()
         torch.cuda.synchronize()
-        assert r.matched.cpu().tolist() == acc["accept"].tolist()
+        # drafts block[1:] against posterior rows 0..14 (the reference's wiring)
+        matched = [min(a, 15) for a in acc["accept"].tolist()]
+        assert r.matched.cpu().tolist() == matched
+        assert r.keep.cpu().tolist() == [m + 1 for m in matched]
         runs.append(r)
     explicit, fused = runs
     assert torch.equal(explicit.tape, fused.tape)
@@ -296,15 +300,18 @@ def test_accept_conv_rollback_matches_two_calls(device, B, N, V, L, K1, C, offse
     post_b = torch.full((B, N), -7, dtype=torch.int32, device=device)
     m_b = torch.full((B,), -7, dtype=torch.int32, device=device)
     b_b = torch.full((B,), -7, dtype=torch.int32, device=device)
+    keep = torch.full((B,), -7, dtype=torch.int32, device=device)
     cin = [c.to(device) for c in conv]
     qd = [q.to(device) for q in qkv]
     cout = [torch.empty_like(c) for c in cin]
     _lib.call("dflash_greedy_accept_conv_rollback", ld.data_ptr(), _lib.dtype_tag(dtype), N * V, V,
               dd.data_ptr(), N, N, post_b.data_ptr(), m_b.data_ptr(), b_b.data_ptr(), B, N, V,
               ws.data_ptr(), ws.numel(), _lib.ptr_array(cin), _lib.ptr_array(qd),
-              _lib.ptr_array(cout), offset, L, N, K1, C, N * C, C, 2, _lib.stream_handle(device))
+              _lib.ptr_array(cout), offset, keep.data_ptr(), L, N, K1, C, N * C, C, 2,
+              _lib.stream_handle(device))
     torch.cuda.synchronize()
     assert m_b.cpu().tolist() == accept.tolist()
+    assert keep.cpu().tolist() == [min(a + offset, N) for a in accept.tolist()]
     assert torch.equal(post_a, post_b) and torch.equal(m_a, m_b) and torch.equal(b_a, b_b)
     for l in range(L):
         assert torch.equal(conv_a[l], cout[l]), f"layer {l}"
