@@ -67,7 +67,8 @@ def parse_args():
                          "and c2 under 'configs')")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the measurements of the next-row kernels (fused LM head)")
-    ap.add_argument("--only", choices=("lm_head", "layer", "prefill", "hybrid"), default=None,
+    ap.add_argument("--only", choices=("lm_head", "layer", "prefill", "hybrid", "gemm"),
+                    default=None,
                     help="measure one next-row kernel alone and print its JSON (for profiling)")
     ap.add_argument("--probe", action="store_true",
                     help="for rocprofv3 --pmc runs: 3 explicit scans, 3 fused scans and 3 "
@@ -112,6 +113,22 @@ def traffic_from_profiles(workload: str):
         return None
     m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", path.read_text())
     return int(m.group(1)) if m else None
+
+
+def mfma_from_profiles(name: str):
+    """Counter-measured MFMA busy fraction and executed TFLOP/s per kernel from
+    a committed rocprofv3 --pmc summary (profiles/<name>_mfma_pmc.md)."""
+    path = ROOT / "profiles" / f"{name}_mfma_pmc.md"
+    if not path.exists():
+        return None
+    text = path.read_text()
+    out = {}
+    for key in ("mfma_busy_frac", "mfma_executed_tflops"):
+        m = re.search(rf"^{key}:(.*)$", text, re.M)
+        if m:
+            out[key] = {k: float(v) for k, v in (kv.split("=") for kv in m.group(1).split())}
+    out["source"] = f"profiles/{path.name}"
+    return out
 
 
 def time_steps(torch, K: int, phases):
@@ -252,10 +269,64 @@ def measure_prefill(torch, dev, n=10):
         "flops_alg": flops,
         "tflops": round(tflops, 2),
         "mfma_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "mfma_counters": mfma_from_profiles("chunked_prefill_c3-prefill-8k"),
         "hbm_bytes_alg": hbm,
         "hbm_frac": round(hbm / (chunked_us / 1e6) / 1e9 / PEAK_HBM_GBPS, 4),
         "note": "per call incl. Python dispatch; two kernels (chunk prep, chunk state)",
     }
+
+
+def measure_gemm(torch, dev, reps=8, copies=4):
+    """The c4 step's six verify-sized projection GEMMs alone (M = 16 block
+    rows, fragment-tiled weights, the runner's launch plans), each timed over
+    `copies` distinct weights in rotation so that, as in the step, no launch
+    finds its weight in the 256 MB Infinity Cache."""
+    from dflash_mlx import _lib
+    from dflash_mlx.hybrid_model import HybridConfig, HybridVerifyRunner
+    from dflash_mlx.runtime import tile_weight
+
+    cfg = HybridConfig()
+    lc, H, I, M = cfg.linear, cfg.hidden_size, cfg.intermediate_size, 16
+    dims = {"w_in": (cfg.in_proj_rows, H), "w_out": (H, lc.value_dim),
+            "w_qkv": (cfg.attn_proj_rows, H), "w_o": (H, cfg.num_attention_heads * cfg.head_dim),
+            "w_gu": (2 * I, H), "w_down": (H, I)}
+    lib = _lib.load()
+    stream = _lib.stream_handle(dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    x = (torch.randn(M, max(k for _, k in dims.values()), generator=gen, device=dev)
+         ).to(torch.bfloat16)
+    res = {}
+    for name, (N, K) in dims.items():
+        ns, rpw, kw = HybridVerifyRunner.TILED_PLAN[name]
+        ws = [tile_weight((0.02 * torch.randn(N, K, generator=gen, device=dev)).to(torch.bfloat16))
+              for _ in range(copies)]
+        splits = int(lib.dflash_gemm_splits(K, ns)) if ns > 1 else 0
+        out = torch.empty(max(splits, 1) * M * N, dtype=torch.float32, device=dev)
+
+        def call(w):
+            if name == "w_gu":
+                _lib.call("dflash_gemm_bf16_swiglu_tiled", x.data_ptr(), x.stride(0), w.data_ptr(),
+                          out.data_ptr(), N // 2, M, N, K, kw, stream)
+            else:
+                _lib.call("dflash_gemm_bf16_tiled", x.data_ptr(), x.stride(0), w.data_ptr(),
+                          out.data_ptr(), 0 if splits else N, M, N, K, ns, rpw, kw, stream)
+
+        for w in ws:
+            call(w)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            for w in ws:
+                call(w)
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * copies)
+        res[name] = {"N": N, "K": K, "plan": [ns, rpw, kw], "splits": splits, "us": round(us, 2),
+                     "weight_gbps": round(2 * N * K / us / 1e3, 1)}
+        del ws, out
+    return {"M": M, "projections": res,
+            "note": "per launch incl. dispatch; weights rotated over %d copies" % copies}
 
 
 def measure_hybrid(torch, dev, steps=40):
@@ -644,7 +715,7 @@ def main() -> int:
     if args.only is not None:
         dev = torch.device("cuda", 0)
         fn = {"lm_head": measure_lm_head, "layer": measure_layer, "prefill": measure_prefill,
-              "hybrid": measure_hybrid}
+              "hybrid": measure_hybrid, "gemm": measure_gemm}
         print(json.dumps({args.only: fn[args.only](torch, dev)}), flush=True)
         return 0
 
