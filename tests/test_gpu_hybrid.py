@@ -39,7 +39,9 @@ def _np(x):
 def _np_weights(w: HybridWeights):
     layers = []
     for lw in w.layers:
-        d = {k: _np(v) for k, v in lw.items() if k != "gdn"}
+        # the weights as drawn (not the runner's regrouped / fragment-tiled copies)
+        d = {k: _np(v) for k, v in lw.items()
+             if k != "gdn" and not k.startswith("w_gu_pairs") and not k.endswith("_tiled")}
         if "gdn" in lw:
             g = lw["gdn"]
             d.update(conv_w=_np(g.conv_weight), A_log=_np(g.A_log), dt_bias=_np(g.dt_bias),
@@ -280,3 +282,62 @@ def test_c4_full_shape_step_runs_and_is_deterministic(device):
     assert torch.isfinite(xa.float()).all()
     assert torch.equal(xa, xb) and torch.equal(pa, pb) and torch.equal(la, lb)
     assert 1 <= int(ka[0]) <= T and int(la[0]) > L0
+
+
+def test_c4_width_layers_match_oracle(device):
+    """The first four layers of the c4 model at their real widths (hidden
+    2560, MLP 9216, 16 key / 32 value heads of 128 in the gated-delta layers,
+    16 query / 4 KV heads over a 4096-token cache in the attention layer,
+    the full 151936-token LM head) against the fp64 oracle: each layer's
+    residual stream (captured on the GPU), the gated-delta tapes, the final
+    hidden and logits, and the greedy accept on the clear-margin rows."""
+    cfg = HybridConfig(num_hidden_layers=4)
+    B, T, L0, Smax = 1, 16, 4096, 4160
+    print("[hybrid c4-width] drawing weights on the host", flush=True)
+    w = HybridWeights.random(cfg, device, seed=61, on_device=False)
+    st = _initial_state(cfg, B, [L0], seed=62)
+    gen = torch.Generator().manual_seed(63)
+    tokens = torch.randint(0, cfg.vocab_size, (B, T), generator=gen, dtype=torch.int32)
+    run = _runner(cfg, w, st, B, T, Smax, device)
+    run.set_capture(range(cfg.num_hidden_layers))
+    run.tokens.copy_(tokens)
+    print("[hybrid c4-width] GPU forward", flush=True)
+    run.forward_accept()
+    torch.cuda.synchronize()
+    print("[hybrid c4-width] oracle step", flush=True)
+    o_state = dict(lens=np.array(st["lens"]), conv=[_np(c) for c in st["conv"]],
+                   rec=[_np(s) for s in st["rec"]], k=[_np(k) for k in st["k"]],
+                   v=[_np(v) for v in st["v"]])
+    ref = ho.model_step(cfg, _np_weights(w), o_state, tokens.numpy(), cfg.rms_norm_eps)
+    H = cfg.hidden_size
+    cap = _np(run.captured).reshape(B, T, cfg.num_hidden_layers, H)
+    for i in range(cfg.num_hidden_layers):
+        r = ref["layer_hidden"][i]
+        err = np.max(np.abs(cap[:, :, i] - r)) / np.max(np.abs(r))
+        print(f"  layer {i} ({'gated-delta' if cfg.is_linear(i) else 'attention'}) hidden rel "
+              f"{err:.2e}", flush=True)
+        assert err <= 2e-2
+    for gi in range(cfg.n_linear):
+        terr = np.max(np.abs(_np(run.tape[gi]) - ref["tape"][gi])) / np.max(np.abs(ref["tape"][gi]))
+        print(f"  tape {gi} rel {terr:.2e}", flush=True)
+        assert terr <= 1e-2
+    hid = _np(run.xn).reshape(B, T, H)
+    herr = np.max(np.abs(hid - ref["hidden"])) / np.max(np.abs(ref["hidden"]))
+    logits = _np(run.logits())
+    lerr = np.max(np.abs(logits - ref["logits"])) / np.max(np.abs(ref["logits"]))
+    print(f"  final hidden rel {herr:.2e}  logits rel {lerr:.2e}", flush=True)
+    assert herr <= 3e-2 and lerr <= 3e-2
+    post = run.posterior.cpu().numpy()
+    srt = np.sort(ref["logits"], axis=-1)
+    clear = (srt[..., -1] - srt[..., -2]) > 2e-2 * np.max(np.abs(ref["logits"]))
+    assert np.array_equal(post[clear], ref["posterior"][clear])
+    m = int(run.matched.cpu()[0])
+    assert m == gdn_oracle.longest_prefix_match(tokens.numpy()[0, 1:], post[0, :-1])
+    assert int(run.bonus.cpu()[0]) == post[0, m]
+    print(f"  posterior equal to the oracle's on {int(clear.sum())} clear-margin rows of {T}",
+          flush=True)
+    assert clear.sum() >= 4
+    # on the other rows the GPU's token is a near tie of the oracle's top one
+    scale = np.max(np.abs(ref["logits"]))
+    chosen = np.take_along_axis(ref["logits"], post[..., None].astype(np.int64), -1)[..., 0]
+    assert np.all(srt[..., -1] - chosen <= 2e-2 * scale)

@@ -98,3 +98,32 @@ def test_planted_prologue_mistakes_are_caught(oracle, mistake):
     else:
         g2 = np.exp(-np.exp(x["A_log"]) * (x["a"] + x["dt_bias"]))
         assert np.max(np.abs(g2 - g)) > 1e-2
+
+
+def test_decay_with_dt_bias_closed_form(oracle):
+    """compute_g with dt_bias != 0: a = -dt_bias zeroes the softplus
+    argument, so g = exp(-exp(A_log) * ln 2): 1/2 at A_log = 0, 1/8 at
+    A_log = ln 3, whatever dt_bias is."""
+    dt_bias = np.array([1.7, -0.6, 3.0, 0.25])
+    a = -dt_bias
+    np.testing.assert_allclose(oracle.compute_g(0.0, a, dt_bias), 0.5, rtol=1e-14)
+    np.testing.assert_allclose(oracle.compute_g(np.log(3.0), a, dt_bias), 0.125, rtol=1e-14)
+    # A planted sign slip, softplus(a - dt_bias), misses the closed form.
+    slip = np.exp(-np.log1p(np.exp(a - dt_bias)))
+    assert np.max(np.abs(slip - 0.5)) > 1e-2
+
+
+def test_gated_norm_weight_hand_row(oracle):
+    """RMSNormGated with a non-unit weight against a row worked by hand:
+    x = [3, 4] has rms sqrt(12.5); silu(z) = z / (1 + e^-z)."""
+    x = np.array([[3.0, 4.0]])
+    z = np.array([[1.0, -2.0]])
+    w = np.array([2.0, 0.5])
+    r = np.sqrt(12.5)
+    silu = z / (1 + np.exp(-z))
+    want = np.array([[2.0 * 3.0 / r, 0.5 * 4.0 / r]]) * silu
+    np.testing.assert_allclose(oracle.gated_rmsnorm(x, z, w, eps=0.0), want, rtol=1e-14)
+    # A (1 + w) weight shift (a load-time transform of some checkpoints, never
+    # applied at run time) misses the hand row.
+    shifted = oracle.gated_rmsnorm(x, z, 1.0 + w, eps=0.0)
+    assert np.max(np.abs(shifted - want)) > 1e-2

@@ -136,3 +136,150 @@ def test_swiglu_closed_forms():
     assert abs(out[1] - 60.0) < 1e-9
     assert abs(out[2]) < 1e-10
     assert abs(out[3] - 4.0 / (1 + np.exp(-1.0))) < 1e-12
+
+
+def test_rmsnorm_weight_hand_row():
+    """nn.RMSNorm with a non-unit weight against a row worked by hand
+    (x = [3, 4]: rms sqrt(12.5)), and the residual add before it.  The
+    reference shifts norm weights by 1 only when loading some checkpoints
+    (custom_qwen35_model.py:1156-1180); at run time y = w * x / rms, so a
+    planted (1 + w) misses the row."""
+    x = np.array([[3.0, 4.0]])
+    w = np.array([2.0, 0.5])
+    r = np.sqrt(12.5)
+    want = np.array([[2.0 * 3.0 / r, 0.5 * 4.0 / r]])
+    np.testing.assert_allclose(ho.rms_norm_w(x, w, 0.0), want, rtol=1e-14)
+    h, y = ho.add_rmsnorm(np.array([[1.0, 5.0]]), np.array([[2.0, -1.0]]), w, 0.0)
+    np.testing.assert_array_equal(h, [[3.0, 4.0]])
+    np.testing.assert_allclose(y, want, rtol=1e-14)
+    assert np.max(np.abs(ho.rms_norm_w(x, 1.0 + w, 0.0) - want)) > 1e-2
+
+
+# ---------------------------------------------------------------- model wiring
+from dflash_mlx.gdn_layer import GatedDeltaConfig  # noqa: E402
+from dflash_mlx.hybrid_model import HybridConfig  # noqa: E402
+
+TINY = HybridConfig(hidden_size=128, num_hidden_layers=4, intermediate_size=256, vocab_size=96,
+                    num_attention_heads=2, num_key_value_heads=1, head_dim=128,
+                    linear=GatedDeltaConfig(linear_num_key_heads=1, linear_num_value_heads=2,
+                                            linear_key_head_dim=64, linear_value_head_dim=64))
+
+
+def _tiny_weights(rng, scale=0.05):
+    cfg, lc = TINY, TINY.linear
+    H, I, D = cfg.hidden_size, cfg.intermediate_size, cfg.head_dim
+    bf = ho.bf16
+    layers = []
+    for i in range(cfg.num_hidden_layers):
+        lw = {"ln_in": bf(1 + 0.2 * rng.standard_normal(H)),
+              "ln_post": bf(1 + 0.2 * rng.standard_normal(H)),
+              "w_gu": bf(scale * rng.standard_normal((2 * I, H))),
+              "w_down": bf(scale * rng.standard_normal((H, I)))}
+        if cfg.is_linear(i):
+            lw.update(w_in=bf(scale * rng.standard_normal((cfg.in_proj_rows, H))),
+                      w_out=bf(scale * rng.standard_normal((H, lc.value_dim))),
+                      conv_w=bf(0.5 * rng.standard_normal((lc.conv_dim, lc.linear_conv_kernel_dim))),
+                      A_log=np.log(rng.uniform(0.5, 8, lc.linear_num_value_heads)),
+                      dt_bias=bf(rng.standard_normal(lc.linear_num_value_heads)),
+                      norm_w=bf(1 + 0.2 * rng.standard_normal(lc.linear_value_head_dim)))
+        else:
+            lw.update(w_qkv=bf(scale * rng.standard_normal((cfg.attn_proj_rows, H))),
+                      w_o=bf(scale * rng.standard_normal((H, cfg.num_attention_heads * D))),
+                      q_norm=bf(1 + 0.2 * rng.standard_normal(D)),
+                      k_norm=bf(1 + 0.2 * rng.standard_normal(D)))
+        layers.append(lw)
+    return dict(embed=bf(rng.standard_normal((cfg.vocab_size, H))),
+                final_norm=bf(1 + 0.2 * rng.standard_normal(H)),
+                lm_head=bf(scale * rng.standard_normal((cfg.vocab_size, H))), layers=layers)
+
+
+def _empty_state(B=1):
+    lc = TINY.linear
+    return dict(lens=np.zeros(B, np.int64),
+                conv=[np.zeros((B, lc.linear_conv_kernel_dim - 1, lc.conv_dim))] * TINY.n_linear,
+                rec=[np.zeros((B, lc.linear_num_value_heads, lc.linear_value_head_dim,
+                               lc.linear_key_head_dim))] * TINY.n_linear,
+                k=[np.zeros((B, TINY.num_key_value_heads, 0, TINY.head_dim))] * TINY.n_attention,
+                v=[np.zeros((B, TINY.num_key_value_heads, 0, TINY.head_dim))] * TINY.n_attention)
+
+
+def _carry(state, res, T, conv_shift=0, lens_shift=0):
+    """The caches after a model_step over T tokens (the runtime's
+    all-accepted hand-off): conv windows advanced, recurrent state =
+    tape[T-1], keys / values appended, lengths += T.  The shifts plant
+    hand-off mistakes."""
+    K1 = TINY.linear.linear_conv_kernel_dim - 1
+    out = dict(lens=state["lens"] + T + lens_shift, conv=[], rec=[], k=[], v=[])
+    for gi in range(TINY.n_linear):
+        x = np.concatenate([state["conv"][gi], res["qkv"][gi]], axis=1)
+        end = x.shape[1] - conv_shift
+        out["conv"].append(x[:, end - K1:end])
+        out["rec"].append(res["tape"][gi][T - 1])
+    for ai in range(TINY.n_attention):
+        out["k"].append(np.concatenate([state["k"][ai], res["k_new"][ai].transpose(0, 2, 1, 3)], 2))
+        out["v"].append(np.concatenate([state["v"][ai], res["v_new"][ai].transpose(0, 2, 1, 3)], 2))
+    return out
+
+
+def test_model_step_zero_projections_pass_the_residual_through():
+    """With every projection zero each layer adds nothing: the residual
+    stream after every layer is the embedding row, the normed hidden is
+    final_norm * rms_norm(embedding) and the logits are its LM-head
+    product.  A dropped residual, a norm on the wrong stream or a missing
+    final norm all break this."""
+    rng = np.random.default_rng(11)
+    w = _tiny_weights(rng)
+    for lw in w["layers"]:
+        for k in ("w_gu", "w_down", "w_in", "w_out", "w_qkv", "w_o"):
+            if k in lw:
+                lw[k] = np.zeros_like(lw[k])
+    tokens = rng.integers(0, TINY.vocab_size, (2, 5))
+    st = _empty_state(2)
+    st["conv"] = [rng.standard_normal(c.shape) for c in st["conv"]]  # nonzero windows
+    res = ho.model_step(TINY, w, st, tokens, 1e-6)
+    emb = w["embed"][tokens]
+    for lh in res["layer_hidden"]:
+        np.testing.assert_array_equal(lh, emb)
+    want = ho.rms_norm_w(emb, w["final_norm"], 1e-6)
+    np.testing.assert_allclose(res["hidden"], ho.bf16(want), rtol=1e-14)  # rounded as the GPU
+    np.testing.assert_allclose(res["logits"], ho.bf16(want) @ w["lm_head"].T, rtol=1e-12)
+
+
+@pytest.mark.parametrize("split", [1, 3, 5])
+def test_model_step_one_block_equals_two_blocks(split, oracle):
+    """A block of 8 tokens in one model_step equals the same tokens in two
+    steps with the caches carried between them (conv windows, recurrent
+    state from the tape, keys / values and lengths): the layer wiring, the
+    causal masks and the position offsets agree across the boundary."""
+    rng = np.random.default_rng(12)
+    w = _tiny_weights(rng)
+    tokens = rng.integers(0, TINY.vocab_size, (1, 8))
+    one = ho.model_step(TINY, w, _empty_state(), tokens, 1e-6)
+    st0 = _empty_state()
+    a = ho.model_step(TINY, w, st0, tokens[:, :split], 1e-6)
+    b = ho.model_step(TINY, w, _carry(st0, a, split), tokens[:, split:], 1e-6)
+    scale = np.max(np.abs(one["logits"]))
+    for i in range(TINY.num_hidden_layers):
+        got = np.concatenate([a["layer_hidden"][i], b["layer_hidden"][i]], axis=1)
+        err = np.max(np.abs(got - one["layer_hidden"][i]))
+        assert err <= 1e-6 * np.max(np.abs(one["layer_hidden"][i])), (i, err)
+    got = np.concatenate([a["logits"], b["logits"]], axis=1)
+    assert np.max(np.abs(got - one["logits"])) <= 1e-6 * scale  # (equal in fp64 here)
+
+
+@pytest.mark.parametrize("mistake", ["conv_window", "kv_length"])
+def test_model_step_split_catches_a_wrong_hand_off(mistake, oracle):
+    rng = np.random.default_rng(12)
+    w = _tiny_weights(rng)
+    tokens = rng.integers(0, TINY.vocab_size, (1, 8))
+    one = ho.model_step(TINY, w, _empty_state(), tokens, 1e-6)
+    st0 = _empty_state()
+    a = ho.model_step(TINY, w, st0, tokens[:, :3], 1e-6)
+    bad = _carry(st0, a, 3, conv_shift=1 if mistake == "conv_window" else 0,
+                 lens_shift=-1 if mistake == "kv_length" else 0)
+    if mistake == "kv_length":  # the last key is overwritten at the wrong position
+        bad["k"] = [k[:, :, :-1] for k in bad["k"]]
+        bad["v"] = [v[:, :, :-1] for v in bad["v"]]
+    b = ho.model_step(TINY, w, bad, tokens[:, 3:], 1e-6)
+    got = np.concatenate([a["logits"], b["logits"]], axis=1)
+    assert np.max(np.abs(got - one["logits"])) > 1e-2 * np.max(np.abs(one["logits"]))
