@@ -41,7 +41,12 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int CH = 64;   // chunk length
 constexpr int D = 128;   // Dk = Dv supported by these kernels
-constexpr int RB = 16;   // state rows per phase-2 wave
+constexpr int RB = 16;   // state rows per phase-2 workgroup
+// Phase-2 state waves per workgroup; each owns 128 / kStateWaves state
+// columns of the workgroup's 16 rows (1, 2 or 4), and output waves, each of
+// which computes 64 / kOutputWaves of a chunk's output rows (1 or 2).
+constexpr int kStateWaves = 4;
+constexpr int kOutputWaves = 2;
 constexpr int KTP = 72;  // bf16 row pitch of the K^T / V^T tiles in LDS
 constexpr int TPF = 68;  // fp32 row pitch of A / T in LDS
 
@@ -445,34 +450,15 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
 // barrier per chunk; the output wave computes O = diag(EG) Q S^T + P U one
 // chunk behind, off the chain.
 
-struct WOps {                // state wave, per chunk: W rows, [token tile it][k-step s]
-  u32x4 hi[4][4], lo[4][4];
-};
 struct UOps {                // state wave, per chunk (loaded at the chunk's start)
   f32x4 ut[4];               // U~[16it + 4g + e][16rb + lane%16]
   f32x4 ed[4];               // exp(G_63 - G) of the same token rows
   float egC;                 // exp(G_63)
 };
-struct QOps {                // output wave, per chunk
-  u32x4 q[4][4];             // Q rows, [it][s]
-  u32x4 ph[4][2], pl[4][2];  // P rows, [it][s] (tiles 0, 1: k-step 0 only)
-  f32x4 eg[4];               // exp(G) of the lane's token rows
-};
 struct Exchange {            // one chunk's S and U operand halves, [k-step][lane]
   u32x4 shi[4][64], slo[4][64];
   u32x4 uh[2][64], ul[2][64];
 };
-
-__device__ __forceinline__ void load_w(const uint8_t* wsc, uint32_t lf, WOps& o) {
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      o.hi[it][s] = ld16(wsc + kWHi + lf + (it * 4 + s) * 1024);
-      o.lo[it][s] = ld16(wsc + kWLo + lf + (it * 4 + s) * 1024);
-    }
-  }
-}
 
 __device__ __forceinline__ void load_u(const uint8_t* wsc, uint32_t lu, uint32_t ld, UOps& o) {
 #pragma unroll
@@ -481,31 +467,6 @@ __device__ __forceinline__ void load_u(const uint8_t* wsc, uint32_t lu, uint32_t
     o.ed[it] = ldf4(wsc + kED + ld + it * 64);
   }
   o.egC = *reinterpret_cast<const float*>(wsc + kEG + (CH - 1) * 4);
-}
-
-__device__ __forceinline__ void load_kt(const uint8_t* wsc, uint32_t lf, u32x4 (&kt)[8][2]) {
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt) {
-#pragma unroll
-    for (int s = 0; s < 2; ++s) kt[dt][s] = ld16(wsc + kKT + lf + (dt * 2 + s) * 1024);
-  }
-}
-
-// wsq: the chunk slot holding Q (the key head's first value head), wsc: this
-// value head's slot (P, EG).
-__device__ __forceinline__ void load_q(const uint8_t* wsq, const uint8_t* wsc, uint32_t lf,
-                                       uint32_t ld, QOps& o) {
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) o.q[it][s] = ld16(wsq + kQ + lf + (it * 4 + s) * 1024);
-#pragma unroll
-    for (int s = 0; s < (it < 2 ? 1 : 2); ++s) {
-      o.ph[it][s] = ld16(wsc + kPHi + lf + (it * 2 + s) * 1024);
-      o.pl[it][s] = ld16(wsc + kPLo + lf + (it * 2 + s) * 1024);
-    }
-    o.eg[it] = ldf4(wsc + kEG + ld + it * 64);
-  }
 }
 
 // Tiles x0 (slots 0..3) and x1 (slots 4..7) as one B operand, hi and lo halves.
@@ -538,8 +499,25 @@ __device__ __forceinline__ const uint8_t* qk_base(const ChunkParams& p, int bh) 
   return p.ws + (int64_t)(bh - hv % p.rep) * p.NC * kWsChunk;
 }
 
-__device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb, int lane,
-                                           Exchange* xb) {
+// State wave h of NSW owns state columns [128h/NSW, 128(h+1)/NSW): result
+// tiles dt in [8h/NSW, 8(h+1)/NSW) and k-steps s in [4h/NSW, 4(h+1)/NSW) of
+// the products with S.  Per chunk it forms its partial W[:, its k] S[:, its k]^T,
+// the waves exchange partials through LDS (one barrier), every wave sums
+// them in wave order (so all hold the same U, bit for bit), and each
+// updates only its own columns of S; the output wave reads S and U after a
+// second barrier.  With NSW = 1 there is no partial exchange (the first
+// barrier is still passed, so every wave counts two per chunk).
+template <int NSW>
+struct Partials {            // the state waves' W S^T partials, [wave][token tile][lane]
+  f32x4 p[NSW][4][64];
+};
+
+template <int NSW>
+__device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb, int h, int lane,
+                                           Exchange* xb, Partials<NSW>* xp) {
+  constexpr int NT = 8 / NSW;  // own result tiles (state columns / 16)
+  constexpr int NS = 4 / NSW;  // own k-steps (state columns / 32)
+  const int dt0 = NT * h, s0 = NS * h;
   const int r16 = lane & 15;
   const int g4 = lane >> 4;
   const uint32_t lf = lane * 16;              // operand fragments
@@ -549,92 +527,129 @@ __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb,
   const uint8_t* wk0 = qk_base(p, bh);
   const int last = p.NC - 1;
 
-  f32x4 sT[8];
+  f32x4 sT[NT];
   {
-    const float* s0 = p.state_in + ((int64_t)bh * D + rb * RB + r16) * D + 4 * g4;
+    const float* sp = p.state_in + ((int64_t)bh * D + rb * RB + r16) * D + 4 * g4;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) sT[dt] = ldf4(s0 + 16 * dt);
+    for (int j = 0; j < NT; ++j) sT[j] = ldf4(sp + 16 * (dt0 + j));
   }
-  WOps w;
-  u32x4 kt[8][2];
-  load_w(ws0, lf, w);
-  load_kt(wk0, lf, kt);
+  u32x4 whi[4][NS], wlo[4][NS];  // this chunk's W rows, own k-steps
+  u32x4 kt[NT][2];               // this chunk's K^T, own tiles
+  auto load_w_own = [&](const uint8_t* wsc) {
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        whi[it][j] = ld16(wsc + kWHi + lf + (it * 4 + s0 + j) * 1024);
+        wlo[it][j] = ld16(wsc + kWLo + lf + (it * 4 + s0 + j) * 1024);
+      }
+    }
+  };
+  auto load_kt_own = [&](const uint8_t* wsc) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) kt[j][s] = ld16(wsc + kKT + lf + ((dt0 + j) * 2 + s) * 1024);
+    }
+  };
+  load_w_own(ws0);
+  load_kt_own(wk0);
   for (int c = 0; c < p.NC; ++c) {
     // Chunks past the last re-read the last one: the loads stay unconditional.
     const uint8_t* wsc = ws0 + (int64_t)c * kWsChunk;
     const uint8_t* wsn = ws0 + (int64_t)min(c + 1, last) * kWsChunk;
     Exchange& x = xb[c & 1];
-    // U~ and the decays are needed only after the W product: loaded here,
-    // they are not carried across iterations.
     UOps uo;
     load_u(wsc, lu, ld, uo);
 
-    // S as the B operand (k = state column), hi / lo halves, shared.
-    u32x4 shi[4], slo[4];
+    // Own columns of S as the B operand (k = state column), hi / lo halves.
+    u32x4 shi[NS], slo[NS];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      split_pair(sT[2 * s], sT[2 * s + 1], shi[s], slo[s]);
-      x.shi[s][lane] = shi[s];
-      x.slo[s][lane] = slo[s];
+    for (int j = 0; j < NS; ++j) {
+      split_pair(sT[2 * j], sT[2 * j + 1], shi[j], slo[j]);
+      x.shi[s0 + j][lane] = shi[j];
+      x.slo[s0 + j][lane] = slo[j];
     }
-
-    // U = U~ - W S^T and Ud = diag(ED) U, token tile it.
-    f32x4 u[4], ud[4];
+    // Own partial of W S^T, token tile it.
+    f32x4 part[4];
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        acc = mfma(w.hi[it][s], shi[s], acc);
-        acc = mfma(w.hi[it][s], slo[s], acc);
-        acc = mfma(w.lo[it][s], shi[s], acc);
+      for (int j = 0; j < NS; ++j) {
+        acc = mfma(whi[it][j], shi[j], acc);
+        acc = mfma(whi[it][j], slo[j], acc);
+        acc = mfma(wlo[it][j], shi[j], acc);
+      }
+      part[it] = acc;
+      if (NSW > 1) xp->p[h][it][lane] = acc;
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load_w_own(wsn);  // this chunk's W is consumed
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();  // partials (and S) published
+
+    // U = U~ - sum of the partials (in wave order), Ud = diag(ED) U.
+    f32x4 u[4], ud[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      f32x4 acc = part[it];
+      if (NSW > 1) {
+        acc = h == 0 ? part[it] : xp->p[0][it][lane];
+#pragma unroll
+        for (int w = 1; w < NSW; ++w) acc = acc + (w == h ? part[it] : xp->p[w][it][lane]);
       }
       u[it] = uo.ut[it] - acc;
       ud[it] = uo.ed[it] * u[it];
     }
     const float egC = uo.egC;
-    // This chunk's W is consumed: fetch the next.  The fences keep the W and
-    // K^T groups in program order, so waiting for W never waits for K^T.
-    __builtin_amdgcn_sched_barrier(0);
-    load_w(wsn, lf, w);
-    __builtin_amdgcn_sched_barrier(0);
 
-    // U (shared) and Ud as the B operand (k = token), hi / lo halves.
+    // U (for the output wave, written by wave 0) and Ud as the B operand
+    // (k = token), hi / lo halves.
     u32x4 dh[2], dl[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      u32x4 uh, ul;
-      split_pair(u[2 * s], u[2 * s + 1], uh, ul);
-      x.uh[s][lane] = uh;
-      x.ul[s][lane] = ul;
+      if (h == 0) {
+        u32x4 uh, ul;
+        split_pair(u[2 * s], u[2 * s + 1], uh, ul);
+        x.uh[s][lane] = uh;
+        x.ul[s][lane] = ul;
+      }
       split_pair(ud[2 * s], ud[2 * s + 1], dh[s], dl[s]);
     }
-    lds_barrier();  // chunk c's S and U are visible to the output wave
+    lds_barrier();  // chunk c's S and U are visible to the output wave; partials read
 
-    // S^T = gamma_C S^T + K^T Ud  (K^T exact in bf16: two terms).
+    // Own columns: S^T = gamma_C S^T + K^T Ud  (K^T exact in bf16: two terms).
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      f32x4 a = egC * sT[dt];
+    for (int j = 0; j < NT; ++j) {
+      f32x4 a = egC * sT[j];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        a = mfma(kt[dt][s], dh[s], a);
-        a = mfma(kt[dt][s], dl[s], a);
+        a = mfma(kt[j][s], dh[s], a);
+        a = mfma(kt[j][s], dl[s], a);
       }
-      sT[dt] = a;
+      sT[j] = a;
     }
     __builtin_amdgcn_sched_barrier(0);
-    load_kt(wk0 + (int64_t)min(c + 1, last) * kWsChunk, lf, kt);
+    load_kt_own(wk0 + (int64_t)min(c + 1, last) * kWsChunk);
     __builtin_amdgcn_sched_barrier(0);
   }
   if (p.final_state != nullptr) {
     float* s1 = p.final_state + ((int64_t)bh * D + rb * RB + r16) * D + 4 * g4;
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(s1 + 16 * dt) = sT[dt];
+    for (int j = 0; j < NT; ++j) *reinterpret_cast<f32x4*>(s1 + 16 * (dt0 + j)) = sT[j];
   }
 }
 
-__device__ __forceinline__ void output_wave(const ChunkParams& p, int bh, int rb, int lane,
+// Output wave j of NOW computes O = diag(EG) Q S^T + P U for token tiles
+// it in [4j/NOW, 4(j+1)/NOW) of each chunk: Q S^T between the state waves'
+// two barriers (S is published at the first), P U and the stores after the
+// second, so neither half holds the chain up at a barrier.
+template <int NOW>
+__device__ __forceinline__ void output_wave(const ChunkParams& p, int bh, int rb, int j, int lane,
                                             const Exchange* xb) {
+  constexpr int NIT = 4 / NOW;  // own token tiles
+  const int it0 = NIT * j;
   const int r16 = lane & 15;
   const int g4 = lane >> 4;
   const uint32_t lf = lane * 16;
@@ -646,37 +661,70 @@ __device__ __forceinline__ void output_wave(const ChunkParams& p, int bh, int rb
   const int last = p.NC - 1;
   const int64_t orow = (int64_t)p.Hv * D;  // out row stride (elements)
 
-  // L2 prefetch: the output wave has slack on the chain, so it touches one
-  // dword per 128-byte line of chunk c + 3 of this head (its eighth of the
-  // lines), for the state wave's W and K^T loads two chunks later.  Each
-  // touch is consumed (waited for) one chunk after it is issued, and after
-  // that chunk's own loads, so in-order completion never holds them up.
+  // L2 prefetch (output wave 0): the output wave has slack on the chain, so
+  // it touches one dword per 128-byte line of chunk c + 3 of this head (its
+  // eighth of the lines), for the state waves' W and K^T loads two chunks
+  // later.  Each touch is consumed (waited for) one chunk after it is
+  // issued, and after that chunk's own loads, so in-order completion never
+  // holds them up.
   const uint32_t t0o = min((uint32_t)((rb * 113 + lane) * 128), (uint32_t)(kWsChunk - 4));
   const uint32_t t1o = min((uint32_t)((rb * 113 + min(lane + 64, 112)) * 128), (uint32_t)(kWsChunk - 4));
   // Lines of the Q / K^T range are touched in the key head's slot.
   const uint8_t* t0b = (t0o >= kQ && t0o < kPHi) ? wk0 : ws0;
   const uint8_t* t1b = (t1o >= kQ && t1o < kPHi) ? wk0 : ws0;
-  QOps qo;
-  load_q(wk0, ws0, lf, ld, qo);
+  u32x4 q[NIT][4], ph[NIT][2], pl[NIT][2];
+  f32x4 eg[NIT];
+  auto load_q_own = [&](const uint8_t* wsq, const uint8_t* wsc) {
+#pragma unroll
+    for (int i = 0; i < NIT; ++i) {
+      const int it = it0 + i;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) q[i][s] = ld16(wsq + kQ + lf + (it * 4 + s) * 1024);
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (s == 0 || it >= 2) {  // P tiles 0, 1 hold only k-step 0 (causal)
+          ph[i][s] = ld16(wsc + kPHi + lf + (it * 2 + s) * 1024);
+          pl[i][s] = ld16(wsc + kPLo + lf + (it * 2 + s) * 1024);
+        }
+      }
+      eg[i] = ldf4(wsc + kEG + ld + it * 64);
+    }
+  };
+  load_q_own(wk0, ws0);
   // The first touches (chunk 2) go after chunk 0's Q / P loads, as in the
   // loop, so the wait for Q / P at the loop head counts the same on entry.
   __builtin_amdgcn_sched_barrier(0);
-  uint32_t ta, tb;
-  {
+  uint32_t ta = 0, tb = 0;
+  if (j == 0) {
     const int64_t co = (int64_t)min(2, last) * kWsChunk;
     ta = *reinterpret_cast<const uint32_t*>(t0b + co + t0o);
     tb = *reinterpret_cast<const uint32_t*>(t1b + co + t1o);
   }
   __builtin_amdgcn_sched_barrier(0);
   for (int c = 0; c < p.NC; ++c) {
-    lds_barrier();  // the state wave has published chunk c
+    lds_barrier();  // the state waves have published chunk c's S
     const Exchange& x = xb[c & 1];
-    u32x4 shi[4], slo[4], uh[2], ul[2];
+    f32x4 o[NIT];
+    {
+      u32x4 shi[4], slo[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      shi[s] = x.shi[s][lane];
-      slo[s] = x.slo[s][lane];
+      for (int s = 0; s < 4; ++s) {
+        shi[s] = x.shi[s][lane];
+        slo[s] = x.slo[s][lane];
+      }
+#pragma unroll
+      for (int i = 0; i < NIT; ++i) {
+        o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          o[i] = mfma(q[i][s], shi[s], o[i]);
+          o[i] = mfma(q[i][s], slo[s], o[i]);
+        }
+        o[i] = eg[i] * o[i];
+      }
     }
+    lds_barrier();  // ... and U
+    u32x4 uh[2], ul[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       uh[s] = x.uh[s][lane];
@@ -684,40 +732,36 @@ __device__ __forceinline__ void output_wave(const ChunkParams& p, int bh, int rb
     }
     const int nvalid = p.T - c * CH;
     uint16_t* obase = p.out + ((int64_t)b * p.T + (int64_t)c * CH) * orow + hv * D + rb * RB + r16;
-    f32x4 o[4];
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      o[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i < NIT; ++i) {
+      const int it = it0 + i;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        o[it] = mfma(qo.q[it][s], shi[s], o[it]);
-        o[it] = mfma(qo.q[it][s], slo[s], o[it]);
-      }
-      o[it] = qo.eg[it] * o[it];
-#pragma unroll
-      for (int s = 0; s < (it < 2 ? 1 : 2); ++s) {
-        o[it] = mfma(qo.ph[it][s], uh[s], o[it]);
-        o[it] = mfma(qo.ph[it][s], ul[s], o[it]);
-        o[it] = mfma(qo.pl[it][s], uh[s], o[it]);
+      for (int s = 0; s < 2; ++s) {
+        if (s == 0 || it >= 2) {
+          o[i] = mfma(ph[i][s], uh[s], o[i]);
+          o[i] = mfma(ph[i][s], ul[s], o[i]);
+          o[i] = mfma(pl[i][s], uh[s], o[i]);
+        }
       }
     }
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
+    for (int i = 0; i < NIT; ++i) {
+      const int it = it0 + i;
       if (nvalid >= CH)
-        store_out<false>(obase, orow, o[it], 16 * it + 4 * g4, nvalid);
+        store_out<false>(obase, orow, o[i], 16 * it + 4 * g4, nvalid);
       else
-        store_out<true>(obase, orow, o[it], 16 * it + 4 * g4, nvalid);
+        store_out<true>(obase, orow, o[i], 16 * it + 4 * g4, nvalid);
     }
     // Loads after the stores: waiting for them next chunk never depends on
     // how many stores the guarded path issued.
     __builtin_amdgcn_sched_barrier(0);
     {  // this chunk's Q, P consumed
       const int64_t cn = (int64_t)min(c + 1, last) * kWsChunk;
-      load_q(wk0 + cn, ws0 + cn, lf, ld, qo);
+      load_q_own(wk0 + cn, ws0 + cn);
     }
     __builtin_amdgcn_sched_barrier(0);
-    asm volatile("" ::"v"(ta), "v"(tb));
-    {
+    if (j == 0) {
+      asm volatile("" ::"v"(ta), "v"(tb));
       const int64_t co = (int64_t)min(c + 3, last) * kWsChunk;
       ta = *reinterpret_cast<const uint32_t*>(t0b + co + t0o);
       tb = *reinterpret_cast<const uint32_t*>(t1b + co + t1o);
@@ -727,23 +771,27 @@ __device__ __forceinline__ void output_wave(const ChunkParams& p, int bh, int rb
   asm volatile("" ::"v"(ta), "v"(tb));
 }
 
-// grid 64 * ceil(B*Hv / 8) two-wave workgroups.  Workgroup id x -> head
+// grid 64 * ceil(B*Hv / 8) workgroups of NSW state waves + NOW output waves.
+// Workgroup id x -> head
 // bh = 8 (x / 64) + x % 8, rows 16 ((x / 8) % 8): the 8 workgroups of a head
 // share x % 8, which places them on one XCD (workgroups go round-robin over
 // the 8 XCDs), so a chunk's operands come from HBM once and from that XCD's
-// L2 for the other 7.  Both waves pass the same number of barriers (one per
-// chunk) and leave together.
-__global__ __launch_bounds__(128) void chunk_state_kernel(const ChunkParams p) {
+// L2 for the other 7.  Every wave passes the same number of barriers (two
+// per chunk) and they leave together.
+template <int NSW, int NOW>
+__global__ __launch_bounds__(64 * (NSW + NOW)) void chunk_state_kernel(const ChunkParams p) {
   __shared__ Exchange xb[2];
+  __shared__ Partials<NSW> xp;
   const int id = blockIdx.x;
   const int rb = (id >> 3) & 7;
   const int bh = (id >> 6) * 8 + (id & 7);
   if (bh >= p.B * p.Hv) return;  // uniform over the workgroup
   const int lane = threadIdx.x & 63;
-  if (threadIdx.x < 64)
-    state_wave(p, bh, rb, lane, xb);
+  const int wave = threadIdx.x >> 6;
+  if (wave < NSW)
+    state_wave<NSW>(p, bh, rb, wave, lane, xb, &xp);
   else
-    output_wave(p, bh, rb, lane, xb);
+    output_wave<NOW>(p, bh, rb, wave - NSW, lane, xb);
 }
 
 }  // namespace
@@ -811,6 +859,8 @@ extern "C" int dflash_gdn_chunked_prefill(const void* q, const void* k, const vo
   hipLaunchKernelGGL(chunk_prep_kernel, dim3(p.NC, nbh), dim3(256), 0, s, p);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  hipLaunchKernelGGL(chunk_state_kernel, dim3((unsigned)(64 * ceil_div(nbh, 8))), dim3(128), 0, s, p);
+  const dim3 sgrid((unsigned)(64 * ceil_div(nbh, 8)));
+  hipLaunchKernelGGL((chunk_state_kernel<kStateWaves, kOutputWaves>), sgrid,
+                     dim3(64 * (kStateWaves + kOutputWaves)), 0, s, p);
   return to_status(hipGetLastError());
 }
