@@ -455,9 +455,10 @@ struct UOps {                // state wave, per chunk (loaded at the chunk's sta
   f32x4 ed[4];               // exp(G_63 - G) of the same token rows
   float egC;                 // exp(G_63)
 };
-struct Exchange {            // one chunk's S and U operand halves, [k-step][lane]
+struct Exchange {            // one chunk's S, U and diag(ED) U operand halves, [k-step][lane]
   u32x4 shi[4][64], slo[4][64];
   u32x4 uh[2][64], ul[2][64];
+  u32x4 dh[2][64], dl[2][64];
 };
 
 __device__ __forceinline__ void load_u(const uint8_t* wsc, uint32_t lu, uint32_t ld, UOps& o) {
@@ -515,9 +516,10 @@ struct Partials {            // the state waves' W S^T partials, [wave][token ti
 template <int NSW>
 __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb, int h, int lane,
                                            Exchange* xb, Partials<NSW>* xp) {
-  constexpr int NT = 8 / NSW;  // own result tiles (state columns / 16)
-  constexpr int NS = 4 / NSW;  // own k-steps (state columns / 32)
-  const int dt0 = NT * h, s0 = NS * h;
+  constexpr int NT = 8 / NSW;   // own result tiles (state columns / 16)
+  constexpr int NS = 4 / NSW;   // own k-steps (state columns / 32)
+  constexpr int TPW = 4 / NSW;  // own token tiles of U (reduced by this wave)
+  const int dt0 = NT * h, s0 = NS * h, it0 = TPW * h;
   const int r16 = lane & 15;
   const int g4 = lane >> 4;
   const uint32_t lf = lane * 16;              // operand fragments
@@ -552,15 +554,29 @@ __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb,
       for (int s = 0; s < 2; ++s) kt[j][s] = ld16(wsc + kKT + lf + ((dt0 + j) * 2 + s) * 1024);
     }
   };
-  load_w_own(ws0);
-  load_kt_own(wk0);
-  for (int c = 0; c < p.NC; ++c) {
-    // Chunks past the last re-read the last one: the loads stay unconditional.
-    const uint8_t* wsc = ws0 + (int64_t)c * kWsChunk;
+  auto load_u_own = [&](const uint8_t* wsc, UOps& o) {
+#pragma unroll
+    for (int i = 0; i < TPW; ++i) {
+      o.ut[i] = ldf4(wsc + kUT + lu + (it0 + i) * 1024);
+      o.ed[i] = ldf4(wsc + kED + ld + (it0 + i) * 64);
+    }
+    o.egC = *reinterpret_cast<const float*>(wsc + kEG + (CH - 1) * 4);
+  };
+  // One chunk of the chain.  uo holds this chunk's U~ / decays (loaded a
+  // chunk ahead); un receives the next chunk's.  The loop below runs it
+  // twice per trip with the two register sets swapped, so the prefetched
+  // values never need a register copy (a copy would wait for the load).
+  // One chunk of the chain.  uo holds this chunk's U~ / decays for the
+  // wave's own token tiles (loaded a chunk ahead); un receives the next
+  // chunk's.  The loop below runs it twice per trip with the two register
+  // sets swapped, so the prefetched values never need a register copy (a
+  // copy would wait for the load).
+  auto chunk = [&](int c, const UOps& uo, UOps& un) {
     const uint8_t* wsn = ws0 + (int64_t)min(c + 1, last) * kWsChunk;
     Exchange& x = xb[c & 1];
-    UOps uo;
-    load_u(wsc, lu, ld, uo);
+    __builtin_amdgcn_sched_barrier(0);
+    load_u_own(ws0 + (int64_t)min(c + 1, last) * kWsChunk, un);
+    __builtin_amdgcn_sched_barrier(0);
 
     // Own columns of S as the B operand (k = state column), hi / lo halves.
     u32x4 shi[NS], slo[NS];
@@ -570,8 +586,9 @@ __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb,
       x.shi[s0 + j][lane] = shi[j];
       x.slo[s0 + j][lane] = slo[j];
     }
-    // Own partial of W S^T, token tile it.
-    f32x4 part[4];
+    // Own partial of W S^T for every token tile: the wave's own tiles stay in
+    // registers, the others go to the waves that own them.
+    f32x4 part[TPW];
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -581,45 +598,47 @@ __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb,
         acc = mfma(whi[it][j], slo[j], acc);
         acc = mfma(wlo[it][j], shi[j], acc);
       }
-      part[it] = acc;
-      if (NSW > 1) xp->p[h][it][lane] = acc;
+      if (it / TPW == h)
+        part[it - it0] = acc;
+      else
+        xp->p[h][it][lane] = acc;
     }
     __builtin_amdgcn_sched_barrier(0);
     load_w_own(wsn);  // this chunk's W is consumed
     __builtin_amdgcn_sched_barrier(0);
     lds_barrier();  // partials (and S) published
 
-    // U = U~ - sum of the partials (in wave order), Ud = diag(ED) U.
-    f32x4 u[4], ud[4];
+    // Own token tiles: U = U~ - the partials summed in wave order,
+    // Ud = diag(ED) U; their hi / lo operand halves go to LDS (U for the
+    // output waves, Ud for the state update of every state wave).  Tile it
+    // fills words 2(it % 2), +1 of k-step it / 2.
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      f32x4 acc = part[it];
-      if (NSW > 1) {
-        acc = h == 0 ? part[it] : xp->p[0][it][lane];
+    for (int i = 0; i < TPW; ++i) {
+      const int it = it0 + i;
+      f32x4 acc = h == 0 ? part[i] : xp->p[0][it][lane];
 #pragma unroll
-        for (int w = 1; w < NSW; ++w) acc = acc + (w == h ? part[it] : xp->p[w][it][lane]);
-      }
-      u[it] = uo.ut[it] - acc;
-      ud[it] = uo.ed[it] * u[it];
+      for (int w = 1; w < NSW; ++w) acc = acc + (w == h ? part[i] : xp->p[w][it][lane]);
+      const f32x4 u = uo.ut[i] - acc;
+      const f32x4 ud = uo.ed[i] * u;
+      u32x2 hi, lo;
+      split4(u, hi, lo);
+      const int sk = it >> 1, wd = (it & 1) * 8;  // byte offset of the two words
+      *reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(&x.uh[sk][lane]) + wd) = hi;
+      *reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(&x.ul[sk][lane]) + wd) = lo;
+      split4(ud, hi, lo);
+      *reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(&x.dh[sk][lane]) + wd) = hi;
+      *reinterpret_cast<u32x2*>(reinterpret_cast<uint8_t*>(&x.dl[sk][lane]) + wd) = lo;
     }
     const float egC = uo.egC;
+    lds_barrier();  // chunk c's U and Ud are complete; the partials are read
 
-    // U (for the output wave, written by wave 0) and Ud as the B operand
-    // (k = token), hi / lo halves.
+    // Own columns: S^T = gamma_C S^T + K^T Ud  (K^T exact in bf16: two terms).
     u32x4 dh[2], dl[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      if (h == 0) {
-        u32x4 uh, ul;
-        split_pair(u[2 * s], u[2 * s + 1], uh, ul);
-        x.uh[s][lane] = uh;
-        x.ul[s][lane] = ul;
-      }
-      split_pair(ud[2 * s], ud[2 * s + 1], dh[s], dl[s]);
+      dh[s] = x.dh[s][lane];
+      dl[s] = x.dl[s][lane];
     }
-    lds_barrier();  // chunk c's S and U are visible to the output wave; partials read
-
-    // Own columns: S^T = gamma_C S^T + K^T Ud  (K^T exact in bf16: two terms).
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       f32x4 a = egC * sT[j];
@@ -633,6 +652,16 @@ __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb,
     __builtin_amdgcn_sched_barrier(0);
     load_kt_own(wk0 + (int64_t)min(c + 1, last) * kWsChunk);
     __builtin_amdgcn_sched_barrier(0);
+  };
+
+  UOps ua, ub;
+  load_u_own(ws0, ua);
+  load_w_own(ws0);
+  load_kt_own(wk0);
+  // Chunks past the last re-read the last one: the loads stay unconditional.
+  for (int c = 0; c < p.NC; c += 2) {
+    chunk(c, ua, ub);
+    if (c + 1 < p.NC) chunk(c + 1, ub, ua);  // uniform: NC is the same for every wave
   }
   if (p.final_state != nullptr) {
     float* s1 = p.final_state + ((int64_t)bh * D + rb * RB + r16) * D + 4 * g4;
