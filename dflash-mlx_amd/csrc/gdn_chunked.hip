@@ -513,13 +513,15 @@ struct Partials {            // the state waves' W S^T partials, [wave][token ti
   f32x4 p[NSW][4][64];
 };
 
-template <int NSW>
-__device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb, int h, int lane,
+// The wave index H is a template argument, so which tiles are the wave's own
+// is known at compile time (no exec-masked selects around the LDS traffic).
+template <int NSW, int H>
+__device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb, int lane,
                                            Exchange* xb, Partials<NSW>* xp) {
   constexpr int NT = 8 / NSW;   // own result tiles (state columns / 16)
   constexpr int NS = 4 / NSW;   // own k-steps (state columns / 32)
   constexpr int TPW = 4 / NSW;  // own token tiles of U (reduced by this wave)
-  const int dt0 = NT * h, s0 = NS * h, it0 = TPW * h;
+  constexpr int dt0 = NT * H, s0 = NS * H, it0 = TPW * H;
   const int r16 = lane & 15;
   const int g4 = lane >> 4;
   const uint32_t lf = lane * 16;              // operand fragments
@@ -562,10 +564,6 @@ __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb,
     }
     o.egC = *reinterpret_cast<const float*>(wsc + kEG + (CH - 1) * 4);
   };
-  // One chunk of the chain.  uo holds this chunk's U~ / decays (loaded a
-  // chunk ahead); un receives the next chunk's.  The loop below runs it
-  // twice per trip with the two register sets swapped, so the prefetched
-  // values never need a register copy (a copy would wait for the load).
   // One chunk of the chain.  uo holds this chunk's U~ / decays for the
   // wave's own token tiles (loaded a chunk ahead); un receives the next
   // chunk's.  The loop below runs it twice per trip with the two register
@@ -586,23 +584,25 @@ __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb,
       x.shi[s0 + j][lane] = shi[j];
       x.slo[s0 + j][lane] = slo[j];
     }
-    // Own partial of W S^T for every token tile: the wave's own tiles stay in
-    // registers, the others go to the waves that own them.
-    f32x4 part[TPW];
+    // Own partial of W S^T for every token tile, the four tiles' accumulation
+    // chains interleaved (each tile still sums its terms in the same order):
+    // the wave's own tiles stay in registers, the others go to the waves that
+    // own them.
+    f32x4 acc[4];
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int it = 0; it < 4; ++it) acc[it] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int j = 0; j < NS; ++j) {
-        acc = mfma(whi[it][j], shi[j], acc);
-        acc = mfma(whi[it][j], slo[j], acc);
-        acc = mfma(wlo[it][j], shi[j], acc);
-      }
-      if (it / TPW == h)
-        part[it - it0] = acc;
-      else
-        xp->p[h][it][lane] = acc;
+    for (int j = 0; j < NS; ++j) {
+#pragma unroll
+      for (int it = 0; it < 4; ++it) acc[it] = mfma(whi[it][j], shi[j], acc[it]);
+#pragma unroll
+      for (int it = 0; it < 4; ++it) acc[it] = mfma(whi[it][j], slo[j], acc[it]);
+#pragma unroll
+      for (int it = 0; it < 4; ++it) acc[it] = mfma(wlo[it][j], shi[j], acc[it]);
     }
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+      if (it / TPW != H) xp->p[H][it][lane] = acc[it];
     __builtin_amdgcn_sched_barrier(0);
     load_w_own(wsn);  // this chunk's W is consumed
     __builtin_amdgcn_sched_barrier(0);
@@ -615,10 +615,10 @@ __device__ __forceinline__ void state_wave(const ChunkParams& p, int bh, int rb,
 #pragma unroll
     for (int i = 0; i < TPW; ++i) {
       const int it = it0 + i;
-      f32x4 acc = h == 0 ? part[i] : xp->p[0][it][lane];
+      f32x4 sum = H == 0 ? acc[it] : xp->p[0][it][lane];
 #pragma unroll
-      for (int w = 1; w < NSW; ++w) acc = acc + (w == h ? part[i] : xp->p[w][it][lane]);
-      const f32x4 u = uo.ut[i] - acc;
+      for (int w = 1; w < NSW; ++w) sum = sum + (w == H ? acc[it] : xp->p[w][it][lane]);
+      const f32x4 u = uo.ut[i] - sum;
       const f32x4 ud = uo.ed[i] * u;
       u32x2 hi, lo;
       split4(u, hi, lo);
@@ -800,6 +800,18 @@ __device__ __forceinline__ void output_wave(const ChunkParams& p, int bh, int rb
   asm volatile("" ::"v"(ta), "v"(tb));
 }
 
+// Runs state wave `wave` (uniform) with its index as a template argument.
+template <int NSW, int H = 0>
+__device__ __forceinline__ void state_dispatch(int wave, const ChunkParams& p, int bh, int rb,
+                                               int lane, Exchange* xb, Partials<NSW>* xp) {
+  if constexpr (H < NSW) {
+    if (wave == H)
+      state_wave<NSW, H>(p, bh, rb, lane, xb, xp);
+    else
+      state_dispatch<NSW, H + 1>(wave, p, bh, rb, lane, xb, xp);
+  }
+}
+
 // grid 64 * ceil(B*Hv / 8) workgroups of NSW state waves + NOW output waves.
 // Workgroup id x -> head
 // bh = 8 (x / 64) + x % 8, rows 16 ((x / 8) % 8): the 8 workgroups of a head
@@ -816,9 +828,9 @@ __global__ __launch_bounds__(64 * (NSW + NOW)) void chunk_state_kernel(const Chu
   const int bh = (id >> 6) * 8 + (id & 7);
   if (bh >= p.B * p.Hv) return;  // uniform over the workgroup
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (wave < NSW)
-    state_wave<NSW>(p, bh, rb, wave, lane, xb, &xp);
+    state_dispatch<NSW>(wave, p, bh, rb, lane, xb, &xp);
   else
     output_wave<NOW>(p, bh, rb, wave - NSW, lane, xb);
 }
