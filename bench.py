@@ -27,7 +27,7 @@ and c2 (B = 32 serving batch) under "configs", each with its own roofline and
 CPU baseline.  Prints one JSON line.
 
 python bench.py [--steps K] [--warmup W] [--config 0|1|2] [--cpu-seconds S]
-                [--no-configs] [--no-extras] [--only lm_head|layer|prefill|hybrid]
+                [--no-configs] [--no-extras] [--only lm_head|layer|prefill|hybrid|gemm]
 """
 from __future__ import annotations
 

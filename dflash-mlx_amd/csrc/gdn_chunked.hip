@@ -16,14 +16,17 @@
 // fp32, then W^T = K^T (T diag(beta gamma))^T and U~ = (T diag(beta)) V on
 // bf16 MFMA with T split into hi + lo bf16 halves.  Everything phase 2 reads
 // is written pre-arranged in the operand order of its MFMAs.
-// Phase 2 (chunk_state_kernel, sequential over chunks, one wave per (head,
-// 16 state rows)): the state stays in registers in fp32; every product with
-// an fp32 operand splits it into hi + lo bf16 halves (x = hi + lo to about
-// 2^-16 relative) and accumulates hi*hi + hi*lo + lo*hi in fp32, so the state
-// keeps fp32-level accuracy over all chunks while running on the bf16 matrix
-// cores.  The wave owns all 128 columns of its 16 state rows, so the chunk
-// loop needs no LDS and no barrier: every intermediate comes out of one MFMA
-// in the register layout the next MFMA reads.
+// Phase 2 (chunk_state_kernel, sequential over chunks, one workgroup per
+// (head, 16 state rows)): the state stays in registers in fp32; every
+// product with an fp32 operand splits it into hi + lo bf16 halves (x = hi +
+// lo to about 2^-16 relative) and accumulates hi*hi + hi*lo + lo*hi in fp32,
+// so the state keeps fp32-level accuracy over all chunks while running on
+// the bf16 matrix cores.  Four state waves each own 32 of the 128 state
+// columns: per chunk each forms its partial of W S^T over its columns, the
+// partials meet in LDS, each wave reduces one 16-token tile of U and
+// publishes U and diag(ED) U as bf16 halves, and each updates its own
+// columns of S (two barriers per chunk).  Two output waves compute
+// O = diag(EG) Q S^T + P U from the same LDS exchange, off the chain.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -437,18 +440,17 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(const ChunkParams p) {
 }
 
 // ------------------------------------------------------------------ phase 2
-// A workgroup of two waves owns state rows r = 16rb + (lane % 16) of one head.
-// The state wave keeps all 128 columns of those rows in fp32 as the 8 result
-// tiles of the state update S^T[dk][r] (tile dt: lane holds columns
-// 16dt + 4g + e, g = lane / 16).  Read pairwise, tiles 2s and 2s+1 are
-// exactly the B operand of k-step s of the products with S (slot t*4+e =
-// column 32s+16t+4g+e), and the U tiles of the W product are the B operand
-// of P U and of the state update in the same way, so the state chain
+// A workgroup owns state rows r = 16rb + (lane % 16) of one head.  The
+// state is held as the 8 result tiles of the state update S^T[dk][r] (tile
+// dt: lane holds columns 16dt + 4g + e, g = lane / 16), split over the state
+// waves by column.  Read pairwise, tiles 2s and 2s+1 are exactly the B
+// operand of k-step s of the products with S (slot t*4+e = column
+// 32s+16t+4g+e), and the U tiles of the W product are the B operand of P U
+// and of the state update in the same way, so the state chain
 //   U = U~ - W S^T,  S^T <- gamma_C S^T + K^T diag(ED) U
-// is MFMAs and register arithmetic only.  It hands S and U (as bf16 hi / lo
-// operand halves) to the output wave through LDS, double-buffered, with one
-// barrier per chunk; the output wave computes O = diag(EG) Q S^T + P U one
-// chunk behind, off the chain.
+// is MFMAs, register arithmetic and LDS exchanges.  S and U (as bf16 hi / lo
+// operand halves) are double-buffered in LDS for the output waves, which
+// compute O = diag(EG) Q S^T + P U between the same two barriers per chunk.
 
 struct UOps {                // state wave, per chunk (loaded at the chunk's start)
   f32x4 ut[4];               // U~[16it + 4g + e][16rb + lane%16]
@@ -502,12 +504,13 @@ __device__ __forceinline__ const uint8_t* qk_base(const ChunkParams& p, int bh) 
 
 // State wave h of NSW owns state columns [128h/NSW, 128(h+1)/NSW): result
 // tiles dt in [8h/NSW, 8(h+1)/NSW) and k-steps s in [4h/NSW, 4(h+1)/NSW) of
-// the products with S.  Per chunk it forms its partial W[:, its k] S[:, its k]^T,
-// the waves exchange partials through LDS (one barrier), every wave sums
-// them in wave order (so all hold the same U, bit for bit), and each
-// updates only its own columns of S; the output wave reads S and U after a
-// second barrier.  With NSW = 1 there is no partial exchange (the first
-// barrier is still passed, so every wave counts two per chunk).
+// the products with S, and token tiles [4h/NSW, 4(h+1)/NSW) of U.  Per chunk
+// it forms its partial W[:, its k] S[:, its k]^T for every token tile and
+// hands the other waves theirs through LDS (first barrier); it sums the
+// partials of its own token tiles in wave order and publishes U and
+// diag(ED) U as bf16 halves (second barrier); then every wave updates its
+// own columns of S from the whole diag(ED) U.  The output waves read S after
+// the first barrier and U after the second.
 template <int NSW>
 struct Partials {            // the state waves' W S^T partials, [wave][token tile][lane]
   f32x4 p[NSW][4][64];
