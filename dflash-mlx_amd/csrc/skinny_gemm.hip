@@ -61,6 +61,24 @@ struct GemmParams {
   float* part;  // [nsplit][M][N] when f32_out
   int M, N, K, nsplit, ks_per_split, f32_out;
   int swiglu;  // bf16 epilogue silu(tile 0) * tile 1 into column block N/2 (VT == 2)
+  // fin (KW == 16, one 16-column tile per workgroup): the projection's output
+  // r = bf16(x . w^T) is added to the residual stream, h = bf16(resid + r)
+  // to h_out (and hc), and the tile's per-row sum of h^2 goes to
+  // row_sumsq[tile][m]; nothing else is stored.
+  int fin;
+  const uint16_t* resid;  // [M][N], may alias h_out
+  uint16_t* h_out;        // [M][N]
+  uint16_t* hc;           // [M] rows of stride hc_stride, or null
+  int64_t hc_stride;
+  float* row_sumsq;       // [N / 16][M]
+  // NRM kernels: x holds h, and the B operand is the RMSNorm output
+  // bf16((h * inv[m]) * nw[k]) with inv[m] = 1 / sqrt(sum_t norm_sumsq[t][m]
+  // / K + eps), the sum over the norm_tiles row sums of the producing call.
+  const uint16_t* nw;          // [K]
+  const float* norm_sumsq;     // [norm_tiles][M]
+  int norm_tiles;
+  float eps;
+  float* row_inv_out;          // [M] or null: inv, stored by workgroup (0, 0)
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -71,20 +89,116 @@ struct GStage {
   u32x4 b[MT][2];
 };
 
-// KW = waves of the workgroup that share one group of weight rows: 1 (each
-// wave streams its own 16*VT rows over the split's k-range) or 4 (the four
-// waves stream the same 16*VT rows over quarters of the k-range and merge
-// their sums through LDS: four times the loads in flight per output tile,
-// without partial sums in memory).
-template <int MT, int VT, int D, int KW, bool TILED>
-__global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams p) {
-  __shared__ __attribute__((aligned(16))) unsigned char atile[kGThreads / 64][VT * 16 * kGTileRowBytes];
+// Largest K of an NRM launch: the norm weight of the workgroup's k-range is
+// staged in LDS (2 bytes per k).
+constexpr int kMaxNormK = 16384;
+
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+// bf16((h * inv) * w) for 8 packed bf16 h and w: the RMSNorm output, with the
+// arithmetic of the standalone add + RMSNorm kernel (the packing is the
+// hardware round to nearest even, v_cvt_pk_bf16_f32: the same bits for every
+// finite value).
+__device__ __forceinline__ u32x4 norm8(u32x4 h, u32x4 w, float inv) {
+  const uint32_t hv[4] = {h.x, h.y, h.z, h.w}, wv[4] = {w.x, w.y, w.z, w.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = bf16_lo(hv[i]) * inv * bf16_lo(wv[i]);
+    const float b = bf16_hi(hv[i]) * inv * bf16_hi(wv[i]);
+    o[i] = __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
+  }
+  return u32x4{o[0], o[1], o[2], o[3]};
+}
+
+__device__ __forceinline__ float bf16r(float x) { return bf16_bits_to_f32(f32_to_bf16_rne(x)); }
+
+// The fin epilogue (KW 8 or 16): wave 0 holds the workgroup's whole tile.
+// Lane (r16, g) of tile (vt, mt) holds out[m = mt*16 + r16][n = nwave +
+// vt*16 + 4g .. +3].
+template <int MT, int VT>
+__device__ __forceinline__ void residual_tile(const GemmParams& p, const f32x4 (&acc)[VT][MT],
+                                              int nwave, int lane) {
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + r16;
+    const bool mv = m < p.M;
+    const int mc = mv ? m : p.M - 1;
+#pragma unroll
+    for (int vt = 0; vt < VT; ++vt) {
+      const int n = nwave + vt * 16 + 4 * g;
+      if (n >= p.N) continue;  // N % 16 == 0: whole 16-column tiles
+      float ss = 0.f;
+      const u32x2 rr = *reinterpret_cast<const u32x2*>(p.resid + (int64_t)mc * p.N + n);
+      float v[4] = {bf16_lo(rr.x), bf16_hi(rr.x), bf16_lo(rr.y), bf16_hi(rr.y)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = bf16r(v[i] + bf16r(acc[vt][mt][i]));
+      const u32x2 hv = u32x2{(uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16),
+                             (uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16)};
+      if (mv) {
+        *reinterpret_cast<u32x2*>(p.h_out + (int64_t)m * p.N + n) = hv;
+        if (p.hc != nullptr) *reinterpret_cast<u32x2*>(p.hc + (int64_t)m * p.hc_stride + n) = hv;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) ss = fmaf(v[i], v[i], ss);
+      ss += __shfl_xor(ss, 16, 64);  // the row's four column groups, in a fixed tree
+      ss += __shfl_xor(ss, 32, 64);
+      if (g == 0 && mv) p.row_sumsq[(int64_t)(nwave / 16 + vt) * p.M + m] = ss;
+    }
+  }
+}
+
+// NRM prologue: inv[m] for every row from the producer's per-tile row sums.
+// Fixed order whatever M and the launch shape: row m's sums are split over
+// 16 groups (group j takes tiles j, j + 16, ...; in order), the 16 group
+// sums added in order.  Uses the first 256 threads; ends with a barrier.
+__device__ __forceinline__ void norm_inv(const GemmParams& p, float* invp, float* invs) {
+  const int t = threadIdx.x;
+  for (int m0 = 0; m0 < p.M; m0 += 16) {
+    if (t < 256) {
+      const int m = m0 + (t & 15), j = t >> 4;
+      const int mc = min(m, p.M - 1);
+      float part = 0.f;
+      for (int t0 = j; t0 < p.norm_tiles; t0 += 16 * 16) {  // 16 loads in flight
+        float v[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          v[i] = p.norm_sumsq[(int64_t)min(t0 + 16 * i, p.norm_tiles - 1) * p.M + mc];
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (t0 + 16 * i < p.norm_tiles) part += v[i];
+      }
+      invp[j * 16 + (t & 15)] = part;
+    }
+    __syncthreads();
+    if (t < 16 && m0 + t < p.M) {
+      float tot = 0.f;
+      for (int j = 0; j < 16; ++j) tot += invp[j * 16 + t];
+      const float iv = 1.f / sqrtf(tot / (float)p.K + p.eps);
+      invs[m0 + t] = iv;
+      if (p.row_inv_out != nullptr && blockIdx.x == 0 && blockIdx.y == 0) p.row_inv_out[m0 + t] = iv;
+    }
+    __syncthreads();
+  }
+}
+
+template <int MT, int VT, int D, int KW, bool TILED, bool NRM = false>
+__global__ __launch_bounds__(KW >= 8 ? 64 * KW : kGThreads) void skinny_gemm_kernel(const GemmParams p) {
+  constexpr int kThreads = KW >= 8 ? 64 * KW : kGThreads;  // KW 8 / 16: one row group
+  // the row-major path's per-wave staging tile (tiled weights load straight
+  // into registers)
+  __shared__ __attribute__((aligned(16))) unsigned char atile[kThreads / 64][TILED ? 16 : VT * 16 * kGTileRowBytes];
   __shared__ f32x4 red[KW > 1 ? KW - 1 : 1][VT * MT][64];
+  __shared__ __attribute__((aligned(16))) uint16_t nwl[NRM ? kMaxNormK : 8];
+  __shared__ float invp[NRM ? 256 : 1], invs[NRM ? 64 : 1];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int r16 = lane & 15;
   const int g = lane >> 4;
-  constexpr int kRowGroups = (kGThreads / 64) / KW;  // row groups per workgroup
+  constexpr int kRowGroups = (kThreads / 64) / KW;  // row groups per workgroup
   static_assert(KW == 1 || kRowGroups == 1, "red[] holds the k-parts of one row group");
   const int kpart = wave % KW;                        // this wave's quarter of the k-range
   const int nwave = (blockIdx.x * kRowGroups + wave / KW) * VT * 16;
@@ -115,6 +229,8 @@ __global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
     xrow[mt] = p.x + (int64_t)min(mt * 16 + r16, p.M - 1) * p.xs + (int64_t)ks_begin * kGKStep + g * 16;
+  // this wave's norm-weight pieces: k-step ks at nwb + ks * kGKStep
+  const uint16_t* nwb = nwl + (ks_begin - split_begin) * kGKStep + g * 16;
 
   auto load = [&](GStage<MT, VT>& st, int ks) {
     const int off = ks * kGKStep;
@@ -143,6 +259,20 @@ __global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams
   for (int d = 0; d < D; ++d)
     if (d < nks) load(ring[d], d);
 
+  // NRM: with the first weight loads in flight, the norm weight of the
+  // split's k-range goes to LDS and inv[m] is formed (every wave is here).
+  float inv[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) inv[mt] = 1.f;
+  if (NRM) {
+    const int k0 = split_begin * kGKStep, n8 = split_len * (kGKStep / 8);
+    for (int i = threadIdx.x; i < n8; i += kThreads)
+      *reinterpret_cast<u32x4*>(nwl + 8 * i) = *reinterpret_cast<const u32x4*>(p.nw + k0 + 8 * i);
+    norm_inv(p, invp, invs);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) inv[mt] = invs[min(mt * 16 + r16, p.M - 1)];
+  }
+
   for (int ks0 = 0; ks0 < nks; ks0 += D) {
 #pragma unroll
     for (int d = 0; d < D; ++d) {
@@ -166,14 +296,25 @@ __global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams
             for (int h = 0; h < 2; ++h)
               a[vt][h] = *reinterpret_cast<const u32x4*>(tile + (vt * 16 + r16) * kGTileRowBytes + (2 * g + h) * 16);
         }
+        u32x4 b[MT][2];
+        u32x4 nwv[2] = {};
+        if (NRM) {
+          nwv[0] = *reinterpret_cast<const u32x4*>(nwb + ks * kGKStep);
+          nwv[1] = *reinterpret_cast<const u32x4*>(nwb + ks * kGKStep + 8);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            b[mt][h] = NRM ? norm8(ring[d].b[mt][h], nwv[h], inv[mt]) : ring[d].b[mt][h];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int vt = 0; vt < VT; ++vt) {
             acc[vt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                as_bf16x8(a[vt][0]), as_bf16x8(ring[d].b[mt][0]), acc[vt][mt], 0, 0, 0);
+                as_bf16x8(a[vt][0]), as_bf16x8(b[mt][0]), acc[vt][mt], 0, 0, 0);
             acc[vt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                as_bf16x8(a[vt][1]), as_bf16x8(ring[d].b[mt][1]), acc[vt][mt], 0, 0, 0);
+                as_bf16x8(a[vt][1]), as_bf16x8(b[mt][1]), acc[vt][mt], 0, 0, 0);
           }
         if (ks + D < nks) load(ring[d], ks + D);
       }
@@ -195,6 +336,10 @@ __global__ __launch_bounds__(kGThreads) void skinny_gemm_kernel(const GemmParams
       for (int vt = 0; vt < VT; ++vt)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[vt][mt] += red[q][vt * MT + mt][lane];
+  }
+  if (KW >= 8 && p.fin) {
+    residual_tile<MT, VT>(p, acc, nwave, lane);
+    return;
   }
   // Lane (r16, g) of tile (vt, mt) holds out[m = mt*16 + r16][n = nwave + vt*16 + 4g .. +3].
 #pragma unroll
@@ -255,21 +400,25 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, i
   }
 }
 
-template <int MT, int VT, int KW, bool TILED>
+template <int MT, int VT, int KW, bool TILED, bool NRM = false>
 hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
   constexpr int D = MT == 1 ? 4 : (MT == 2 ? 4 : 2);
-  const int rows_per_wg = (kGThreads / 64 / KW) * VT * 16;
+  constexpr int kThreads = KW >= 8 ? 64 * KW : kGThreads;
+  const int rows_per_wg = (kThreads / 64 / KW) * VT * 16;
   const dim3 grid((unsigned)ceil_div(p.N, rows_per_wg), (unsigned)p.nsplit);
-  hipLaunchKernelGGL((skinny_gemm_kernel<MT, VT, D, KW, TILED>), grid, dim3(kGThreads), 0, s, p);
+  hipLaunchKernelGGL((skinny_gemm_kernel<MT, VT, D, KW, TILED, NRM>), grid, dim3(kThreads), 0, s, p);
   return hipGetLastError();
 }
 
-template <int VT, int KW, bool TILED = false>
+template <int VT, int KW, bool TILED = false, bool NRM = false>
 hipError_t launch_m(const GemmParams& p, hipStream_t s) {
   const int mt = (int)ceil_div(p.M, 16);
-  return mt == 1 ? launch_gemm<1, VT, KW, TILED>(p, s) : mt == 2 ? launch_gemm<2, VT, KW, TILED>(p, s)
-       : mt == 3 ? launch_gemm<3, VT, KW, TILED>(p, s) : launch_gemm<4, VT, KW, TILED>(p, s);
+  return mt == 1 ? launch_gemm<1, VT, KW, TILED, NRM>(p, s)
+       : mt == 2 ? launch_gemm<2, VT, KW, TILED, NRM>(p, s)
+       : mt == 3 ? launch_gemm<3, VT, KW, TILED, NRM>(p, s)
+                 : launch_gemm<4, VT, KW, TILED, NRM>(p, s);
 }
+
 
 // dst = src stored as A fragments: dst[((ks * (N/16) + rt) * 2 + h) * 512 + lane * 8 + e]
 //   = src[16 rt + lane % 16][64 ks + 16 (lane / 16) + 8 h + e].
@@ -474,4 +623,136 @@ extern "C" int dflash_gemm_bf16_swiglu_tiled(const void* x, int64_t x_row_stride
   p.swiglu = 1;
   hipStream_t s = static_cast<hipStream_t>(stream);
   return to_status(k_waves == 1 ? launch_m<2, 1, true>(p, s) : launch_m<2, 4, true>(p, s));
+}
+
+// ----------------------------------------------- residual + RMSNorm folded in
+// The decoder's `h = h + proj(...)` then `x = rms_norm(h, w)` (the residual
+// adds and norms around every projection pair) without a launch of their
+// own: the projection that produces the branch adds it to h and stores h's
+// per-tile row sums of squares (fin: 16 waves per workgroup split K, so a
+// workgroup owns whole output columns and needs nothing from another), and
+// the next projection forms the norm's row scale from them and normalizes
+// its activation rows on load (NRM).
+
+extern "C" int dflash_gemm_bf16_tiled_residual_norm(const void* x, int64_t x_row_stride,
+                                                    const void* w_tiled, int M, int N, int K,
+                                                    const void* resid, void* h_out, void* h_copy,
+                                                    int64_t h_copy_row_stride, float* row_sumsq,
+                                                    void* stream) {
+  if (M < 0 || M > 64 || N <= 0 || N % 16 != 0 || K <= 0 || K % kGKStep != 0) return DFLASH_ERR_SHAPE;
+  if (h_copy != nullptr && h_copy_row_stride < N) return DFLASH_ERR_SHAPE;
+  if (M == 0) return DFLASH_OK;
+  if (x == nullptr || w_tiled == nullptr || resid == nullptr || h_out == nullptr ||
+      row_sumsq == nullptr)
+    return DFLASH_ERR_NULL;
+  if (((uintptr_t)x & 15) || ((uintptr_t)w_tiled & 15) || (x_row_stride % 8) || x_row_stride < K ||
+      ((uintptr_t)resid & 7) || ((uintptr_t)h_out & 7) || ((uintptr_t)h_copy & 7) ||
+      (h_copy != nullptr && (h_copy_row_stride % 4)) || ((uintptr_t)row_sumsq & 3))
+    return DFLASH_ERR_ALIGN;
+  GemmParams p{};
+  p.x = static_cast<const uint16_t*>(x);
+  p.xs = x_row_stride;
+  p.w = static_cast<const uint16_t*>(w_tiled);
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.ks_per_split = K / kGKStep;
+  p.nsplit = 1;
+  p.fin = 1;
+  p.resid = static_cast<const uint16_t*>(resid);
+  p.h_out = static_cast<uint16_t*>(h_out);
+  p.hc = static_cast<uint16_t*>(h_copy);
+  p.hc_stride = h_copy_row_stride;
+  p.row_sumsq = row_sumsq;
+  return to_status(launch_m<1, 16, true>(p, static_cast<hipStream_t>(stream)));
+}
+
+namespace dflash {
+namespace {
+int set_norm_input(GemmParams& p, const void* h, int64_t h_row_stride, const void* norm_weight,
+                   const float* row_sumsq, int norm_tiles, float eps, float* row_inv_out, int K) {
+  if (K > kMaxNormK || norm_tiles < 1) return DFLASH_ERR_SHAPE;
+  if (h == nullptr || norm_weight == nullptr || row_sumsq == nullptr) return DFLASH_ERR_NULL;
+  if (((uintptr_t)h & 15) || ((uintptr_t)norm_weight & 15) || (h_row_stride % 8) ||
+      h_row_stride < K || ((uintptr_t)row_sumsq & 3) || ((uintptr_t)row_inv_out & 3))
+    return DFLASH_ERR_ALIGN;
+  p.x = static_cast<const uint16_t*>(h);
+  p.xs = h_row_stride;
+  p.nw = static_cast<const uint16_t*>(norm_weight);
+  p.norm_sumsq = row_sumsq;
+  p.norm_tiles = norm_tiles;
+  p.eps = eps;
+  p.row_inv_out = row_inv_out;
+  return DFLASH_OK;
+}
+}  // namespace
+}  // namespace dflash
+
+extern "C" int dflash_gemm_bf16_tiled_normed(const void* h, int64_t h_row_stride,
+                                             const void* norm_weight, const float* row_sumsq,
+                                             int norm_tiles, float eps, float* row_inv_out,
+                                             const void* w_tiled, void* out, int64_t out_row_stride,
+                                             int M, int N, int K, int nsplit, int rows_per_wave,
+                                             int k_waves, void* stream) {
+  if (M < 0 || M > 64 || N <= 0 || N % 16 != 0 || K <= 0 || K % kGKStep != 0 || nsplit < 1)
+    return DFLASH_ERR_SHAPE;
+  if ((rows_per_wave != 16 && rows_per_wave != 32 && rows_per_wave != 64) || k_waves != 4)
+    return DFLASH_ERR_UNSUPPORTED;
+  if (M == 0) return DFLASH_OK;
+  GemmParams p{};
+  int st = set_norm_input(p, h, h_row_stride, norm_weight, row_sumsq, norm_tiles, eps, row_inv_out, K);
+  if (st != DFLASH_OK) return st;
+  if (w_tiled == nullptr || out == nullptr) return DFLASH_ERR_NULL;
+  if ((uintptr_t)w_tiled & 15) return DFLASH_ERR_ALIGN;
+  p.w = static_cast<const uint16_t*>(w_tiled);
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  const int nks = K / kGKStep;
+  p.ks_per_split = (int)ceil_div(nks, std::min(nsplit, nks));
+  p.nsplit = (int)ceil_div(nks, p.ks_per_split);
+  p.f32_out = nsplit > 1;
+  if (p.f32_out) {
+    if ((uintptr_t)out & 15) return DFLASH_ERR_ALIGN;
+    p.part = static_cast<float*>(out);
+  } else {
+    if (((uintptr_t)out & 7) || (out_row_stride % 4) || out_row_stride < N) return DFLASH_ERR_ALIGN;
+    p.out = static_cast<uint16_t*>(out);
+    p.os = out_row_stride;
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (rows_per_wave == 16) e = launch_m<1, 4, true, true>(p, s);
+  else if (rows_per_wave == 32) e = launch_m<2, 4, true, true>(p, s);
+  else e = launch_m<4, 4, true, true>(p, s);
+  return to_status(e);
+}
+
+extern "C" int dflash_gemm_bf16_swiglu_tiled_normed(const void* h, int64_t h_row_stride,
+                                                    const void* norm_weight, const float* row_sumsq,
+                                                    int norm_tiles, float eps, float* row_inv_out,
+                                                    const void* w_pairs_tiled, void* out,
+                                                    int64_t out_row_stride, int M, int N, int K,
+                                                    int k_waves, void* stream) {
+  if (M < 0 || M > 64 || N <= 0 || N % 32 != 0 || K <= 0 || K % kGKStep != 0)
+    return DFLASH_ERR_SHAPE;
+  if (k_waves != 4) return DFLASH_ERR_UNSUPPORTED;
+  if (M == 0) return DFLASH_OK;
+  GemmParams p{};
+  int st = set_norm_input(p, h, h_row_stride, norm_weight, row_sumsq, norm_tiles, eps, row_inv_out, K);
+  if (st != DFLASH_OK) return st;
+  if (w_pairs_tiled == nullptr || out == nullptr) return DFLASH_ERR_NULL;
+  if (((uintptr_t)w_pairs_tiled & 15) || ((uintptr_t)out & 7) || (out_row_stride % 4) ||
+      out_row_stride < N / 2)
+    return DFLASH_ERR_ALIGN;
+  p.w = static_cast<const uint16_t*>(w_pairs_tiled);
+  p.out = static_cast<uint16_t*>(out);
+  p.os = out_row_stride;
+  p.M = M;
+  p.N = N;
+  p.K = K;
+  p.ks_per_split = K / kGKStep;
+  p.nsplit = 1;
+  p.swiglu = 1;
+  return to_status(launch_m<2, 4, true, true>(p, static_cast<hipStream_t>(stream)));
 }

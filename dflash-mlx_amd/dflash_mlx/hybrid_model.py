@@ -183,7 +183,8 @@ class HybridVerifyRunner:
     pieces, single tokens, chunked verify)."""
 
     def __init__(self, cfg: HybridConfig, weights: HybridWeights, B: int, T: int, Smax: int,
-                 device: torch.device, weight_layout: str = "tiled", fused_prologue: bool = True):
+                 device: torch.device, weight_layout: str = "tiled", fused_prologue: bool = True,
+                 fused_norms: bool = True):
         """weight_layout: "tiled" streams weights re-laid out once as MFMA
         fragments (dflash_weight_tile_bf16, cached in the layer dicts as
         "<name>_tiled"; same sums bit for bit) wherever the row count is a
@@ -191,10 +192,17 @@ class HybridVerifyRunner:
         nn.Linear [N, K] weights as they are.  fused_prologue: each
         gated-delta layer's scan computes its own prologue
         (dflash_gdn_prologue_scan_rollback, one launch, same bits) instead of
-        a prologue launch then the scan."""
+        a prologue launch then the scan.  fused_norms (tiled weights): the
+        residual adds and RMSNorms between projections run inside them
+        (dflash_gemm_bf16_tiled_residual_norm adds the branch to h and stores
+        h's row sums of squares, the next projection normalizes on load) instead
+        of an add + RMSNorm launch per norm; the producing projections then
+        split K inside a workgroup instead of across workgroups, so their
+        sums (and what follows) differ from the launch form in rounding."""
         if weight_layout not in ("tiled", "rowmajor"):
             raise ValueError(f"weight_layout must be 'tiled' or 'rowmajor', got {weight_layout!r}")
         self.tiled = weight_layout == "tiled"
+        self.fused_norms = bool(fused_norms) and self.tiled
         self.fused_prologue = bool(fused_prologue) and cfg.linear.linear_key_head_dim == 128
         if B < 1 or T < 1 or T > 16 or B * T > 64:
             raise ValueError("the verify step takes 1 <= T <= 16 block tokens and B*T <= 64 rows")
@@ -214,6 +222,9 @@ class HybridVerifyRunner:
         self.xn = e(M, H)
         self.r = e(M, H)
         self.mlp_act = e(M, I)
+        # fused norms: the per-16-column row sums of h^2 a producing projection
+        # hands the next (normed) projection
+        self.row_sumsq = z(max(H // 16, 1) * M, dt=f32)
         # gated-delta layers: per-layer projection rows (the conv rollback reads
         # their qkv part after the accept), conv window, state, tape
         nl, na = cfg.n_linear, cfg.n_attention
@@ -315,6 +326,9 @@ class HybridVerifyRunner:
                     n = lw[name].shape[0]
                     if n % 16 == 0:  # the fragment layout needs whole 16-row tiles
                         tile(lw, name)
+        if self.fused_norms and not (all(self.plan[n][2] == 4 for n in ("w_in", "w_qkv", "w_gu"))
+                                     and H % 16 == 0 and H <= 16384):
+            self.fused_norms = False  # the normed projections stream with k_waves == 4
         if self.tiled and cfg.vocab_size % 16 == 0 and self.w.lm_head_tiled is None:
             from .runtime import tile_weight
 
@@ -358,6 +372,27 @@ class HybridVerifyRunner:
         rpw, kw = self.GEMM_PLAN[name][1], self.GEMM_PLAN[name][2]
         return ("dflash_gemm_bf16", (x.data_ptr(), x.stride(0), w.data_ptr(), w.stride(0), out_ptr,
                                      out_stride, M, n, k, ns, rpw, kw))
+
+    def _fusable(self, lw, *names) -> bool:
+        """The fused-norm forms apply: every named projection of this layer
+        has its tiled copy."""
+        return self.fused_norms and all(n + "_tiled" in lw for n in names)
+
+    def _residual_norm_op(self, lw, name, x, M, capture):
+        """Projection `name` with h += its output and the row sums of h^2 (per
+        16 columns) for the next (normed) projection."""
+        n, k = self._dims()[name]
+        cap, cap_stride = capture if capture is not None else (None, 0)
+        return ("dflash_gemm_bf16_tiled_residual_norm",
+                (x.data_ptr(), x.stride(0), lw[name + "_tiled"].data_ptr(), M, n, k,
+                 self.h.data_ptr(), self.h.data_ptr(), cap, cap_stride, self.row_sumsq.data_ptr()))
+
+    def _norm_input(self, w_norm):
+        """Arguments of a normed projection's input: RMSNorm(h) with weight
+        w_norm, from the producing call's row sums."""
+        H = self.cfg.hidden_size
+        return (self.h.data_ptr(), self.h.stride(0), w_norm.data_ptr(), self.row_sumsq.data_ptr(),
+                H // 16, float(self.cfg.rms_norm_eps), None)
 
     def _residual_op(self, name, w_norm, M, capture):
         """h += the branch projection `name` just produced; xn = norm(h);
@@ -408,11 +443,15 @@ class HybridVerifyRunner:
                     (self.w.embed.data_ptr(), self.tokens.data_ptr(), cfg.vocab_size,
                      self.w.layers[0]["ln_in"].data_ptr(), self.h.data_ptr(), self.xn.data_ptr(),
                      M, H, eps)))
+        L = cfg.num_hidden_layers
         gi = ai = 0
-        for i in range(cfg.num_hidden_layers):
+        for i in range(L):
             lw = self.w.layers[i]
             if i > 0:
                 fwd.append(self._residual_op("w_down", lw["ln_in"], M, capture_of(i - 1)))
+            # the post-attention norm folds when this layer's output projection
+            # and its gate|up GEMM both have tiled copies
+            post = self._fusable(lw, "w_out" if cfg.is_linear(i) else "w_o", "w_gu_pairs")
             if cfg.is_linear(i):
                 gw = lw["gdn"]
                 base = self.proj[gi].data_ptr()
@@ -441,9 +480,13 @@ class HybridVerifyRunner:
                 fwd.append(("dflash_gdn_gated_rmsnorm",
                             (out, base + 2 * C, z_strides, gw.norm_weight.data_ptr(),
                              self.gnorm.data_ptr(), B, T, Hv, Dv, eps)))
-                fwd.append(self._gemm_op(lw, "w_out", self.gnorm.view(-1, Hv * Dv),
-                                         *dst("w_out", self.r), M))
-                fwd.append(self._residual_op("w_out", lw["ln_post"], M, None))
+                if post:
+                    fwd.append(self._residual_norm_op(lw, "w_out", self.gnorm.view(-1, Hv * Dv), M,
+                                                      None))
+                else:
+                    fwd.append(self._gemm_op(lw, "w_out", self.gnorm.view(-1, Hv * Dv),
+                                             *dst("w_out", self.r), M))
+                    fwd.append(self._residual_op("w_out", lw["ln_post"], M, None))
                 gi += 1
             else:
                 fwd.append(self._gemm_op(lw, "w_qkv", self.xn, *dst("w_qkv", self.aproj), M))
@@ -462,11 +505,19 @@ class HybridVerifyRunner:
                              self.aproj.data_ptr(), arows, self.attn_out.data_ptr(), B, T, Hq, Hkv,
                              D, self.Smax, self.Smax, float(D ** -0.5), self.attn_ws.data_ptr(),
                              self.attn_ws.numel())))
-                fwd.append(self._gemm_op(lw, "w_o", self.attn_out, *dst("w_o", self.r), M))
-                fwd.append(self._residual_op("w_o", lw["ln_post"], M, None))
+                if post:
+                    fwd.append(self._residual_norm_op(lw, "w_o", self.attn_out, M, None))
+                else:
+                    fwd.append(self._gemm_op(lw, "w_o", self.attn_out, *dst("w_o", self.r), M))
+                    fwd.append(self._residual_op("w_o", lw["ln_post"], M, None))
                 ai += 1
             gu_key = "w_gu_pairs_tiled" if self.tiled and "w_gu_pairs_tiled" in lw else None
-            if gu_key:
+            if post:
+                fwd.append(("dflash_gemm_bf16_swiglu_tiled_normed",
+                            self._norm_input(lw["ln_post"]) + (lw[gu_key].data_ptr(),
+                                                               self.mlp_act.data_ptr(), I, M, 2 * I,
+                                                               H, self.plan["w_gu"][2])))
+            elif gu_key:
                 fwd.append(("dflash_gemm_bf16_swiglu_tiled",
                             (self.xn.data_ptr(), H, lw[gu_key].data_ptr(), self.mlp_act.data_ptr(),
                              I, M, 2 * I, H, self.plan["w_gu"][2])))
@@ -474,9 +525,11 @@ class HybridVerifyRunner:
                 fwd.append(("dflash_gemm_bf16_swiglu",
                             (self.xn.data_ptr(), H, lw["w_gu_pairs"].data_ptr(), H,
                              self.mlp_act.data_ptr(), I, M, 2 * I, H, self.plan["w_gu"][2])))
+            # The next layer's input norm stays a launch: the down projection
+            # (K = intermediate) streams faster split over workgroups than as
+            # one workgroup per 16 columns, by more than the launch costs.
             fwd.append(self._gemm_op(lw, "w_down", self.mlp_act, *dst("w_down", self.r), M))
-        fwd.append(self._residual_op("w_down", self.w.final_norm, M,
-                                     capture_of(cfg.num_hidden_layers - 1)))
+        fwd.append(self._residual_op("w_down", self.w.final_norm, M, capture_of(L - 1)))
         # LM head + greedy accept: draft = block[1:] of each sequence (row stride T)
         tail = (self.tokens.data_ptr() + 4, T, T - 1, self.posterior.data_ptr(),
                 self.matched.data_ptr(), self.bonus.data_ptr(), B, T, self.lm_ws.data_ptr(),

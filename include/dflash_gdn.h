@@ -544,6 +544,52 @@ int dflash_gemm_bf16_swiglu_tiled(const void* x, int64_t x_row_stride,
                                   int k_waves, void* stream);
 
 /*
+ * The decoder layer's residual add and the next RMSNorm folded into the two
+ * projections around them, with no launch of their own (the residual adds
+ * `h = h + r` and norms `input_layernorm` / `post_attention_layernorm` of the
+ * decoder layer, custom_qwen35_model.py:836-846, and the RMSNorm of mlx-lm):
+ *
+ * dflash_gemm_bf16_tiled_residual_norm: the tiled projection r = bf16(x .
+ * w^T) (no K split across workgroups: 16 wavefronts of a workgroup share
+ * each 16-column tile's k-range), then
+ *   h = bf16(resid + r),  h_out = h (h_copy = h too, row stride
+ *   h_copy_row_stride, when not NULL),
+ *   row_sumsq[t, m] = sum of h[m, n]^2 over the tile's columns n in
+ *   [16t, 16t + 16)   (fp32 [N / 16, M]).
+ * resid may alias h_out.  Supported: N % 16 == 0, K % 64 == 0.
+ *
+ * dflash_gemm_bf16_tiled_normed / dflash_gemm_bf16_swiglu_tiled_normed: the
+ * tiled projections (k_waves 4, K <= 16384) whose activation rows are the
+ * RMSNorm output of h over its K columns,
+ *   y = bf16((h[m, k] * inv[m]) * norm_weight[k]),
+ *   inv[m] = 1 / sqrt(sum_t row_sumsq[t, m] / K + eps)
+ * (the row sums of the producing call, norm_tiles = its N / 16, added in a
+ * fixed order that depends on neither M nor the launch), computed on load.
+ * row_inv_out (fp32 [M]) receives inv when not NULL.  Apart from inv's
+ * summation order, y is what dflash_add_rmsnorm computes.
+ */
+int dflash_gemm_bf16_tiled_residual_norm(const void* x, int64_t x_row_stride,
+                                         const void* w_tiled, int M, int N,
+                                         int K, const void* resid, void* h_out,
+                                         void* h_copy, int64_t h_copy_row_stride,
+                                         float* row_sumsq, void* stream);
+int dflash_gemm_bf16_tiled_normed(const void* h, int64_t h_row_stride,
+                                  const void* norm_weight,
+                                  const float* row_sumsq, int norm_tiles,
+                                  float eps, float* row_inv_out,
+                                  const void* w_tiled, void* out,
+                                  int64_t out_row_stride, int M, int N, int K,
+                                  int nsplit, int rows_per_wave, int k_waves,
+                                  void* stream);
+int dflash_gemm_bf16_swiglu_tiled_normed(const void* h, int64_t h_row_stride,
+                                         const void* norm_weight,
+                                         const float* row_sumsq, int norm_tiles,
+                                         float eps, float* row_inv_out,
+                                         const void* w_pairs_tiled, void* out,
+                                         int64_t out_row_stride, int M, int N,
+                                         int K, int k_waves, void* stream);
+
+/*
  * out[m, n] = bf16(sum_s partials[s, m, n]) for partials fp32 [nsplit, M, N]
  * (N % 4 == 0), out bf16 with row stride out_row_stride.
  */

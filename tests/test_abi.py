@@ -44,6 +44,8 @@ def test_header_declares_expected_entry_points():
         "dflash_add_rmsnorm_splitk", "dflash_add_rmsnorm_capture", "dflash_embed_rmsnorm", "dflash_gemm_bf16", "dflash_gemm_splits",
         "dflash_splitk_reduce", "dflash_gemm_bf16_swiglu", "dflash_weight_tile_bytes",
         "dflash_weight_tile_bf16", "dflash_gemm_bf16_tiled", "dflash_gemm_bf16_swiglu_tiled",
+        "dflash_gemm_bf16_tiled_residual_norm",
+        "dflash_gemm_bf16_tiled_normed", "dflash_gemm_bf16_swiglu_tiled_normed",
     ])
 
 
