@@ -23,6 +23,7 @@
 
 #include <type_traits>
 
+#include "argmax_common.h"
 #include "dflash_gdn.h"
 #include "device_common.h"
 #include "gdn_prologue_math.h"
@@ -79,6 +80,15 @@ struct ScanParams {
   const uint16_t* pro_dt_bias;    // [Hv]
   int pro_C, pro_K, pro_Hk;
   float pro_eps, pro_q_scale, pro_k_scale;
+  // Greedy-accept argmax in the same launch: the last acc_blocks workgroups
+  // (after the scan's, so the scan's dispatch and XCD walk are those of a
+  // launch without them; the scan leaves room on every CU for them to run
+  // alongside) each reduce one slice of one logits row to its key
+  // (argmax_common.h).  acc_blocks == 0: no accept.
+  int acc_blocks, acc_rows, acc_splits, acc_chunk, acc_N, acc_V, acc_bf16;
+  const void* acc_logits;
+  int64_t acc_bs, acc_rs;
+  uint64_t* acc_keys;
 };
 
 // Tokens per block the on-the-fly prologue supports (its LDS is sized for it).
@@ -315,12 +325,27 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
   const bool has_q = PRO || p.q != nullptr;
   const bool has_tape = p.tape != nullptr;
 
-  int item_begin = blockIdx.x, item_end = p.items, item_step = gridDim.x;
+  const int bid = blockIdx.x, nblk = gridDim.x - p.acc_blocks;
+  if (bid >= nblk) {  // an accept workgroup (uniform over the workgroup)
+    const int a = bid - nblk;
+    const int row = a / p.acc_splits;
+    const int split = a - row * p.acc_splits;
+    if (p.acc_bf16)
+      argmax_partial_block<uint16_t, true>(static_cast<const uint16_t*>(p.acc_logits), p.acc_bs,
+                                           p.acc_rs, p.acc_N, p.acc_V, p.acc_chunk, p.acc_splits,
+                                           p.acc_keys, row, split);
+    else
+      argmax_partial_block<float, true>(static_cast<const float*>(p.acc_logits), p.acc_bs,
+                                        p.acc_rs, p.acc_N, p.acc_V, p.acc_chunk, p.acc_splits,
+                                        p.acc_keys, row, split);
+    return;
+  }
+  int item_begin = bid, item_end = p.items, item_step = nblk;
   if (p.xcd_items > 0) {
-    const int x = blockIdx.x & 7;
-    item_begin = x * p.xcd_items + (blockIdx.x >> 3);
+    const int x = bid & 7;
+    item_begin = x * p.xcd_items + (bid >> 3);
     item_end = (x + 1) * p.xcd_items;
-    item_step = gridDim.x >> 3;
+    item_step = nblk >> 3;
   }
   for (int item = item_begin; item < item_end; item += item_step) {
     const int rb = item % p.row_blocks;
@@ -519,9 +544,10 @@ hipError_t launch_dk(const ScanParams& base, int R, int grid, int xcd, hipStream
   const bool xcd_ok = blocks % 8 == 0 && p.items % 8 == 0 && blocks < p.items;
   p.xcd_items = (xcd != 0 && xcd_ok) ? p.items / 8 : 0;
   const bool deep = p.items <= scan_cus();
+  const unsigned total = (unsigned)(blocks + p.acc_blocks);  // accept workgroups last
   if constexpr (PRO) {
     if (R != 1) return hipErrorInvalidValue;
-    const dim3 g(blocks), b(256);
+    const dim3 g(total), b(256);
     if (p.pro_K == 4) {  // the Qwen3.5 conv width, taps fixed at compile time
       if (deep) hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 4, true, 4>), g, b, 0, s, p);
       else hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 1, true, 4>), g, b, 0, s, p);
@@ -532,12 +558,12 @@ hipError_t launch_dk(const ScanParams& base, int R, int grid, int xcd, hipStream
     return hipGetLastError();
   }
   switch (R * (deep ? 10 : 1)) {
-    case 1: hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 1>), dim3(blocks), dim3(256), 0, s, p); break;
-    case 2: hipLaunchKernelGGL((gdn_scan_kernel<DK, 2, 1>), dim3(blocks), dim3(256), 0, s, p); break;
-    case 4: hipLaunchKernelGGL((gdn_scan_kernel<DK, 4, 1>), dim3(blocks), dim3(256), 0, s, p); break;
-    case 10: hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 4>), dim3(blocks), dim3(256), 0, s, p); break;
-    case 20: hipLaunchKernelGGL((gdn_scan_kernel<DK, 2, 4>), dim3(blocks), dim3(256), 0, s, p); break;
-    case 40: hipLaunchKernelGGL((gdn_scan_kernel<DK, 4, 4>), dim3(blocks), dim3(256), 0, s, p); break;
+    case 1: hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 1>), dim3(total), dim3(256), 0, s, p); break;
+    case 2: hipLaunchKernelGGL((gdn_scan_kernel<DK, 2, 1>), dim3(total), dim3(256), 0, s, p); break;
+    case 4: hipLaunchKernelGGL((gdn_scan_kernel<DK, 4, 1>), dim3(total), dim3(256), 0, s, p); break;
+    case 10: hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 4>), dim3(total), dim3(256), 0, s, p); break;
+    case 20: hipLaunchKernelGGL((gdn_scan_kernel<DK, 2, 4>), dim3(total), dim3(256), 0, s, p); break;
+    case 40: hipLaunchKernelGGL((gdn_scan_kernel<DK, 4, 4>), dim3(total), dim3(256), 0, s, p); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -584,11 +610,20 @@ struct Select {
   int period;
 };
 
+// The greedy accept's argmax run in the scan's launch (see ScanParams::acc_*).
+struct AcceptArgs {
+  const void* logits;
+  int bf16;  // 0: fp32 logits, 1: bf16
+  int64_t bs, rs;
+  int B, N, V;
+  uint64_t* keys;
+};
+
 int scan_impl(const void* q, const void* k, const void* v, const float* g,
               const float* beta, const float* state_in, void* out,
               float* final_state, float* tape, const int32_t* lengths, int B,
               int T, int Hk, int Hv, int Dk, int Dv, const int64_t* strides,
-              const Select* sel, void* stream) {
+              const Select* sel, void* stream, const AcceptArgs* acc = nullptr) {
   if (B < 0 || T < 0 || Hk <= 0 || Hv <= 0 || Dk <= 0 || Dv <= 0) return DFLASH_ERR_SHAPE;
   if (Hv % Hk != 0) return DFLASH_ERR_SHAPE;
   if (Dv % 16 != 0) return DFLASH_ERR_UNSUPPORTED;
@@ -669,6 +704,20 @@ int scan_impl(const void* q, const void* k, const void* v, const float* g,
   if (((uintptr_t)v & 1) || ((uintptr_t)out & 1) || ((uintptr_t)g & 3) || ((uintptr_t)beta & 3))
     return DFLASH_ERR_ALIGN;
 
+  if (acc != nullptr) {
+    const Split sp = plan_split(acc->B, acc->N, acc->V);
+    p.acc_rows = acc->B * acc->N;
+    p.acc_splits = sp.splits;
+    p.acc_chunk = sp.chunk;
+    p.acc_blocks = p.acc_rows * sp.splits;
+    p.acc_N = acc->N;
+    p.acc_V = acc->V;
+    p.acc_bf16 = acc->bf16;
+    p.acc_logits = acc->logits;
+    p.acc_bs = acc->bs;
+    p.acc_rs = acc->rs;
+    p.acc_keys = acc->keys;
+  }
   const int R = pick_rows(Dv);
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
@@ -786,6 +835,34 @@ extern "C" int dflash_gdn_verify_scan_rollback(
   const dflash::Select sel{prev_tape, prev_accepted, state, prev_T, accepted_period};
   return dflash::scan_impl(q, k, v, g, beta, state, out, final_state, tape, nullptr, B, T, Hk,
                            Hv, Dk, Dv, strides, &sel, stream);
+}
+
+extern "C" int dflash_gdn_verify_scan_rollback_argmax(
+    const void* q, const void* k, const void* v, const float* g, const float* beta,
+    float* state, const float* prev_tape, const int32_t* prev_accepted, int prev_T,
+    int accepted_period, void* out, float* final_state, float* tape, int B, int T, int Hk,
+    int Hv, int Dk, int Dv, const int64_t* strides, const void* logits, int logits_dtype,
+    int64_t logits_batch_stride, int64_t logits_row_stride, int accept_B, int N, int V,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace dflash;
+  if (state == nullptr) return DFLASH_ERR_NULL;
+  if (final_state != nullptr && final_state == state) return DFLASH_ERR_SHAPE;
+  if (accept_B <= 0 || N <= 0 || V <= 0 || (int64_t)accept_B * N > 16384) return DFLASH_ERR_SHAPE;
+  if (B <= 0 || T <= 0) return DFLASH_ERR_SHAPE;  // the launch has scan work
+  if (logits == nullptr || workspace == nullptr) return DFLASH_ERR_NULL;
+  if (logits_dtype != DFLASH_DTYPE_F32 && logits_dtype != DFLASH_DTYPE_BF16)
+    return DFLASH_ERR_UNSUPPORTED;
+  if (workspace_bytes < dflash_greedy_accept_workspace_bytes(accept_B, N, V)) return DFLASH_ERR_WORKSPACE;
+  // the vector path of the argmax: 16-byte aligned rows
+  const int per = logits_dtype == DFLASH_DTYPE_F32 ? 4 : 8;
+  if (((uintptr_t)logits & 15) || (logits_batch_stride % per) || (logits_row_stride % per) ||
+      ((uintptr_t)workspace & 7))
+    return DFLASH_ERR_ALIGN;
+  const AcceptArgs acc{logits, logits_dtype == DFLASH_DTYPE_BF16 ? 1 : 0, logits_batch_stride,
+                       logits_row_stride, accept_B, N, V, static_cast<uint64_t*>(workspace)};
+  const Select sel{prev_tape, prev_accepted, state, prev_T, accepted_period};
+  return scan_impl(q, k, v, g, beta, state, out, final_state, tape, nullptr, B, T, Hk, Hv, Dk, Dv,
+                   strides, &sel, stream, &acc);
 }
 
 extern "C" int dflash_gdn_replay(const void* k, const void* v, const float* g,

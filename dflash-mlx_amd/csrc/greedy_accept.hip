@@ -7,9 +7,7 @@
 //
 // Two launches, HBM-bound on the logits read:
 //   1. argmax_partial: grid (B*N rows, splits).  Each workgroup reduces one
-//      contiguous slice of one logits row to a 64-bit key
-//      (order-preserving value bits << 32 | ~index), so an integer max gives
-//      the largest value and, among equal values, the lowest index.
+//      contiguous slice of one logits row to a 64-bit key (argmax_common.h).
 //   2. accept_finalize: one workgroup per sequence, one wavefront per logits
 //      row, merges the split keys of all rows at once, writes the posterior
 //      tokens, then finds the first draft mismatch with a 64-lane ballot.
@@ -23,6 +21,7 @@
 #include <mutex>
 
 #include "accept_common.h"
+#include "argmax_common.h"
 #include "conv_window.h"
 #include "dflash_gdn.h"
 #include "device_common.h"
@@ -31,121 +30,14 @@
 namespace dflash {
 namespace {
 
-constexpr int kArgmaxThreads = 256;
 constexpr int kMaxAcceptRows = 16384;
-
-template <typename T>
-__device__ __forceinline__ float load_logit(const T* p);
-template <>
-__device__ __forceinline__ float load_logit<float>(const float* p) { return *p; }
-template <>
-__device__ __forceinline__ float load_logit<uint16_t>(const uint16_t* p) {
-  return bf16_bits_to_f32(*p);
-}
-struct F16Tag { uint16_t bits; };
-template <>
-__device__ __forceinline__ float load_logit<F16Tag>(const F16Tag* p) {
-  return f16_bits_to_f32(p->bits);
-}
-
-// Keys of 16 bytes holding 16/sizeof(T) consecutive logits starting at idx.
-template <typename T>
-__device__ __forceinline__ uint64_t key16(u32x4 raw, int idx, uint64_t best);
-template <>
-__device__ __forceinline__ uint64_t key16<float>(u32x4 raw, int idx, uint64_t best) {
-  best = u64_max(best, argmax_key(__uint_as_float(raw.x), idx + 0));
-  best = u64_max(best, argmax_key(__uint_as_float(raw.y), idx + 1));
-  best = u64_max(best, argmax_key(__uint_as_float(raw.z), idx + 2));
-  best = u64_max(best, argmax_key(__uint_as_float(raw.w), idx + 3));
-  return best;
-}
-template <>
-__device__ __forceinline__ uint64_t key16<uint16_t>(u32x4 raw, int idx, uint64_t best) {
-  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    best = u64_max(best, argmax_key(bf16_lo(w[j]), idx + 2 * j));
-    best = u64_max(best, argmax_key(bf16_hi(w[j]), idx + 2 * j + 1));
-  }
-  return best;
-}
-template <>
-__device__ __forceinline__ uint64_t key16<F16Tag>(u32x4 raw, int idx, uint64_t best) {
-  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    best = u64_max(best, argmax_key(f16_bits_to_f32((uint16_t)(w[j] & 0xffffu)), idx + 2 * j));
-    best = u64_max(best, argmax_key(f16_bits_to_f32((uint16_t)(w[j] >> 16)), idx + 2 * j + 1));
-  }
-  return best;
-}
 
 template <typename T, bool VECTOR>
 __global__ __launch_bounds__(kArgmaxThreads) void argmax_partial_kernel(
     const T* __restrict__ logits, int64_t bstride, int64_t rstride, int N, int V, int chunk,
     int splits, uint64_t* __restrict__ keys) {
-  const int row = blockIdx.x;
-  const int split = blockIdx.y;
-  const int b = row / N;
-  const int i = row - b * N;
-  const T* base = logits + (int64_t)b * bstride + (int64_t)i * rstride;
-  const int start = split * chunk;
-  const int end = min(V, start + chunk);
-  uint64_t best = 0;
-  if (VECTOR) {
-    constexpr int PER = 16 / sizeof(T);
-    const int nvec = (end - start) / PER;
-    const u32x4* vbase = reinterpret_cast<const u32x4*>(base + start);
-    int j = threadIdx.x;
-    // Four independent 16-byte loads in flight per lane.
-    for (; j + 3 * kArgmaxThreads < nvec; j += 4 * kArgmaxThreads) {
-      const u32x4 r0 = __builtin_nontemporal_load(vbase + j);
-      const u32x4 r1 = __builtin_nontemporal_load(vbase + j + kArgmaxThreads);
-      const u32x4 r2 = __builtin_nontemporal_load(vbase + j + 2 * kArgmaxThreads);
-      const u32x4 r3 = __builtin_nontemporal_load(vbase + j + 3 * kArgmaxThreads);
-      best = key16<T>(r0, start + j * PER, best);
-      best = key16<T>(r1, start + (j + kArgmaxThreads) * PER, best);
-      best = key16<T>(r2, start + (j + 2 * kArgmaxThreads) * PER, best);
-      best = key16<T>(r3, start + (j + 3 * kArgmaxThreads) * PER, best);
-    }
-    for (; j < nvec; j += kArgmaxThreads) best = key16<T>(vbase[j], start + j * PER, best);
-    for (int idx = start + nvec * PER + threadIdx.x; idx < end; idx += kArgmaxThreads)
-      best = u64_max(best, argmax_key(load_logit<T>(base + idx), idx));
-  } else {
-    for (int idx = start + threadIdx.x; idx < end; idx += kArgmaxThreads)
-      best = u64_max(best, argmax_key(load_logit<T>(base + idx), idx));
-  }
-  best = wave_max_u64(best);
-  __shared__ uint64_t wbest[kArgmaxThreads / 64];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  if (lane == 0) wbest[wave] = best;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint64_t m = wbest[0];
-#pragma unroll
-    for (int w = 1; w < kArgmaxThreads / 64; ++w) m = u64_max(m, wbest[w]);
-    keys[(int64_t)row * splits + split] = m;
-  }
-}
-
-struct Split {
-  int splits;
-  int chunk;
-};
-
-// Deterministic split of one vocabulary row; the workspace size depends on it.
-Split plan_split(int B, int N, int V) {
-  const int64_t rows = (int64_t)B * N;
-  int64_t splits = ceil_div(2048, rows > 0 ? rows : 1);
-  const int64_t max_by_len = ceil_div(V, 2048);
-  if (splits > max_by_len) splits = max_by_len;
-  if (splits < 1) splits = 1;
-  if (splits > 1024) splits = 1024;
-  int64_t chunk = ceil_div(V, splits);
-  chunk = ceil_div(chunk, 16) * 16;  // keeps 16-byte alignment of each slice
-  splits = ceil_div(V, chunk);
-  return Split{(int)splits, (int)chunk};
+  argmax_partial_block<T, VECTOR>(logits, bstride, rstride, N, V, chunk, splits, keys, blockIdx.x,
+                                  blockIdx.y);
 }
 
 template <typename T>
@@ -278,24 +170,27 @@ extern "C" int dflash_greedy_accept(const void* logits, int logits_dtype,
                                           posterior, matched, bonus, s));
 }
 
-extern "C" int dflash_greedy_accept_conv_rollback(
+namespace dflash {
+namespace {
+// dflash_greedy_accept_conv_rollback; with logits == nullptr the argmax keys
+// are already in the workspace (dflash_accept_keys_conv_rollback).
+int accept_conv_rollback(
     const void* logits, int logits_dtype, int64_t logits_batch_stride,
     int64_t logits_row_stride, const int32_t* draft, int64_t draft_stride, int n_draft,
     int32_t* posterior, int32_t* matched, int32_t* bonus, int B, int N, int V, void* workspace,
     size_t workspace_bytes, const void* const* conv_in, const void* const* qkv,
     void* const* conv_out, int accepted_offset, int32_t* accepted_out, int L, int T, int K1,
-    int64_t C,
-    int64_t qkv_batch_stride, int64_t qkv_row_stride, int elem_bytes, void* stream) {
-  using namespace dflash;
+    int64_t C, int64_t qkv_batch_stride, int64_t qkv_row_stride, int elem_bytes, void* stream,
+    bool run_argmax) {
   if (B < 0 || N <= 0 || V <= 0 || n_draft < 0) return DFLASH_ERR_SHAPE;
   if (N > kMaxAcceptRows || (int64_t)B * N > INT32_MAX) return DFLASH_ERR_SHAPE;
   if (L < 0 || T < 0 || K1 < 0 || C < 0 || B > 65535) return DFLASH_ERR_SHAPE;
   if (K1 > kMaxConvRows) return DFLASH_ERR_UNSUPPORTED;
   if (elem_bytes != 2 && elem_bytes != 4) return DFLASH_ERR_UNSUPPORTED;
   if (B == 0) return DFLASH_OK;
-  if (logits == nullptr || workspace == nullptr) return DFLASH_ERR_NULL;
+  if ((run_argmax && logits == nullptr) || workspace == nullptr) return DFLASH_ERR_NULL;
   if (n_draft > 0 && draft == nullptr) return DFLASH_ERR_NULL;
-  if (logits_dtype != DFLASH_DTYPE_F32 && logits_dtype != DFLASH_DTYPE_BF16 &&
+  if (run_argmax && logits_dtype != DFLASH_DTYPE_F32 && logits_dtype != DFLASH_DTYPE_BF16 &&
       logits_dtype != DFLASH_DTYPE_F16)
     return DFLASH_ERR_UNSUPPORTED;
   if (workspace_bytes < dflash_greedy_accept_workspace_bytes(B, N, V)) return DFLASH_ERR_WORKSPACE;
@@ -311,8 +206,10 @@ extern "C" int dflash_greedy_accept_conv_rollback(
   const Split sp = plan_split(B, N, V);
   uint64_t* keys = static_cast<uint64_t*>(workspace);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  hipError_t e;
-  if (logits_dtype == DFLASH_DTYPE_F32)
+  hipError_t e = hipSuccess;
+  if (!run_argmax)
+    ;
+  else if (logits_dtype == DFLASH_DTYPE_F32)
     e = launch_partial<float>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, keys, s);
   else if (logits_dtype == DFLASH_DTYPE_BF16)
     e = launch_partial<uint16_t>(logits, logits_batch_stride, logits_row_stride, B, N, V, sp, keys, s);
@@ -349,6 +246,35 @@ extern "C" int dflash_greedy_accept_conv_rollback(
     if (e != hipSuccess) return (int)e;
   }
   return DFLASH_OK;
+}
+}  // namespace
+}  // namespace dflash
+
+extern "C" int dflash_greedy_accept_conv_rollback(
+    const void* logits, int logits_dtype, int64_t logits_batch_stride,
+    int64_t logits_row_stride, const int32_t* draft, int64_t draft_stride, int n_draft,
+    int32_t* posterior, int32_t* matched, int32_t* bonus, int B, int N, int V, void* workspace,
+    size_t workspace_bytes, const void* const* conv_in, const void* const* qkv,
+    void* const* conv_out, int accepted_offset, int32_t* accepted_out, int L, int T, int K1,
+    int64_t C, int64_t qkv_batch_stride, int64_t qkv_row_stride, int elem_bytes, void* stream) {
+  return dflash::accept_conv_rollback(
+      logits, logits_dtype, logits_batch_stride, logits_row_stride, draft, draft_stride, n_draft,
+      posterior, matched, bonus, B, N, V, workspace, workspace_bytes, conv_in, qkv, conv_out,
+      accepted_offset, accepted_out, L, T, K1, C, qkv_batch_stride, qkv_row_stride, elem_bytes,
+      stream, true);
+}
+
+extern "C" int dflash_accept_keys_conv_rollback(
+    const int32_t* draft, int64_t draft_stride, int n_draft, int32_t* posterior, int32_t* matched,
+    int32_t* bonus, int B, int N, int V, const void* workspace, size_t workspace_bytes,
+    const void* const* conv_in, const void* const* qkv, void* const* conv_out,
+    int accepted_offset, int32_t* accepted_out, int L, int T, int K1, int64_t C,
+    int64_t qkv_batch_stride, int64_t qkv_row_stride, int elem_bytes, void* stream) {
+  return dflash::accept_conv_rollback(
+      nullptr, DFLASH_DTYPE_F32, 0, 0, draft, draft_stride, n_draft, posterior, matched, bonus, B,
+      N, V, const_cast<void*>(workspace), workspace_bytes, conv_in, qkv, conv_out,
+      accepted_offset, accepted_out, L, T, K1, C, qkv_batch_stride, qkv_row_stride, elem_bytes,
+      stream, false);
 }
 
 // ------------------------------------------------ allocation-free variant

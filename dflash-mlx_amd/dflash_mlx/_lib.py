@@ -38,6 +38,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I,
          _VP, _VP],
     ),
+    "dflash_gdn_verify_scan_rollback_argmax": (
+        _I,
+        [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I,
+         _VP, _VP, _I, _I64, _I64, _I, _I, _I, _VP, _SZ, _VP],
+    ),
     "dflash_gdn_replay": (
         _I,
         [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP, _VP],
@@ -115,6 +120,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_VP, _I, _I64, _I64, _VP, _I64, _I, _VP, _VP, _VP, _I, _I, _I, _VP, _SZ,  # accept
          _VP, _VP, _VP, _I, _VP, _I, _I, _I, _I64, _I64, _I64, _I, _VP],  # conv rollback
+    ),
+    "dflash_accept_keys_conv_rollback": (
+        _I,
+        [_VP, _I64, _I, _VP, _VP, _VP, _I, _I, _I, _VP, _SZ,
+         _VP, _VP, _VP, _I, _VP, _I, _I, _I, _I64, _I64, _I64, _I, _VP],
     ),
     "dflash_tape_select": (_I, [_VP, _VP, _VP, _VP, _I, _I, _I, _I64, _I64, _VP]),
     "dflash_conv_rollback": (

@@ -6,7 +6,8 @@ allocation), in the order of the reference's verify_block_parallel_replay
 (dflash_mlx/runtime.py:117-163) with the rollback moved onto the device:
 
   1. gated-delta scan of all linear layers' inputs, writing out, the final
-     state and the per-token state tape       (dflash_gdn_verify_scan)
+     state and the per-token state tape       (dflash_gdn_verify_scan; in the
+     fused form the accept's argmax runs in the same launch)
   2. greedy accept on the verify logits       (dflash_greedy_accept): the
      block's drafts block[1:] against the posterior rows 0..T-2, bonus =
      posterior[matched] (runtime.py:145-147), then keep = matched + 1
@@ -145,8 +146,19 @@ class VerifyStepRunner:
             self._accept_conv_args = self._accept_args + (
                 cins, qkvs, couts, 1, self.keep.data_ptr(), s.L, s.T, s.K1, s.conv_dim,
                 s.T * s.conv_dim, s.conv_dim, 2)
+            # the same with the argmax already run by the scan's launch
+            self._scan_rb_argmax_args = self._scan_rb_args + (
+                self.logits.data_ptr(), _lib.DFLASH_DTYPE_F32, s.T * s.V, s.V, s.B, s.T, s.V,
+                self.workspace.data_ptr(), self.workspace.numel())
+            self._keys_conv_args = (
+                self.block.data_ptr() + 4, s.T, s.T - 1, self.posterior.data_ptr(),
+                self.matched.data_ptr(), self.bonus.data_ptr(), s.B, s.T, s.V,
+                self.workspace.data_ptr(), self.workspace.numel(), cins, qkvs, couts, 1,
+                self.keep.data_ptr(), s.L, s.T, s.K1, s.conv_dim, s.T * s.conv_dim, s.conv_dim, 2)
         lib = _lib.load()
         self._accept_conv = lib.dflash_greedy_accept_conv_rollback
+        self._scan_rb_argmax = lib.dflash_gdn_verify_scan_rollback_argmax
+        self._keys_conv = lib.dflash_accept_keys_conv_rollback
         self._scan = lib.dflash_gdn_verify_scan
         self._scan_rb = lib.dflash_gdn_verify_scan_rollback
         self._accept = lib.dflash_greedy_accept
@@ -190,6 +202,18 @@ class VerifyStepRunner:
         _lib.check("dflash_greedy_accept_conv_rollback",
                    self._accept_conv(*self._accept_conv_args, st))
 
+    def scan_rolled_argmax(self, stream: int | None = None) -> None:
+        """scan_rolled() with the accept's argmax (per-slice keys of the
+        verify logits) run by extra workgroups of the same launch."""
+        _lib.check("dflash_gdn_verify_scan_rollback_argmax",
+                   self._scan_rb_argmax(*self._scan_rb_argmax_args, stream or self._stream()))
+
+    def accept_keys_conv_rollback(self, stream: int | None = None) -> None:
+        """The accept's finalize inside the conv-window rollback, from the keys
+        scan_rolled_argmax() left in the workspace (one launch)."""
+        _lib.check("dflash_accept_keys_conv_rollback",
+                   self._keys_conv(*self._keys_conv_args, stream or self._stream()))
+
     def run(self) -> None:
         """Explicit form: scan (with final state) -> accept -> gather rollback."""
         st = self._stream()
@@ -203,10 +227,15 @@ class VerifyStepRunner:
         the call, the state after keeping keep[b] = matched[b] + 1 tokens of
         this block is tape[keep[b]-1, b], which the next run_fused() picks up
         on the device.  Start with keep zeroed (the first scan then starts
-        from state)."""
+        from state).  With conv windows: two launches (the scan with the
+        accept's argmax, then the finalize inside the window copy)."""
         st = self._stream()
-        self.scan_rolled(st)
-        self.accept_conv_rollback(st)
+        if self.shape.conv_dim:
+            self.scan_rolled_argmax(st)
+            self.accept_keys_conv_rollback(st)
+        else:
+            self.scan_rolled(st)
+            self.accept_conv_rollback(st)
 
     def rolled_back_state(self) -> torch.Tensor:
         """Materialise the state the next fused step starts from (test helper;

@@ -130,6 +130,28 @@ int dflash_gdn_verify_scan_rollback(const void* q, const void* k, const void* v,
                                     const int64_t* strides, void* stream);
 
 /*
+ * dflash_gdn_verify_scan_rollback with the argmax phase of the greedy accept
+ * (dflash_greedy_accept's first launch: per-slice argmax keys of the verify
+ * logits into `workspace`) run by extra workgroups of the same launch,
+ * dispatched after the scan's; the keys are then merged by
+ * dflash_accept_keys_conv_rollback.  The verify step's scan and the accept
+ * read disjoint inputs, so sharing the launch changes nothing but the launch
+ * count (the reference's verify_block_parallel_replay runs them in order,
+ * dflash_mlx/runtime.py:117-147).  Scan arguments as
+ * dflash_gdn_verify_scan_rollback (B, T > 0); logits fp32 or bf16 [accept_B,
+ * N, V] with 16-byte aligned rows (strides in elements); workspace as for
+ * dflash_greedy_accept(accept_B, N, V).
+ */
+int dflash_gdn_verify_scan_rollback_argmax(
+    const void* q, const void* k, const void* v, const float* g,
+    const float* beta, float* state, const float* prev_tape,
+    const int32_t* prev_accepted, int prev_T, int accepted_period, void* out,
+    float* final_state, float* tape, int B, int T, int Hk, int Hv, int Dk,
+    int Dv, const int64_t* strides, const void* logits, int logits_dtype,
+    int64_t logits_batch_stride, int64_t logits_row_stride, int accept_B,
+    int N, int V, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * State-only replay of the first n_b tokens: the same recurrence without q,
  * out or tape.  Replaces advance_gated_delta_states(initial_states, keys,
  * values, g, beta) (dflash_mlx/custom_qwen35_model.py:97-139, duplicate at
@@ -416,6 +438,21 @@ int dflash_greedy_accept_conv_rollback(
     int N, int V, void* workspace, size_t workspace_bytes,
     const void* const* conv_in, const void* const* qkv, void* const* conv_out,
     int accepted_offset, int32_t* accepted_out, int L, int T, int K1, int64_t C,
+    int64_t qkv_batch_stride, int64_t qkv_row_stride, int elem_bytes,
+    void* stream);
+
+/*
+ * The second launch of dflash_greedy_accept_conv_rollback alone: the same
+ * finalize + conv-window rollback from argmax keys already in `workspace`
+ * (written by dflash_gdn_verify_scan_rollback_argmax for the same B, N, V).
+ * Arguments and outputs as dflash_greedy_accept_conv_rollback, the same bits.
+ */
+int dflash_accept_keys_conv_rollback(
+    const int32_t* draft, int64_t draft_stride, int n_draft, int32_t* posterior,
+    int32_t* matched, int32_t* bonus, int B, int N, int V,
+    const void* workspace, size_t workspace_bytes, const void* const* conv_in,
+    const void* const* qkv, void* const* conv_out, int accepted_offset,
+    int32_t* accepted_out, int L, int T, int K1, int64_t C,
     int64_t qkv_batch_stride, int64_t qkv_row_stride, int elem_bytes,
     void* stream);
 

@@ -37,7 +37,8 @@ def test_header_declares_expected_entry_points():
         "dflash_conv_rollback", "dflash_lm_head_accept_workspace_bytes",
         "dflash_lm_head_greedy_accept", "dflash_gdn_prologue", "dflash_gdn_gated_rmsnorm",
         "dflash_gdn_prologue_scan_rollback", "dflash_lm_head_greedy_accept_tiled",
-        "dflash_greedy_accept_conv_rollback",
+        "dflash_greedy_accept_conv_rollback", "dflash_gdn_verify_scan_rollback_argmax",
+        "dflash_accept_keys_conv_rollback",
         "dflash_gdn_chunked_prefill_workspace_bytes", "dflash_gdn_chunked_prefill",
         "dflash_add_rmsnorm", "dflash_swiglu", "dflash_attn_prep",
         "dflash_attn_verify_workspace_bytes", "dflash_attn_verify", "dflash_commit_accept",

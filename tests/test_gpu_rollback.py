@@ -315,3 +315,79 @@ def test_accept_conv_rollback_matches_two_calls(device, B, N, V, L, K1, C, offse
     assert torch.equal(post_a, post_b) and torch.equal(m_a, m_b) and torch.equal(b_a, b_b)
     for l in range(L):
         assert torch.equal(conv_a[l], cout[l]), f"layer {l}"
+
+
+@pytest.mark.parametrize("B,Hk,Hv,D,V,dtype", [
+    (1, 4, 4, 64, 1024, torch.float32),     # c0 shapes
+    (3, 16, 32, 128, 5000, torch.bfloat16),  # batched, GQA, bf16 logits
+])
+def test_scan_with_argmax_matches_separate_launches(device, B, Hk, Hv, D, V, dtype):
+    """dflash_gdn_verify_scan_rollback_argmax + dflash_accept_keys_conv_rollback
+    (the accept's argmax in the scan's launch) against
+    dflash_gdn_verify_scan_rollback + dflash_greedy_accept_conv_rollback over
+    two chained steps (the second starts from the first one's keep): out,
+    tape, state, posterior, matched, bonus, keep and every conv window
+    bit-identical."""
+    from dflash_mlx import _lib
+
+    T, L, K1, C = 16, 2, 3, 96
+    print(f"[scan+argmax B={B} Hk={Hk} Hv={Hv} D={D} V={V} {dtype}]", flush=True)
+    gen = torch.Generator().manual_seed(B * 7 + V)
+    lib = _lib.load()
+    st = _lib.stream_handle(device)
+    steps = []
+    for _ in range(2):
+        q = torch.randn(B, T, Hk, D, generator=gen).bfloat16()
+        k = torch.nn.functional.normalize(torch.randn(B, T, Hk, D, generator=gen), dim=-1).bfloat16()
+        v = torch.randn(B, T, Hv, D, generator=gen).bfloat16()
+        g = torch.sigmoid(torch.randn(B, T, Hv, generator=gen)) * 0.5 + 0.5
+        beta = torch.sigmoid(torch.randn(B, T, Hv, generator=gen))
+        logits = torch.randn(B, T, V, generator=gen).to(dtype)
+        am = logits.float().argmax(-1).to(torch.int32)
+        acc = torch.randint(0, T + 1, (B,), generator=gen, dtype=torch.int32)
+        pos = torch.arange(T, dtype=torch.int32)[None, :]
+        draft = torch.where(pos < acc[:, None], am, (am + 1) % V)
+        block = torch.zeros(B, T, dtype=torch.int32)
+        block[:, 1:] = draft[:, :-1]
+        qkv = [torch.randn(B, T, C, generator=gen).bfloat16() for _ in range(L)]
+        steps.append([t.to(device) for t in (q, k, v, g, beta, logits, block)] +
+                     [[x.to(device) for x in qkv]])
+    state0 = (0.05 * torch.randn(B, Hv, D, D, generator=gen)).to(device)
+    conv0 = [torch.randn(B, K1, C, generator=gen).bfloat16().to(device) for _ in range(L)]
+    results = []
+    for joint in (True, False):
+        state = state0.clone()
+        tape = torch.zeros(T, B, Hv, D, D, device=device)
+        keep = torch.zeros(B, dtype=torch.int32, device=device)
+        conv = [c.clone() for c in conv0]
+        ws = torch.empty(int(lib.dflash_greedy_accept_workspace_bytes(B, T, V)), dtype=torch.uint8,
+                         device=device)
+        got = []
+        for q, k, v, g, beta, logits, block, qkv in steps:
+            out = torch.empty(B, T, Hv, D, device=device).bfloat16()
+            post = torch.full((B, T), -7, dtype=torch.int32, device=device)
+            matched = torch.full((B,), -7, dtype=torch.int32, device=device)
+            bonus = torch.full((B,), -7, dtype=torch.int32, device=device)
+            scan = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+                    state.data_ptr(), tape.data_ptr(), keep.data_ptr(), T, B, out.data_ptr(), None,
+                    tape.data_ptr(), B, T, Hk, Hv, D, D, None)
+            cv = (_lib.ptr_array(conv), _lib.ptr_array(qkv), _lib.ptr_array(conv), 1,
+                  keep.data_ptr(), L, T, K1, C, T * C, C, 2)
+            if joint:
+                _lib.call("dflash_gdn_verify_scan_rollback_argmax", *scan, logits.data_ptr(),
+                          _lib.dtype_tag(dtype), T * V, V, B, T, V, ws.data_ptr(), ws.numel(), st)
+                _lib.call("dflash_accept_keys_conv_rollback", block.data_ptr() + 4, T, T - 1,
+                          post.data_ptr(), matched.data_ptr(), bonus.data_ptr(), B, T, V,
+                          ws.data_ptr(), ws.numel(), *cv, st)
+            else:
+                _lib.call("dflash_gdn_verify_scan_rollback", *scan, st)
+                _lib.call("dflash_greedy_accept_conv_rollback", logits.data_ptr(),
+                          _lib.dtype_tag(dtype), T * V, V, block.data_ptr() + 4, T, T - 1,
+                          post.data_ptr(), matched.data_ptr(), bonus.data_ptr(), B, T, V,
+                          ws.data_ptr(), ws.numel(), *cv, st)
+            torch.cuda.synchronize()
+            got += [out.clone(), tape.clone(), state.clone(), post.clone(), matched.clone(),
+                    bonus.clone(), keep.clone()] + [c.clone() for c in conv]
+        results.append(got)
+    for a, b in zip(*results):
+        assert torch.equal(a, b)
