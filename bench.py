@@ -89,7 +89,10 @@ def probe(torch, fused, explicit) -> int:
     for _ in range(3):
         explicit.scan()
     for _ in range(3):
-        fused.scan_rolled_argmax()
+        if fused.argmax_in_scan:
+            fused.scan_rolled_argmax()
+        else:
+            fused.scan_rolled()
     for _ in range(3):
         dst.copy_(src)
     torch.cuda.synchronize()
@@ -598,8 +601,16 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
 
     K = steps
     print(f"[bench] {cfg.name}: timing {K} fused + {K} explicit steps", file=sys.stderr, flush=True)
-    tf = time_steps(torch, K, [("scan_argmax", fused.scan_rolled_argmax),
-                               ("accept_rollback", fused.accept_keys_conv_rollback)])
+    # The phases of run_fused(): with small logits the accept's argmax runs in
+    # the scan's launch, otherwise in a launch of its own after it.
+    in_scan = fused.argmax_in_scan
+    lead = "scan_argmax" if in_scan else "scan"
+    if in_scan:
+        tf = time_steps(torch, K, [(lead, fused.scan_rolled_argmax),
+                                   ("accept_rollback", fused.accept_keys_conv_rollback)])
+    else:
+        tf = time_steps(torch, K, [(lead, fused.scan_rolled),
+                                   ("accept_rollback", fused.accept_conv_rollback)])
     te = time_steps(torch, K, [("scan", explicit.scan), ("accept", explicit.accept),
                                ("rollback", explicit.rollback)])
     # The same fused step as the device-driven serving loop launches it: captured
@@ -642,21 +653,22 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
     gather_bytes = 2 * S_bytes * L * B
     tokens = B * T
 
-    # The dominant launch: the scan + tape with the accept's argmax workgroups
-    # (which read the verify logits once).
-    launch_bytes = scan_fused_bytes + accept_bytes
-    achieved = launch_bytes / (tf["scan_argmax"] / 1e6) / 1e9
+    # The dominant launch: the scan + tape, with the accept's argmax workgroups
+    # (which read the verify logits once) when they share its launch.
+    launch_bytes = scan_fused_bytes + (accept_bytes if in_scan else 0)
+    achieved = launch_bytes / (tf[lead] / 1e6) / 1e9
     roof = {
         "bound": "hbm",
-        "kernel": "gdn_scan_kernel<DK,R> + accept argmax workgroups via "
-                  "dflash_gdn_verify_scan_rollback_argmax",
+        "kernel": ("gdn_scan_kernel<DK,R> + accept argmax workgroups via "
+                   "dflash_gdn_verify_scan_rollback_argmax") if in_scan else
+                  "gdn_scan_kernel<DK,R> via dflash_gdn_verify_scan_rollback",
         "achieved": round(achieved, 1),
         "peak": PEAK_HBM_GBPS,
         "unit": "GB/s",
         "frac": round(achieved / PEAK_HBM_GBPS, 4),
         "traffic": traffic_from_profiles(cfg.name),
         "bytes_alg_per_launch": launch_bytes,
-        "avg_launch_us": round(tf["scan_argmax"], 2),
+        "avg_launch_us": round(tf[lead], 2),
     }
     r2 = lambda d: {k: round(v, 2) for k, v in d.items() if k != "ms_per_step"}
     expl_scan_gbps = scan_expl_bytes / (te["scan"] / 1e6) / 1e9
@@ -671,10 +683,14 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
             "io": "bf16 q/k/v/out, fp32 g/beta/state/tape, fp32 logits",
             "accept": "drafts block[1:] vs posterior rows 0..T-2, bonus = posterior[matched], "
                       "keep = matched + 1 (runtime.py:145-147)",
-            "step": "fused: scan+tape with the previous step's state rollback in its load, "
-                    "with the greedy accept's argmax slices in the same launch -> the accept's "
-                    "finalize inside the conv-window rollback copy, which also writes keep "
-                    "(2 launches), replayed as one HIP graph",
+            "step": ("fused: scan+tape with the previous step's state rollback in its load, "
+                     "with the greedy accept's argmax slices in the same launch -> the accept's "
+                     "finalize inside the conv-window rollback copy, which also writes keep "
+                     "(2 launches), replayed as one HIP graph") if in_scan else
+                    ("fused: scan+tape with the previous step's state rollback in its load -> "
+                     "the greedy accept's argmax slices -> its finalize inside the conv-window "
+                     "rollback copy, which also writes keep (3 launches; logits above "
+                     "ARGMAX_IN_SCAN_MAX_BYTES), replayed as one HIP graph"),
         },
         "roofline": roof,
         "graph_step_us": round(tg["gpu_step"], 2),

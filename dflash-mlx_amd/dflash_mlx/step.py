@@ -7,7 +7,8 @@ allocation), in the order of the reference's verify_block_parallel_replay
 
   1. gated-delta scan of all linear layers' inputs, writing out, the final
      state and the per-token state tape       (dflash_gdn_verify_scan; in the
-     fused form the accept's argmax runs in the same launch)
+     fused form with small logits the accept's argmax runs in the same
+     launch)
   2. greedy accept on the verify logits       (dflash_greedy_accept): the
      block's drafts block[1:] against the posterior rows 0..T-2, bonus =
      posterior[matched] (runtime.py:145-147), then keep = matched + 1
@@ -28,6 +29,15 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
+
+
+# The fused step runs the accept's argmax as extra workgroups of the scan's
+# launch while the verify logits are at most this many bytes: there a launch
+# of its own would be bound by the ~5 us launch floor rather than by reading
+# the logits (32 MiB at HBM speed), and the extra workgroups hide it.  Larger
+# logits get their own launch after the scan: workgroups sharing CUs with the
+# scan's stretch its per-token chain by more than that launch costs.
+ARGMAX_IN_SCAN_MAX_BYTES = 32 << 20
 
 
 @dataclass(frozen=True)
@@ -51,6 +61,11 @@ class StepShape:
 
     def accept_bytes(self, logit_bytes: int = 4) -> int:
         return logit_bytes * self.B * self.T * self.V + 4 * self.B * self.T
+
+    def fuse_argmax(self) -> bool:
+        """Whether the fused step runs the accept's argmax inside the scan's
+        launch (conv windows present and logits within ARGMAX_IN_SCAN_MAX_BYTES)."""
+        return bool(self.conv_dim) and 4 * self.B * self.T * self.V <= ARGMAX_IN_SCAN_MAX_BYTES
 
     def rollback_bytes(self) -> int:
         """Upper bound (every sequence accepts >= 1 token): state read + write,
@@ -92,6 +107,7 @@ class VerifyStepRunner:
         self.matched = torch.zeros(s.B, dtype=i32, device=device)
         self.keep = torch.zeros(s.B, dtype=i32, device=device)  # accepted_inputs = matched + 1
         self.bonus = z(s.B, dt=i32)
+        self.argmax_in_scan = s.fuse_argmax()
         lib = _lib.load()
         ws = int(lib.dflash_greedy_accept_workspace_bytes(s.B, s.T, s.V))
         self.workspace = z(max(ws, 8), dt=torch.uint8)
@@ -227,10 +243,11 @@ class VerifyStepRunner:
         the call, the state after keeping keep[b] = matched[b] + 1 tokens of
         this block is tape[keep[b]-1, b], which the next run_fused() picks up
         on the device.  Start with keep zeroed (the first scan then starts
-        from state).  With conv windows: two launches (the scan with the
-        accept's argmax, then the finalize inside the window copy)."""
+        from state).  With conv windows and small logits
+        (``argmax_in_scan``): two launches, the scan with the accept's argmax,
+        then the finalize inside the window copy; otherwise three."""
         st = self._stream()
-        if self.shape.conv_dim:
+        if self.argmax_in_scan:
             self.scan_rolled_argmax(st)
             self.accept_keys_conv_rollback(st)
         else:

@@ -70,7 +70,8 @@ def test_layer_verify_and_accept_graph_replays(device):
     assert int(outs[5][0]) == 9
 
 
-def test_fused_step_runner_graph_replays(device):
+@pytest.mark.parametrize("argmax_in_scan", [True, False])
+def test_fused_step_runner_graph_replays(device, argmax_in_scan):
     cfg = ScanConfig(**{**CONFIGS[2].__dict__, "B": 2, "V": 3000})
     x = make_scan_inputs(cfg)
     acc = make_accept_inputs(cfg, gen=x["_gen"])
@@ -78,6 +79,7 @@ def test_fused_step_runner_graph_replays(device):
     runners = []
     for _ in range(2):
         r = VerifyStepRunner(shape, device)
+        r.argmax_in_scan = argmax_in_scan
         for n in ("q", "k", "v", "g", "beta", "state"):
             getattr(r, n).copy_(x[n])
         r.logits.copy_(acc["logits"])

@@ -236,9 +236,11 @@ def test_fused_rollback_scan_equals_gather_then_scan(device, in_place):
     del tape_e
 
 
-def test_step_runner_fused_matches_explicit(device):
+@pytest.mark.parametrize("argmax_in_scan", [True, False])
+def test_step_runner_fused_matches_explicit(device, argmax_in_scan):
     """VerifyStepRunner: run_fused (rollback folded into the next scan) and run
-    (explicit gather) leave the same rolled-back state and the same tape."""
+    (explicit gather) leave the same rolled-back state and the same tape, with
+    the accept's argmax in the scan's launch or in its own."""
     from dflash_mlx.step import StepShape, VerifyStepRunner
     from dflash_mlx.workloads import (CONFIGS, ScanConfig, make_accept_inputs, make_scan_inputs,
                                       make_verify_block)
@@ -250,6 +252,8 @@ def test_step_runner_fused_matches_explicit(device):
     runs = []
     for fused in (False, True):
         r = VerifyStepRunner(shape, device)
+        assert r.argmax_in_scan  # 1.3 MB of logits: the default places it in the scan
+        r.argmax_in_scan = argmax_in_scan
         for n in ("q", "k", "v", "g", "beta", "state"):
             getattr(r, n).copy_(x[n])
         r.logits.copy_(acc["logits"])

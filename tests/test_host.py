@@ -61,6 +61,26 @@ def test_scan_bytes_match_baseline_table():
     assert CONFIGS[2].scan_bytes() == 1_220_673_536
 
 
+def test_argmax_placement_follows_logit_size():
+    """The fused step runs the accept's argmax inside the scan's launch only
+    while the verify logits are small (c1: 9.7 MB) and a conv window exists;
+    c2's 311 MB of logits get a launch of their own."""
+    from dflash_mlx.step import ARGMAX_IN_SCAN_MAX_BYTES, StepShape
+    from dflash_mlx.workloads import CONFIGS
+
+    def shape(c, conv_dim=8192):
+        return StepShape(L=c.layers, B=c.B, T=c.T, Hk=c.Hk, Hv=c.Hv, Dk=c.Dk, Dv=c.Dv, V=c.V,
+                         conv_dim=conv_dim)
+
+    assert shape(CONFIGS[0]).fuse_argmax() and shape(CONFIGS[1]).fuse_argmax()
+    assert not shape(CONFIGS[2]).fuse_argmax()
+    assert not shape(CONFIGS[1], conv_dim=0).fuse_argmax()
+    edge = StepShape(L=1, B=1, T=1, Hk=1, Hv=1, Dk=1, Dv=1, V=ARGMAX_IN_SCAN_MAX_BYTES // 4,
+                     conv_dim=1)
+    assert edge.fuse_argmax()
+    assert not StepShape(**{**edge.__dict__, "V": edge.V + 1}).fuse_argmax()
+
+
 def test_workload_inputs_follow_the_recipe():
     x = make_scan_inputs(CONFIGS[0])
     import torch
