@@ -30,10 +30,16 @@ __global__ __launch_bounds__(64 * kFinalizeWaves) void accept_finalize_kernel(
   for (int r = wave; r < N; r += kFinalizeWaves) {
     const uint64_t* kr = keys + ((int64_t)b * N + r) * splits;
     uint64_t m = 0;
-    // Unrolled so that each lane's key loads go out together (the fused LM
-    // head leaves ~1 200 keys per row: ~19 per lane).
-#pragma unroll 8
-    for (int s = lane; s < splits; s += 64) m = u64_max(m, kr[s]);
+    // Batches of 16 loads per lane issued together (the fused LM head leaves
+    // ~1 200 keys per row: two batches); indices past the row repeat its
+    // last key, which leaves the max as is.
+    for (int s0 = lane; s0 < splits; s0 += 64 * 16) {
+      uint64_t v[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = kr[min(s0 + 64 * i, splits - 1)];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) m = u64_max(m, v[i]);
+    }
     m = wave_max_u64(m);
     if (lane == 0) {
       const int tok = argmax_key_index(m);

@@ -27,11 +27,12 @@ struct ConvTable {
 // it writes, so conv_out may alias conv_in.
 template <typename U>
 __device__ __forceinline__ void conv_window_copy(const ConvTable& tab, int l, int b, int a, int K1,
-                                                 int64_t Cu, int64_t qkv_bs, int64_t qkv_rs) {
+                                                 int64_t Cu, int64_t qkv_bs, int64_t qkv_rs,
+                                                 int64_t c_begin = -1) {
   const U* cin = reinterpret_cast<const U*>(tab.cin[l]) + (int64_t)b * K1 * Cu;
   const U* qkv = reinterpret_cast<const U*>(tab.qkv[l]) + (int64_t)b * qkv_bs;
   U* cout = reinterpret_cast<U*>(tab.cout[l]) + (int64_t)b * K1 * Cu;
-  for (int64_t c = (int64_t)blockIdx.x * kConvThreads + threadIdx.x; c < Cu;
+  for (int64_t c = c_begin >= 0 ? c_begin : (int64_t)blockIdx.x * kConvThreads + threadIdx.x; c < Cu;
        c += (int64_t)gridDim.x * kConvThreads) {
     U vals[kMaxConvRows];
 #pragma unroll
@@ -46,6 +47,47 @@ __device__ __forceinline__ void conv_window_copy(const ConvTable& tab, int l, in
       if (r < K1) cout[(int64_t)r * Cu + c] = vals[r];
   }
 }
+
+// The same copy with the accepted count not yet known: the lane's first column
+// unit's rows 0 .. T+K1-1 of concat(conv_in, qkv) (every row a window can
+// start at, T + K1 <= CAND) are loaded by prefetch() before a is computed;
+// store() then writes the K1 rows at a and copies any further column units as
+// conv_window_copy does.  All loads precede the stores, so conv_out may alias
+// conv_in.
+template <typename U, int CAND>
+struct ConvWindowPrefetch {
+  U rows[CAND];
+
+  // Lanes past the last column unit load unit Cu - 1 and rows past T + K1 - 1
+  // repeat that row (valid addresses, no branch around the loads; never stored).
+  __device__ __forceinline__ void prefetch(const ConvTable& tab, int l, int b, int T, int K1,
+                                           int64_t Cu, int64_t qkv_bs, int64_t qkv_rs) {
+    const int64_t c = min((int64_t)blockIdx.x * kConvThreads + threadIdx.x, Cu - 1);
+    const U* cin = reinterpret_cast<const U*>(tab.cin[l]) + (int64_t)b * K1 * Cu + c;
+    const U* qkv = reinterpret_cast<const U*>(tab.qkv[l]) + (int64_t)b * qkv_bs + c;
+#pragma unroll
+    for (int r = 0; r < CAND; ++r) {
+      const int j = min(r, T + K1 - 1);
+      rows[r] = j < K1 ? cin[(int64_t)j * Cu] : qkv[(int64_t)(j - K1) * qkv_rs];
+    }
+  }
+
+  __device__ __forceinline__ void store(const ConvTable& tab, int l, int b, int a, int K1,
+                                        int64_t Cu, int64_t qkv_bs, int64_t qkv_rs) {
+    const int64_t c = (int64_t)blockIdx.x * kConvThreads + threadIdx.x;
+    if (c < Cu) {
+      U* cout = reinterpret_cast<U*>(tab.cout[l]) + (int64_t)b * K1 * Cu + c;
+      // every row under a compile-time index (the array stays in registers);
+      // a is uniform, so the tests branch the whole wavefront together
+#pragma unroll
+      for (int j = 0; j < CAND; ++j) {
+        const int r = j - a;
+        if (r >= 0 && r < K1) cout[(int64_t)r * Cu] = rows[j];
+      }
+    }
+    conv_window_copy<U>(tab, l, b, a, K1, Cu, qkv_bs, qkv_rs, c + (int64_t)gridDim.x * kConvThreads);
+  }
+};
 
 // Workgroups along x of a (chunks, B, L) copy grid over `units` units:
 // ~2048 workgroups in total, at least one per (sequence, layer).

@@ -64,8 +64,11 @@ hipError_t launch_partial(const void* logits, int64_t bs, int64_t rs, int B, int
 // first launch (write_accept) also writes posterior / matched / bonus of b
 // and, when accepted_out is given, the clamped a (the keep count the next
 // step's rolled-back state load reads).
+// CAND > 0 (T + K1 <= CAND): the lane's window rows are loaded with the keys
+// and the first 64 draft tokens, before the accepted count is known, so the
+// kernel waits on memory once instead of three times.
 // Dynamic LDS: N int32.
-template <typename U>
+template <typename U, int CAND>
 __global__ __launch_bounds__(kConvThreads) void accept_conv_rollback_kernel(
     const uint64_t* __restrict__ keys, int splits, int N, const int32_t* __restrict__ draft,
     int64_t dstride, int n_draft, int32_t* __restrict__ posterior, int32_t* __restrict__ matched,
@@ -77,6 +80,11 @@ __global__ __launch_bounds__(kConvThreads) void accept_conv_rollback_kernel(
   const int b = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int mlen = min(n_draft, N);
+  int draft0 = 0;  // draft token `lane` of the first 64 (wavefront 0)
+  if (wave == 0 && lane < mlen) draft0 = draft[(int64_t)b * dstride + lane];
+  ConvWindowPrefetch<U, (CAND > 0 ? CAND : 1)> win;
+  if (CAND > 0) win.prefetch(tab, blockIdx.z, b, T, K1, Cu, qkv_bs, qkv_rs);
   // 16 lanes per row, 16 rows per pass: every lane's key loads are issued
   // together, then a max over its 16 lanes (exact, so order-free).
   const int sub = threadIdx.x & 15;
@@ -85,8 +93,15 @@ __global__ __launch_bounds__(kConvThreads) void accept_conv_rollback_kernel(
     uint64_t m = 0;
     if (r < N) {
       const uint64_t* kr = keys + ((int64_t)b * N + r) * splits;
-#pragma unroll 8
-      for (int s = sub; s < splits; s += 16) m = u64_max(m, kr[s]);
+      // batches of 8 loads issued together (one batch up to 128 splits);
+      // indices past the row repeat its last key, which leaves the max as is
+      for (int s0 = sub; s0 < splits; s0 += 16 * 8) {
+        uint64_t v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = kr[min(s0 + 16 * i, splits - 1)];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = u64_max(m, v[i]);
+      }
     }
 #pragma unroll
     for (int off = 8; off >= 1; off >>= 1) {
@@ -98,11 +113,11 @@ __global__ __launch_bounds__(kConvThreads) void accept_conv_rollback_kernel(
   }
   __syncthreads();
   if (wave == 0) {
-    const int mlen = min(n_draft, N);
     int first = mlen;
     for (int base0 = 0; base0 < mlen; base0 += 64) {
       const int j = base0 + lane;
-      const bool mismatch = (j < mlen) && (draft[(int64_t)b * dstride + j] != post[j]);
+      const int dj = base0 == 0 ? draft0 : (j < mlen ? draft[(int64_t)b * dstride + j] : 0);
+      const bool mismatch = (j < mlen) && (dj != post[j]);
       const unsigned long long mask = __ballot(mismatch);
       if (mask != 0ull) {
         first = base0 + __ffsll(mask) - 1;
@@ -122,9 +137,15 @@ __global__ __launch_bounds__(kConvThreads) void accept_conv_rollback_kernel(
       if (accepted_out != nullptr) accepted_out[b] = min(max(first + accepted_offset, 0), T);
     }
   }
-  conv_window_copy<U>(tab, blockIdx.z, b, min(max(first + accepted_offset, 0), T), K1, Cu,
-                      qkv_bs, qkv_rs);
+  const int a = min(max(first + accepted_offset, 0), T);
+  if (CAND > 0)
+    win.store(tab, blockIdx.z, b, a, K1, Cu, qkv_bs, qkv_rs);
+  else
+    conv_window_copy<U>(tab, blockIdx.z, b, a, K1, Cu, qkv_bs, qkv_rs);
 }
+
+// Candidate rows the speculative window copy holds (T + K1 <= this).
+constexpr int kConvCandidates = 20;
 
 }  // namespace
 }  // namespace dflash
@@ -227,21 +248,19 @@ int accept_conv_rollback(
     const ConvTable tab = conv_table(conv_in, qkv, conv_out, l0, nl);
     const dim3 grid(copy_grid_chunks(pl.Cu, kConvThreads, B, nl), B, nl);
     const int first = l0 == 0;
-    if (pl.unit == 16)
-      hipLaunchKernelGGL(accept_conv_rollback_kernel<u32x4>, grid, dim3(kConvThreads), lds, s,
-                         keys, sp.splits, N, draft, draft_stride, n_draft, posterior, matched,
-                         bonus, first, accepted_offset, accepted_out, tab, T, K1, pl.Cu, pl.qbs,
-                         pl.qrs);
-    else if (pl.unit == 4)
-      hipLaunchKernelGGL(accept_conv_rollback_kernel<uint32_t>, grid, dim3(kConvThreads), lds, s,
-                         keys, sp.splits, N, draft, draft_stride, n_draft, posterior, matched,
-                         bonus, first, accepted_offset, accepted_out, tab, T, K1, pl.Cu, pl.qbs,
-                         pl.qrs);
-    else
-      hipLaunchKernelGGL(accept_conv_rollback_kernel<uint16_t>, grid, dim3(kConvThreads), lds, s,
-                         keys, sp.splits, N, draft, draft_stride, n_draft, posterior, matched,
-                         bonus, first, accepted_offset, accepted_out, tab, T, K1, pl.Cu, pl.qbs,
-                         pl.qrs);
+    const bool spec = T + K1 <= kConvCandidates;
+#define DFLASH_ACR(U, C)                                                                          \
+  hipLaunchKernelGGL((accept_conv_rollback_kernel<U, C>), grid, dim3(kConvThreads), lds, s, keys, \
+                     sp.splits, N, draft, draft_stride, n_draft, posterior, matched, bonus, first,  \
+                     accepted_offset, accepted_out, tab, T, K1, pl.Cu, pl.qbs, pl.qrs)
+    if (pl.unit == 16) {
+      if (spec) DFLASH_ACR(u32x4, kConvCandidates); else DFLASH_ACR(u32x4, 0);
+    } else if (pl.unit == 4) {
+      if (spec) DFLASH_ACR(uint32_t, kConvCandidates); else DFLASH_ACR(uint32_t, 0);
+    } else {
+      if (spec) DFLASH_ACR(uint16_t, kConvCandidates); else DFLASH_ACR(uint16_t, 0);
+    }
+#undef DFLASH_ACR
     e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }
