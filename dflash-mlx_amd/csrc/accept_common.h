@@ -27,6 +27,10 @@ __global__ __launch_bounds__(64 * kFinalizeWaves) void accept_finalize_kernel(
   const int b = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
+  const int mlen = min(n_draft, N);
+  int draft0 = 0;  // draft token `lane` of the first 64, loaded with the keys (wavefront 0)
+  if (wave == 0 && lane < mlen && (matched != nullptr || bonus != nullptr))
+    draft0 = draft[(int64_t)b * dstride + lane];
   for (int r = wave; r < N; r += kFinalizeWaves) {
     const uint64_t* kr = keys + ((int64_t)b * N + r) * splits;
     uint64_t m = 0;
@@ -49,11 +53,11 @@ __global__ __launch_bounds__(64 * kFinalizeWaves) void accept_finalize_kernel(
   }
   __syncthreads();
   if (wave != 0 || (matched == nullptr && bonus == nullptr)) return;
-  const int mlen = min(n_draft, N);
   int first = mlen;
   for (int base0 = 0; base0 < mlen; base0 += 64) {
     const int j = base0 + lane;
-    const bool mismatch = (j < mlen) && (draft[(int64_t)b * dstride + j] != post[j]);
+    const int dj = base0 == 0 ? draft0 : (j < mlen ? draft[(int64_t)b * dstride + j] : 0);
+    const bool mismatch = (j < mlen) && (dj != post[j]);
     const unsigned long long mask = __ballot(mismatch);
     if (mask != 0ull) {
       first = base0 + __ffsll(mask) - 1;
