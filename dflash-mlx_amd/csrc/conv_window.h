@@ -15,6 +15,8 @@ namespace {
 
 constexpr int kConvThreads = 256;
 constexpr int kMaxConvRows = 8;
+// Candidate rows the speculative window copy holds (used when T + K1 <= this).
+constexpr int kConvCandidates = 20;
 
 struct ConvTable {
   const char* cin[kMaxLayersPerLaunch];

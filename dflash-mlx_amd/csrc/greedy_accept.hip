@@ -144,8 +144,6 @@ __global__ __launch_bounds__(kConvThreads) void accept_conv_rollback_kernel(
     conv_window_copy<U>(tab, blockIdx.z, b, a, K1, Cu, qkv_bs, qkv_rs);
 }
 
-// Candidate rows the speculative window copy holds (T + K1 <= this).
-constexpr int kConvCandidates = 20;
 
 }  // namespace
 }  // namespace dflash

@@ -67,13 +67,21 @@ __global__ __launch_bounds__(kCopyThreads) void tape_select_kernel(
   }
 }
 
-// grid: (column chunks, B, layers).
-template <typename U>
+// grid: (column chunks, B, layers).  CAND > 0 (T + K1 <= CAND): the window
+// rows are loaded with the accepted count instead of after it.
+template <typename U, int CAND>
 __global__ __launch_bounds__(kConvThreads) void conv_rollback_kernel(
     const ConvTable tab, const int32_t* __restrict__ accepted, int T, int K1,
     int64_t Cu, int64_t qkv_bs, int64_t qkv_rs) {
   const int b = blockIdx.y;
-  conv_window_copy<U>(tab, blockIdx.z, b, min(max(accepted[b], 0), T), K1, Cu, qkv_bs, qkv_rs);
+  if constexpr (CAND > 0) {
+    const int a = accepted[b];
+    ConvWindowPrefetch<U, CAND> win;
+    win.prefetch(tab, blockIdx.z, b, T, K1, Cu, qkv_bs, qkv_rs);
+    win.store(tab, blockIdx.z, b, min(max(a, 0), T), K1, Cu, qkv_bs, qkv_rs);
+  } else {
+    conv_window_copy<U>(tab, blockIdx.z, b, min(max(accepted[b], 0), T), K1, Cu, qkv_bs, qkv_rs);
+  }
 }
 
 
@@ -147,15 +155,18 @@ extern "C" int dflash_conv_rollback(const void* const* conv_in, const void* cons
     const int nl = L - l0 < kMaxLayersPerLaunch ? L - l0 : kMaxLayersPerLaunch;
     const ConvTable tab = conv_table(conv_in, qkv, conv_out, l0, nl);
     dim3 grid(copy_grid_chunks(pl.Cu, kConvThreads, B, nl), B, nl);
-    if (pl.unit == 16)
-      hipLaunchKernelGGL(conv_rollback_kernel<u32x4>, grid, dim3(kConvThreads), 0, s, tab,
-                         accepted, T, K1, pl.Cu, pl.qbs, pl.qrs);
-    else if (pl.unit == 4)
-      hipLaunchKernelGGL(conv_rollback_kernel<uint32_t>, grid, dim3(kConvThreads), 0, s, tab,
-                         accepted, T, K1, pl.Cu, pl.qbs, pl.qrs);
-    else
-      hipLaunchKernelGGL(conv_rollback_kernel<uint16_t>, grid, dim3(kConvThreads), 0, s, tab,
-                         accepted, T, K1, pl.Cu, pl.qbs, pl.qrs);
+    const bool spec = T + K1 <= kConvCandidates;
+#define DFLASH_CR(U, C)                                                                            \
+  hipLaunchKernelGGL((conv_rollback_kernel<U, C>), grid, dim3(kConvThreads), 0, s, tab, accepted, T, \
+                     K1, pl.Cu, pl.qbs, pl.qrs)
+    if (pl.unit == 16) {
+      if (spec) DFLASH_CR(u32x4, kConvCandidates); else DFLASH_CR(u32x4, 0);
+    } else if (pl.unit == 4) {
+      if (spec) DFLASH_CR(uint32_t, kConvCandidates); else DFLASH_CR(uint32_t, 0);
+    } else {
+      if (spec) DFLASH_CR(uint16_t, kConvCandidates); else DFLASH_CR(uint16_t, 0);
+    }
+#undef DFLASH_CR
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
   }

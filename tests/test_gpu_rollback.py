@@ -48,13 +48,15 @@ def test_tape_select_in_place_and_scalar_path(oracle, device):
     np.testing.assert_array_equal(st.cpu().numpy(), oracle.tape_select(tape.numpy(), s0.numpy(), acc.numpy()))
 
 
-@pytest.mark.parametrize("dtype,C", [(torch.bfloat16, 8192), (torch.float32, 8192), (torch.bfloat16, 37)])
-def test_conv_rollback(oracle, device, dtype, C):
+@pytest.mark.parametrize("dtype,C,T", [(torch.bfloat16, 8192, 16), (torch.float32, 8192, 16),
+                                       (torch.bfloat16, 37, 16),
+                                       (torch.bfloat16, 8192, 24)])  # T + K1 > 20: rows loaded after the count
+def test_conv_rollback(oracle, device, dtype, C, T):
     gen = torch.Generator().manual_seed(3)
-    L, B, K1, T = 3, 2, 3, 16
+    L, B, K1 = 3, 2, 3
     conv = [torch.randn(B, K1, C, generator=gen).to(dtype) for _ in range(L)]
     qkv = [torch.randn(B, T, C, generator=gen).to(dtype) for _ in range(L)]
-    for accs in ([0, 16], [1, 2], [3, 7]):
+    for accs in ([0, T], [1, 2], [3, 7]):
         acc = torch.tensor(accs, dtype=torch.int32)
         print(f"[conv_rollback {dtype} C={C} a={accs}]", flush=True)
         out = conv_rollback([c.to(device) for c in conv], [q.to(device) for q in qkv], acc.to(device))
@@ -275,6 +277,7 @@ def test_step_runner_fused_matches_explicit(device, argmax_in_scan):
     (1, 16, 151936, 24, 3, 8192, 0, torch.float32),   # the c1 step: 24 layers, 16-byte units
     (3, 16, 3000, 2, 3, 100, 1, torch.bfloat16),      # ragged C (2-byte units), keep = matched + 1
     (2, 5, 1000, 40, 2, 64, 1, torch.float16),        # more layers than one launch holds
+    (2, 24, 2000, 3, 3, 256, 1, torch.bfloat16),      # T + K1 > 20: window rows loaded after the count
 ])
 def test_accept_conv_rollback_matches_two_calls(device, B, N, V, L, K1, C, offset, dtype):
     """dflash_greedy_accept_conv_rollback (finalize inside the window copy)
