@@ -156,3 +156,39 @@ def test_model_op_size_limits(lib):
     # attention: B beyond the partial kernel's grid.z
     assert lib.dflash_attn_verify(d, d, d, d, d, 4096, d, 70000, 16, 16, 4, 128, 4096, 4096,
                                   0.0884, d, 1 << 40, None) == -2
+
+
+def test_scan_with_argmax_and_keys_accept_validation(lib):
+    """The scan launch carrying the accept's argmax, and the accept + conv
+    rollback from those keys, refuse bad arguments before any launch."""
+    d = ctypes.c_void_p(0x1000)
+    f = lib.dflash_gdn_verify_scan_rollback_argmax
+    ws = lib.dflash_greedy_accept_workspace_bytes(1, 16, 1024)
+
+    def scan(logits=d, dtype=0, B_acc=1, N=16, V=1024, work=d, wsb=ws, B=1, T=16):
+        return f(d, d, d, d, d, d, d, d, 16, 1, d, None, d, B, T, 4, 4, 64, 64, None,
+                 logits, dtype, 16 * 1024, 1024, B_acc, N, V, work, wsb, None)
+
+    assert scan(B_acc=0) == -2                  # no accept rows
+    assert scan(B_acc=2048, N=16) == -2         # more than 16384 logits rows
+    assert scan(T=0) == -2                      # the launch must have scan work
+    assert scan(logits=None) == -1
+    assert scan(work=None) == -1
+    assert scan(dtype=2) == -3                  # fp16 logits: not in this launch
+    assert scan(wsb=ws - 8) == -5               # workspace too small
+    assert scan(logits=ctypes.c_void_p(0x1008)) == -4   # rows not 16-byte aligned
+    # final_state aliasing the state buffer
+    assert f(d, d, d, d, d, d, d, d, 16, 1, d, d, d, 1, 16, 4, 4, 64, 64, None,
+             d, 0, 16 * 1024, 1024, 1, 16, 1024, d, ws, None) == -2
+    g = lib.dflash_accept_keys_conv_rollback
+
+    def keys(draft=d, n_draft=15, work=d, wsb=ws, K1=3, elem=2, N=16):
+        return g(draft, 16, n_draft, d, d, d, 1, N, 1024, work, wsb, d, d, d, 1, d, 1, 16, K1,
+                 8192, 16 * 8192, 8192, elem, None)
+
+    assert keys(draft=None) == -1               # drafts missing while n_draft > 0
+    assert keys(work=None) == -1
+    assert keys(wsb=8) == -5
+    assert keys(K1=9) == -3                     # more window rows than one lane holds
+    assert keys(elem=3) == -3
+    assert keys(N=0) == -2
