@@ -303,6 +303,7 @@ def measure_gemm(torch, dev, reps=8, copies=4):
     gen = torch.Generator(device=dev).manual_seed(0)
     x = (torch.randn(M, max(k for _, k in dims.values()), generator=gen, device=dev)
          ).to(torch.bfloat16)
+    gws = torch.zeros(int(lib.dflash_gemm_tail_workspace_bytes()), dtype=torch.uint8, device=dev)
     res = {}
     for name, (N, K) in dims.items():
         ns, rpw, kw = HybridVerifyRunner.TILED_PLAN[name]
@@ -314,7 +315,7 @@ def measure_gemm(torch, dev, reps=8, copies=4):
         def call(w):
             if name == "w_gu":
                 _lib.call("dflash_gemm_bf16_swiglu_tiled", x.data_ptr(), x.stride(0), w.data_ptr(),
-                          out.data_ptr(), N // 2, M, N, K, kw, stream)
+                          out.data_ptr(), N // 2, M, N, K, kw, gws.data_ptr(), gws.numel(), stream)
             else:
                 _lib.call("dflash_gemm_bf16_tiled", x.data_ptr(), x.stride(0), w.data_ptr(),
                           out.data_ptr(), 0 if splits else N, M, N, K, ns, rpw, kw, stream)

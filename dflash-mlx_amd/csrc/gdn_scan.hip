@@ -580,19 +580,8 @@ int pick_rows(int Dv) {
 // Workgroups launched: at most 3 per CU, each walking several (head, row
 // block) items.  On MI355X this beat one workgroup per item by ~12 % on the
 // tape-write-bound verify shapes (fewer concurrent write streams).
-// CUs of the current device (cached per device; 0 if unknown).
-int scan_cus() {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cus[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      return 0;
-    cus[dev] = n;
-  }
-  return cus[dev];
-}
+// CUs of the current device (0 if unknown).
+int scan_cus() { return device_cus(); }
 
 int scan_grid(int items) {
   const int cus = scan_cus();

@@ -79,6 +79,18 @@ struct GemmParams {
   int norm_tiles;
   float eps;
   float* row_inv_out;          // [M] or null: inv, stored by workgroup (0, 0)
+  // Tail split (KW == 4, one k-split, bf16 epilogue).  U row groups on C CUs
+  // make R = U / C whole rounds and a last round of T = U - R*C row groups
+  // that would leave most CUs idle while the slowest CUs run a round more.
+  // Those T run instead as 4T one-wave units (row group tail_first + u % T,
+  // k-quarter u / T), launched first, one per CU.  A unit stores its fp32
+  // sums in tail_part and counts itself in tail_count[tile]; the last of a
+  // row group's four to arrive adds the quarters in k order, as the
+  // workgroup's LDS merge does (same bits), resets the count to zero and
+  // runs the epilogue.
+  int tail_units, tail_tiles, tail_first;
+  float* tail_part;  // [tail_tiles][4 quarters][VT * MT tiles][4 elements][64 lanes]
+  int* tail_count;   // [tail_tiles], zero between calls
 };
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -200,15 +212,28 @@ __global__ __launch_bounds__(KW >= 8 ? 64 * KW : kGThreads) void skinny_gemm_ker
   const int g = lane >> 4;
   constexpr int kRowGroups = (kThreads / 64) / KW;  // row groups per workgroup
   static_assert(KW == 1 || kRowGroups == 1, "red[] holds the k-parts of one row group");
-  const int kpart = wave % KW;                        // this wave's quarter of the k-range
-  const int nwave = (blockIdx.x * kRowGroups + wave / KW) * VT * 16;
+  int kpart = wave % KW;  // this wave's quarter of the k-range
+  int rgroup = blockIdx.x;
+  bool tail = false;  // a tail unit: wave 0 alone runs k-quarter kpart of row group rgroup
+  if (KW == 4 && p.tail_units > 0) {
+    if ((int)blockIdx.x < p.tail_units) {
+      tail = true;
+      rgroup = p.tail_first + (int)blockIdx.x % p.tail_tiles;
+      kpart = (int)blockIdx.x / p.tail_tiles;
+    } else {
+      rgroup = (int)blockIdx.x - p.tail_units;
+    }
+  }
+  const bool idle = tail && wave != 0;  // NRM: still needed for the shared prologue
+  if (idle && !NRM) return;
+  const int nwave = (rgroup * kRowGroups + wave / KW) * VT * 16;
   const int split = blockIdx.y;
   const int nks_all = p.K / kGKStep;
   const int split_begin = split * p.ks_per_split;
   const int split_len = min(p.ks_per_split, nks_all - split_begin);
   const int part_len = (split_len + KW - 1) / KW;
   const int ks_begin = split_begin + min(kpart * part_len, split_len);
-  const int nks = min(part_len, split_begin + split_len - ks_begin);
+  const int nks = idle ? 0 : min(part_len, split_begin + split_len - ks_begin);
 
   const uint16_t* wrow[2 * VT];
   if (TILED) {  // fragment (k-step, row tile, half): 1 KB at ((ks * N/16 + rt) * 2 + h) KB
@@ -272,6 +297,7 @@ __global__ __launch_bounds__(KW >= 8 ? 64 * KW : kGThreads) void skinny_gemm_ker
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) inv[mt] = invs[min(mt * 16 + r16, p.M - 1)];
   }
+  if (idle) return;
 
   for (int ks0 = 0; ks0 < nks; ks0 += D) {
 #pragma unroll
@@ -321,7 +347,51 @@ __global__ __launch_bounds__(KW >= 8 ? 64 * KW : kGThreads) void skinny_gemm_ker
     }
   }
 
-  if (KW > 1) {  // merge the k-quarters: waves 1..KW-1 hand their sums to wave 0
+  if (KW == 4 && tail) {
+    // Cross-workgroup merge.  The quarters travel as agent-scope atomic
+    // stores and loads (write-through to, and read from, the point where
+    // every XCD's L2 sees the same data); the wave waits for its stores to
+    // complete before it counts itself, and the last arriver issues its
+    // loads only once its count has returned.  No wave waits on another.
+    constexpr int kUnit = VT * MT * 4 * 64;  // floats per quarter
+    const int tile = rgroup - p.tail_first;
+    float* tp = p.tail_part + (int64_t)tile * 4 * kUnit;
+#pragma unroll
+    for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          __hip_atomic_store(tp + kpart * kUnit + ((vt * MT + mt) * 4 + i) * 64 + lane, acc[vt][mt][i],
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0);
+    int arrived = 0;
+    if (lane == 0)
+      arrived = __hip_atomic_fetch_add(p.tail_count + tile, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    arrived = __shfl(arrived, 0, 64);
+    if (arrived != 3) return;
+    if (lane == 0) __hip_atomic_store(p.tail_count + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    f32x4 sum[VT][MT];
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          f32x4 v = acc[vt][mt];
+          if (q != kpart) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              v[i] = __hip_atomic_load(tp + q * kUnit + ((vt * MT + mt) * 4 + i) * 64 + lane,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          sum[vt][mt] = q == 0 ? v : sum[vt][mt] + v;
+        }
+#pragma unroll
+    for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) acc[vt][mt] = sum[vt][mt];
+  } else if (KW > 1) {  // merge the k-quarters: waves 1..KW-1 hand their sums to wave 0
     if (kpart > 0) {
 #pragma unroll
       for (int vt = 0; vt < VT; ++vt)
@@ -405,9 +475,37 @@ hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
   constexpr int D = MT == 1 ? 4 : (MT == 2 ? 4 : 2);
   constexpr int kThreads = KW >= 8 ? 64 * KW : kGThreads;
   const int rows_per_wg = (kThreads / 64 / KW) * VT * 16;
-  const dim3 grid((unsigned)ceil_div(p.N, rows_per_wg), (unsigned)p.nsplit);
+  dim3 grid((unsigned)ceil_div(p.N, rows_per_wg), (unsigned)p.nsplit);
+  if (p.tail_units > 0) grid.x = (unsigned)(p.tail_first + p.tail_units);
   hipLaunchKernelGGL((skinny_gemm_kernel<MT, VT, D, KW, TILED, NRM>), grid, dim3(kThreads), 0, s, p);
   return hipGetLastError();
+}
+
+// Workspace of the tail split: the tile counters, then the quarters' fp32
+// sums (VT * MT <= 16 tiles of 4 x 64 floats per quarter).
+constexpr int kTailMaxTiles = 64;
+constexpr size_t kTailCountBytes = 256;
+constexpr size_t kTailWorkspaceBytes = kTailCountBytes + (size_t)kTailMaxTiles * 4 * 16 * 4 * 64 * 4;
+
+// Plans the tail split (GemmParams::tail_*) of a one-split KW == 4 launch of
+// rows_per_wg weight rows per workgroup: used when the row groups fill at
+// least one whole round of the device's CUs and leave a last round of at
+// most a quarter of them.  No workspace: no tail split.
+int plan_tail(GemmParams& p, int rows_per_wg, void* ws, size_t ws_bytes) {
+  if (ws == nullptr) return DFLASH_OK;
+  if (ws_bytes < kTailWorkspaceBytes) return DFLASH_ERR_WORKSPACE;
+  if ((uintptr_t)ws & 255) return DFLASH_ERR_ALIGN;
+  const int cus = device_cus();
+  if (cus <= 0 || p.nsplit != 1) return DFLASH_OK;
+  const int U = (int)ceil_div(p.N, rows_per_wg);
+  const int R = U / cus, T = U - R * cus;
+  if (R < 1 || T == 0 || 4 * T > cus || T > kTailMaxTiles) return DFLASH_OK;
+  p.tail_units = 4 * T;
+  p.tail_tiles = T;
+  p.tail_first = R * cus;
+  p.tail_count = static_cast<int*>(ws);
+  p.tail_part = reinterpret_cast<float*>(static_cast<char*>(ws) + kTailCountBytes);
+  return DFLASH_OK;
 }
 
 template <int VT, int KW, bool TILED = false, bool NRM = false>
@@ -597,10 +695,13 @@ extern "C" int dflash_gemm_bf16_tiled(const void* x, int64_t x_row_stride, const
   return to_status(e);
 }
 
+extern "C" size_t dflash_gemm_tail_workspace_bytes(void) { return kTailWorkspaceBytes; }
+
 extern "C" int dflash_gemm_bf16_swiglu_tiled(const void* x, int64_t x_row_stride,
                                              const void* w_pairs_tiled, void* out,
                                              int64_t out_row_stride, int M, int N, int K,
-                                             int k_waves, void* stream) {
+                                             int k_waves, void* workspace, size_t workspace_bytes,
+                                             void* stream) {
   if (M < 0 || M > 64 || N <= 0 || N % 32 != 0 || K <= 0 || K % kGKStep != 0)
     return DFLASH_ERR_SHAPE;
   if (k_waves != 1 && k_waves != 4) return DFLASH_ERR_UNSUPPORTED;
@@ -621,6 +722,10 @@ extern "C" int dflash_gemm_bf16_swiglu_tiled(const void* x, int64_t x_row_stride
   p.ks_per_split = K / kGKStep;
   p.nsplit = 1;
   p.swiglu = 1;
+  if (k_waves == 4) {
+    const int st = plan_tail(p, 32, workspace, workspace_bytes);
+    if (st != DFLASH_OK) return st;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
   return to_status(k_waves == 1 ? launch_m<2, 1, true>(p, s) : launch_m<2, 4, true>(p, s));
 }
@@ -733,7 +838,8 @@ extern "C" int dflash_gemm_bf16_swiglu_tiled_normed(const void* h, int64_t h_row
                                                     int norm_tiles, float eps, float* row_inv_out,
                                                     const void* w_pairs_tiled, void* out,
                                                     int64_t out_row_stride, int M, int N, int K,
-                                                    int k_waves, void* stream) {
+                                                    int k_waves, void* workspace,
+                                                    size_t workspace_bytes, void* stream) {
   if (M < 0 || M > 64 || N <= 0 || N % 32 != 0 || K <= 0 || K % kGKStep != 0)
     return DFLASH_ERR_SHAPE;
   if (k_waves != 4) return DFLASH_ERR_UNSUPPORTED;
@@ -754,5 +860,7 @@ extern "C" int dflash_gemm_bf16_swiglu_tiled_normed(const void* h, int64_t h_row
   p.ks_per_split = K / kGKStep;
   p.nsplit = 1;
   p.swiglu = 1;
+  st = plan_tail(p, 32, workspace, workspace_bytes);
+  if (st != DFLASH_OK) return st;
   return to_status(launch_m<2, 4, true, true>(p, static_cast<hipStream_t>(stream)));
 }

@@ -64,14 +64,17 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dflash_weight_tile_bytes": (_SZ, [_I, _I]),
     "dflash_weight_tile_bf16": (_I, [_VP, _I64, _VP, _I, _I, _VP]),
     "dflash_gemm_bf16_tiled": (_I, [_VP, _I64, _VP, _VP, _I64, _I, _I, _I, _I, _I, _I, _VP]),
-    "dflash_gemm_bf16_swiglu_tiled": (_I, [_VP, _I64, _VP, _VP, _I64, _I, _I, _I, _I, _VP]),
+    "dflash_gemm_bf16_swiglu_tiled": (
+        _I, [_VP, _I64, _VP, _VP, _I64, _I, _I, _I, _I, _VP, _SZ, _VP]),
+    "dflash_gemm_tail_workspace_bytes": (_SZ, []),
     "dflash_gemm_bf16_tiled_residual_norm": (
         _I, [_VP, _I64, _VP, _I, _I, _I, _VP, _VP, _VP, _I64, _VP, _VP]),
     "dflash_gemm_bf16_tiled_normed": (
         _I, [_VP, _I64, _VP, _VP, _I, ctypes.c_float, _VP, _VP, _VP, _I64, _I, _I, _I, _I, _I, _I,
              _VP]),
     "dflash_gemm_bf16_swiglu_tiled_normed": (
-        _I, [_VP, _I64, _VP, _VP, _I, ctypes.c_float, _VP, _VP, _VP, _I64, _I, _I, _I, _I, _VP]),
+        _I, [_VP, _I64, _VP, _VP, _I, ctypes.c_float, _VP, _VP, _VP, _I64, _I, _I, _I, _I, _VP,
+             _SZ, _VP]),
     "dflash_splitk_reduce": (_I, [_VP, _I, _I, _I, _VP, _I64, _VP]),
     "dflash_swiglu": (_I, [_VP, _VP, _I, _I, _VP]),
     "dflash_attn_prep": (
@@ -132,7 +135,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _I64, _I64, _I64, _I, _VP],
     ),
 }
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

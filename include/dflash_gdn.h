@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define DFLASH_ABI_VERSION 2
+#define DFLASH_ABI_VERSION 3
 
 /* Argument-validation codes (negative).  Positive values are hipError_t. */
 #define DFLASH_OK 0
@@ -578,7 +578,22 @@ int dflash_gemm_bf16_tiled(const void* x, int64_t x_row_stride,
 int dflash_gemm_bf16_swiglu_tiled(const void* x, int64_t x_row_stride,
                                   const void* w_pairs_tiled, void* out,
                                   int64_t out_row_stride, int M, int N, int K,
-                                  int k_waves, void* stream);
+                                  int k_waves, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
+/*
+ * Workspace of the SwiGLU GEMMs' tail split (dflash_gemm_bf16_swiglu_tiled
+ * and _tiled_normed, k_waves 4): bytes to pass, 256-byte aligned, zeroed
+ * once before the first call (every call leaves it zeroed again).  With it,
+ * when the 32-row groups (N / 32) make at least one whole round of the
+ * device's compute units and leave a last round of T <= CUs / 4 (and <= 64)
+ * groups, those T groups run as 4T single-wavefront units of a k-quarter
+ * each, merged through the workspace in the workgroup's own k order: the
+ * same bits as without it (NULL workspace), in less time.  Calls sharing a
+ * workspace must not overlap (one stream).  No reference counterpart
+ * (scheduling of the MLP gate|up projection, mlx-lm Qwen3NextMLP).
+ */
+size_t dflash_gemm_tail_workspace_bytes(void);
 
 /*
  * The decoder layer's residual add and the next RMSNorm folded into the two
@@ -624,7 +639,8 @@ int dflash_gemm_bf16_swiglu_tiled_normed(const void* h, int64_t h_row_stride,
                                          float eps, float* row_inv_out,
                                          const void* w_pairs_tiled, void* out,
                                          int64_t out_row_stride, int M, int N,
-                                         int K, int k_waves, void* stream);
+                                         int K, int k_waves, void* workspace,
+                                         size_t workspace_bytes, void* stream);
 
 /*
  * out[m, n] = bf16(sum_s partials[s, m, n]) for partials fp32 [nsplit, M, N]

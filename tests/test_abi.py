@@ -45,6 +45,7 @@ def test_header_declares_expected_entry_points():
         "dflash_add_rmsnorm_splitk", "dflash_add_rmsnorm_capture", "dflash_embed_rmsnorm", "dflash_gemm_bf16", "dflash_gemm_splits",
         "dflash_splitk_reduce", "dflash_gemm_bf16_swiglu", "dflash_weight_tile_bytes",
         "dflash_weight_tile_bf16", "dflash_gemm_bf16_tiled", "dflash_gemm_bf16_swiglu_tiled",
+        "dflash_gemm_tail_workspace_bytes",
         "dflash_gemm_bf16_tiled_residual_norm",
         "dflash_gemm_bf16_tiled_normed", "dflash_gemm_bf16_swiglu_tiled_normed",
     ])
@@ -68,7 +69,7 @@ def test_library_targets_gfx950_only():
 
 
 def test_abi_version_and_strerror(lib):
-    assert lib.dflash_abi_version() == 2
+    assert lib.dflash_abi_version() == 3
     assert lib.dflash_strerror(0) == b"ok"
     assert b"NULL" in lib.dflash_strerror(-1)
     assert lib.dflash_strerror(-999) == b"unknown dflash error"

@@ -130,13 +130,13 @@ def test_normed_swiglu_bit_identical(device, M, I, K, tiles):
     inv = torch.full((M,), float("nan"), device=device)
     _lib.call("dflash_gemm_bf16_swiglu_tiled_normed", h.data_ptr(), K, nw.data_ptr(),
               sumsq.data_ptr(), tiles, EPS, inv.data_ptr(), wt.data_ptr(), got.data_ptr(), I, M,
-              2 * I, K, 4, st)
+              2 * I, K, 4, None, 0, st)
     torch.cuda.synchronize()
     _check_inv(inv, sumsq, K)
     y = ((h.float() * inv[:, None]) * nw.float()).bfloat16()
     ref = torch.full((M, I), float("nan"), device=device).bfloat16()
     _lib.call("dflash_gemm_bf16_swiglu_tiled", y.data_ptr(), K, wt.data_ptr(), ref.data_ptr(), I, M,
-              2 * I, K, 4, st)
+              2 * I, K, 4, None, 0, st)
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
 

@@ -207,7 +207,7 @@ def test_gemm_swiglu_tiled_bit_identical(device, M, I, K, kw):
     t = _tile(device, pairs)
     out_t = torch.full_like(out, float("nan"))
     _lib.call("dflash_gemm_bf16_swiglu_tiled", x.data_ptr(), K, t.data_ptr(), out_t.data_ptr(), I,
-              M, 2 * I, K, kw, _lib.stream_handle(device))
+              M, 2 * I, K, kw, None, 0, _lib.stream_handle(device))
     torch.cuda.synchronize()
     assert torch.equal(out_t, out)
 
