@@ -318,7 +318,8 @@ def measure_gemm(torch, dev, reps=8, copies=4):
                           out.data_ptr(), N // 2, M, N, K, kw, gws.data_ptr(), gws.numel(), stream)
             else:
                 _lib.call("dflash_gemm_bf16_tiled", x.data_ptr(), x.stride(0), w.data_ptr(),
-                          out.data_ptr(), 0 if splits else N, M, N, K, ns, rpw, kw, stream)
+                          out.data_ptr(), 0 if splits else N, M, N, K, ns, rpw, kw, gws.data_ptr(),
+                          gws.numel(), stream)
 
         for w in ws:
             call(w)

@@ -484,13 +484,17 @@ hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
 // Workspace of the tail split: the tile counters, then the quarters' fp32
 // sums (VT * MT <= 16 tiles of 4 x 64 floats per quarter).
 constexpr int kTailMaxTiles = 64;
-constexpr size_t kTailCountBytes = 256;
+constexpr size_t kTailCountBytes = 1024;
 constexpr size_t kTailWorkspaceBytes = kTailCountBytes + (size_t)kTailMaxTiles * 4 * 16 * 4 * 64 * 4;
 
 // Plans the tail split (GemmParams::tail_*) of a one-split KW == 4 launch of
-// rows_per_wg weight rows per workgroup: used when the row groups fill at
-// least one whole round of the device's CUs and leave a last round of at
-// most a quarter of them.  No workspace: no tail split.
+// rows_per_wg weight rows per workgroup.  A CU streams about the same bytes
+// per microsecond however many workgroups share it, so the launch lasts
+// about as long as the busiest CU's share: R whole rounds plus a last round
+// of T row groups cost R + 1 groups on that CU, while the 4T quarters, one
+// per CU, cost R + 1/4.  Used when the quarters fit one per CU (4T <= CUs):
+// on MI355X the split was slower wherever they did not (T = 130 and 160 of
+// 256 CUs).  No workspace: no tail split.
 int plan_tail(GemmParams& p, int rows_per_wg, void* ws, size_t ws_bytes) {
   if (ws == nullptr) return DFLASH_OK;
   if (ws_bytes < kTailWorkspaceBytes) return DFLASH_ERR_WORKSPACE;
@@ -499,7 +503,7 @@ int plan_tail(GemmParams& p, int rows_per_wg, void* ws, size_t ws_bytes) {
   if (cus <= 0 || p.nsplit != 1) return DFLASH_OK;
   const int U = (int)ceil_div(p.N, rows_per_wg);
   const int R = U / cus, T = U - R * cus;
-  if (R < 1 || T == 0 || 4 * T > cus || T > kTailMaxTiles) return DFLASH_OK;
+  if (T == 0 || 4 * T > cus || T > kTailMaxTiles) return DFLASH_OK;
   p.tail_units = 4 * T;
   p.tail_tiles = T;
   p.tail_first = R * cus;
@@ -654,7 +658,8 @@ extern "C" int dflash_weight_tile_bf16(const void* w, int64_t w_row_stride, void
 
 extern "C" int dflash_gemm_bf16_tiled(const void* x, int64_t x_row_stride, const void* w_tiled,
                                       void* out, int64_t out_row_stride, int M, int N, int K,
-                                      int nsplit, int rows_per_wave, int k_waves, void* stream) {
+                                      int nsplit, int rows_per_wave, int k_waves, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
   if (M < 0 || M > 64 || N <= 0 || N % 16 != 0 || K <= 0 || K % kGKStep != 0 || nsplit < 1)
     return DFLASH_ERR_SHAPE;
   if ((rows_per_wave != 16 && rows_per_wave != 32 && rows_per_wave != 64) ||
@@ -683,6 +688,10 @@ extern "C" int dflash_gemm_bf16_tiled(const void* x, int64_t x_row_stride, const
     if (((uintptr_t)out & 7) || (out_row_stride % 4) || out_row_stride < N) return DFLASH_ERR_ALIGN;
     p.out = static_cast<uint16_t*>(out);
     p.os = out_row_stride;
+  }
+  if (k_waves == 4) {
+    const int st = plan_tail(p, rows_per_wave, workspace, workspace_bytes);
+    if (st != DFLASH_OK) return st;
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
@@ -798,7 +807,8 @@ extern "C" int dflash_gemm_bf16_tiled_normed(const void* h, int64_t h_row_stride
                                              int norm_tiles, float eps, float* row_inv_out,
                                              const void* w_tiled, void* out, int64_t out_row_stride,
                                              int M, int N, int K, int nsplit, int rows_per_wave,
-                                             int k_waves, void* stream) {
+                                             int k_waves, void* workspace, size_t workspace_bytes,
+                                             void* stream) {
   if (M < 0 || M > 64 || N <= 0 || N % 16 != 0 || K <= 0 || K % kGKStep != 0 || nsplit < 1)
     return DFLASH_ERR_SHAPE;
   if ((rows_per_wave != 16 && rows_per_wave != 32 && rows_per_wave != 64) || k_waves != 4)
@@ -825,6 +835,8 @@ extern "C" int dflash_gemm_bf16_tiled_normed(const void* h, int64_t h_row_stride
     p.out = static_cast<uint16_t*>(out);
     p.os = out_row_stride;
   }
+  st = plan_tail(p, rows_per_wave, workspace, workspace_bytes);
+  if (st != DFLASH_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e;
   if (rows_per_wave == 16) e = launch_m<1, 4, true, true>(p, s);

@@ -63,7 +63,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dflash_gemm_bf16_swiglu": (_I, [_VP, _I64, _VP, _I64, _VP, _I64, _I, _I, _I, _I, _VP]),
     "dflash_weight_tile_bytes": (_SZ, [_I, _I]),
     "dflash_weight_tile_bf16": (_I, [_VP, _I64, _VP, _I, _I, _VP]),
-    "dflash_gemm_bf16_tiled": (_I, [_VP, _I64, _VP, _VP, _I64, _I, _I, _I, _I, _I, _I, _VP]),
+    "dflash_gemm_bf16_tiled": (
+        _I, [_VP, _I64, _VP, _VP, _I64, _I, _I, _I, _I, _I, _I, _VP, _SZ, _VP]),
     "dflash_gemm_bf16_swiglu_tiled": (
         _I, [_VP, _I64, _VP, _VP, _I64, _I, _I, _I, _I, _VP, _SZ, _VP]),
     "dflash_gemm_tail_workspace_bytes": (_SZ, []),
@@ -71,7 +72,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I, [_VP, _I64, _VP, _I, _I, _I, _VP, _VP, _VP, _I64, _VP, _VP]),
     "dflash_gemm_bf16_tiled_normed": (
         _I, [_VP, _I64, _VP, _VP, _I, ctypes.c_float, _VP, _VP, _VP, _I64, _I, _I, _I, _I, _I, _I,
-             _VP]),
+             _VP, _SZ, _VP]),
     "dflash_gemm_bf16_swiglu_tiled_normed": (
         _I, [_VP, _I64, _VP, _VP, _I, ctypes.c_float, _VP, _VP, _VP, _I64, _I, _I, _I, _I, _VP,
              _SZ, _VP]),

@@ -258,7 +258,7 @@ class HybridVerifyRunner:
         self.bonus = e(B, dt=i32)
         V = cfg.vocab_size
         self.lm_ws = e(max(int(lib.dflash_lm_head_accept_workspace_bytes(B, T, V)), 8), dt=torch.uint8)
-        # the SwiGLU GEMM's tail split: counters zeroed once here, left zeroed by every call
+        # the tiled GEMMs' tail split: counters zeroed once here, left zeroed by every call
         self.gemm_ws = z(int(lib.dflash_gemm_tail_workspace_bytes()), dt=torch.uint8)
         self.capture_layers: tuple[int, ...] = ()
         self.captured = None  # [B*T, len(capture_layers) * H] after set_capture
@@ -367,7 +367,7 @@ class HybridVerifyRunner:
         if self.tiled and name + "_tiled" in lw:
             return ("dflash_gemm_bf16_tiled",
                     (x.data_ptr(), x.stride(0), lw[name + "_tiled"].data_ptr(), out_ptr, out_stride,
-                     M, n, k, ns, rpw, kw))
+                     M, n, k, ns, rpw, kw) + self._gemm_ws(kw))
         w = lw[name]
         # row-major kernel widths; the split count stays the one the consumers
         # were set up for
@@ -389,9 +389,9 @@ class HybridVerifyRunner:
                 (x.data_ptr(), x.stride(0), lw[name + "_tiled"].data_ptr(), M, n, k,
                  self.h.data_ptr(), self.h.data_ptr(), cap, cap_stride, self.row_sumsq.data_ptr()))
 
-    def _gemm_ws(self):
-        """The tail-split workspace of the k_waves 4 SwiGLU GEMMs (none for 1)."""
-        if self.plan["w_gu"][2] != 4:
+    def _gemm_ws(self, k_waves):
+        """The tail-split workspace of the k_waves 4 tiled GEMMs (none for 1)."""
+        if k_waves != 4:
             return (None, 0)
         return (self.gemm_ws.data_ptr(), self.gemm_ws.numel())
 
@@ -525,11 +525,11 @@ class HybridVerifyRunner:
                             self._norm_input(lw["ln_post"]) + (lw[gu_key].data_ptr(),
                                                                self.mlp_act.data_ptr(), I, M, 2 * I,
                                                                H, self.plan["w_gu"][2])
-                            + self._gemm_ws()))
+                            + self._gemm_ws(self.plan["w_gu"][2])))
             elif gu_key:
                 fwd.append(("dflash_gemm_bf16_swiglu_tiled",
                             (self.xn.data_ptr(), H, lw[gu_key].data_ptr(), self.mlp_act.data_ptr(),
-                             I, M, 2 * I, H, self.plan["w_gu"][2]) + self._gemm_ws()))
+                             I, M, 2 * I, H, self.plan["w_gu"][2]) + self._gemm_ws(self.plan["w_gu"][2])))
             else:
                 fwd.append(("dflash_gemm_bf16_swiglu",
                             (self.xn.data_ptr(), H, lw["w_gu_pairs"].data_ptr(), H,

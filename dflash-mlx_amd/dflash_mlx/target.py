@@ -278,7 +278,7 @@ class HybridTargetModel:
             xp, op = x[m0:].data_ptr(), out[m0:].data_ptr()
             if w.lm_head_tiled is not None and self.weight_layout == "tiled":
                 _lib.call("dflash_gemm_bf16_tiled", xp, x.stride(0), w.lm_head_tiled.data_ptr(),
-                          op, V, m, V, H, 1, 64, 4, stream)
+                          op, V, m, V, H, 1, 64, 4, None, 0, stream)
             else:
                 _lib.call("dflash_gemm_bf16", xp, x.stride(0), w.lm_head.data_ptr(), H, op, V, m, V,
                           H, 1, 32, 4, stream)

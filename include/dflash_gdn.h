@@ -574,6 +574,7 @@ int dflash_gemm_bf16_tiled(const void* x, int64_t x_row_stride,
                            const void* w_tiled, void* out,
                            int64_t out_row_stride, int M, int N, int K,
                            int nsplit, int rows_per_wave, int k_waves,
+                           void* workspace, size_t workspace_bytes,
                            void* stream);
 int dflash_gemm_bf16_swiglu_tiled(const void* x, int64_t x_row_stride,
                                   const void* w_pairs_tiled, void* out,
@@ -582,16 +583,17 @@ int dflash_gemm_bf16_swiglu_tiled(const void* x, int64_t x_row_stride,
                                   size_t workspace_bytes, void* stream);
 
 /*
- * Workspace of the SwiGLU GEMMs' tail split (dflash_gemm_bf16_swiglu_tiled
- * and _tiled_normed, k_waves 4): bytes to pass, 256-byte aligned, zeroed
- * once before the first call (every call leaves it zeroed again).  With it,
- * when the 32-row groups (N / 32) make at least one whole round of the
- * device's compute units and leave a last round of T <= CUs / 4 (and <= 64)
- * groups, those T groups run as 4T single-wavefront units of a k-quarter
- * each, merged through the workspace in the workgroup's own k order: the
- * same bits as without it (NULL workspace), in less time.  Calls sharing a
+ * Workspace of the tiled GEMMs' tail split (dflash_gemm_bf16_tiled,
+ * _swiglu_tiled, _tiled_normed, _swiglu_tiled_normed; k_waves 4, one
+ * K split): bytes to pass, 256-byte aligned, zeroed once before the first
+ * call (every call leaves it zeroed again).  With it, when the row groups
+ * (N / rows_per_wave; 32 rows for the SwiGLU forms) leave a last round of
+ * T groups on the device's compute units with 4T <= CUs (and T <= 64),
+ * those T groups run as 4T single-wavefront units of a k-quarter each,
+ * merged through the workspace in the workgroup's own k order: the same
+ * bits as without it (NULL workspace), in less time.  Calls sharing a
  * workspace must not overlap (one stream).  No reference counterpart
- * (scheduling of the MLP gate|up projection, mlx-lm Qwen3NextMLP).
+ * (scheduling of the verify-sized projections).
  */
 size_t dflash_gemm_tail_workspace_bytes(void);
 
@@ -632,6 +634,7 @@ int dflash_gemm_bf16_tiled_normed(const void* h, int64_t h_row_stride,
                                   const void* w_tiled, void* out,
                                   int64_t out_row_stride, int M, int N, int K,
                                   int nsplit, int rows_per_wave, int k_waves,
+                                  void* workspace, size_t workspace_bytes,
                                   void* stream);
 int dflash_gemm_bf16_swiglu_tiled_normed(const void* h, int64_t h_row_stride,
                                          const void* norm_weight,

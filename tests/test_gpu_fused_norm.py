@@ -99,7 +99,7 @@ def test_normed_consumer_bit_identical(device, M, N, K, nsplit, rpw, tiles):
     inv = torch.full((M,), float("nan"), device=device)
     _lib.call("dflash_gemm_bf16_tiled_normed", h.data_ptr(), K, nw.data_ptr(), sumsq.data_ptr(),
               tiles, EPS, inv.data_ptr(), wt.data_ptr(), got.data_ptr(), N, M, N, K, nsplit, rpw, 4,
-              st)
+              None, 0, st)
     torch.cuda.synchronize()
     _check_inv(inv, sumsq, K)
     # one row alone: the same inverse RMS bits
@@ -107,12 +107,13 @@ def test_normed_consumer_bit_identical(device, M, N, K, nsplit, rpw, tiles):
     got1 = torch.empty((used, 1, N) if nsplit > 1 else (1, N), device=device).to(dt)
     s1 = sumsq[:, :1].contiguous()
     _lib.call("dflash_gemm_bf16_tiled_normed", h.data_ptr(), K, nw.data_ptr(), s1.data_ptr(), tiles,
-              EPS, inv1.data_ptr(), wt.data_ptr(), got1.data_ptr(), N, 1, N, K, nsplit, rpw, 4, st)
+              EPS, inv1.data_ptr(), wt.data_ptr(), got1.data_ptr(), N, 1, N, K, nsplit, rpw, 4, None,
+              0, st)
     # the plain GEMM of y formed by torch with the kernel's inv
     y = ((h.float() * inv[:, None]) * nw.float()).bfloat16()
     ref = torch.full(shape, float("nan"), device=device).to(dt)
     _lib.call("dflash_gemm_bf16_tiled", y.data_ptr(), K, wt.data_ptr(), ref.data_ptr(), N, M, N, K,
-              nsplit, rpw, 4, st)
+              nsplit, rpw, 4, None, 0, st)
     torch.cuda.synchronize()
     assert torch.equal(inv1, inv[:1])
     assert torch.equal(got, ref)
@@ -158,12 +159,12 @@ def test_fused_norm_entry_points_reject_bad_arguments(device):
     # k_waves other than 4 for the normed consumer
     assert lib.dflash_gemm_bf16_tiled_normed(x.data_ptr(), 256, x.data_ptr(), ss.data_ptr(), 16,
                                              EPS, None, wt.data_ptr(), x.data_ptr(), 256, 16, 256,
-                                             256, 1, 32, 1, st) != 0
+                                             256, 1, 32, 1, None, 0, st) != 0
     # K beyond the staged norm weight
     assert lib.dflash_gemm_bf16_tiled_normed(x.data_ptr(), 32768, x.data_ptr(), ss.data_ptr(), 16,
                                              EPS, None, wt.data_ptr(), x.data_ptr(), 256, 16, 256,
-                                             32768, 1, 32, 4, st) != 0
+                                             32768, 1, 32, 4, None, 0, st) != 0
     # no row tiles
     assert lib.dflash_gemm_bf16_tiled_normed(x.data_ptr(), 256, x.data_ptr(), ss.data_ptr(), 0,
                                              EPS, None, wt.data_ptr(), x.data_ptr(), 256, 16, 256,
-                                             256, 1, 32, 4, st) != 0
+                                             256, 1, 32, 4, None, 0, st) != 0

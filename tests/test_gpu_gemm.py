@@ -165,7 +165,7 @@ def test_gemm_tiled_bit_identical(device, N, K, nsplit, rpw, kw):
     t = _tile(device, w)
     out_t = torch.full_like(out, float("nan"))
     _lib.call("dflash_gemm_bf16_tiled", x.data_ptr(), K, t.data_ptr(), out_t.data_ptr(), N, M, N, K,
-              nsplit, rpw, kw, _lib.stream_handle(device))
+              nsplit, rpw, kw, None, 0, _lib.stream_handle(device))
     torch.cuda.synchronize()
     assert torch.equal(out_t, out)
 
@@ -184,7 +184,7 @@ def test_gemm_tiled_64_rows_per_wave(device, M, N, K, nsplit, kw):
     out = (torch.full((used, M, N), float("nan"), device=device) if nsplit > 1 else
            torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=device))
     _lib.call("dflash_gemm_bf16_tiled", x.data_ptr(), K, t.data_ptr(), out.data_ptr(), N, M, N, K,
-              nsplit, 64, kw, _lib.stream_handle(device))
+              nsplit, 64, kw, None, 0, _lib.stream_handle(device))
     torch.cuda.synchronize()
     ref = _ref(x, w)
     scale = ref.pow(2).mean().sqrt().item()
@@ -216,5 +216,7 @@ def test_gemm_tiled_rejects_bad_arguments(device):
     lib = _lib.load()
     assert lib.dflash_weight_tile_bytes(40, 64) == 0          # N % 16
     assert lib.dflash_weight_tile_bf16(None, 64, None, 40, 64, None) == -2
-    assert lib.dflash_gemm_bf16_tiled(None, 64, None, None, 64, 16, 40, 64, 1, 32, 4, None) == -2
-    assert lib.dflash_gemm_bf16_tiled(None, 64, None, None, 64, 16, 48, 64, 1, 48, 4, None) == -3
+    assert lib.dflash_gemm_bf16_tiled(None, 64, None, None, 64, 16, 40, 64, 1, 32, 4, None, 0,
+                                      None) == -2
+    assert lib.dflash_gemm_bf16_tiled(None, 64, None, None, 64, 16, 48, 64, 1, 48, 4, None, 0,
+                                      None) == -3

@@ -1,5 +1,5 @@
-"""The SwiGLU GEMMs' tail split (dflash_gemm_bf16_swiglu_tiled and
-dflash_gemm_bf16_swiglu_tiled_normed with a workspace).
+"""The tiled GEMMs' tail split (dflash_gemm_bf16_tiled, _swiglu_tiled,
+_tiled_normed and _swiglu_tiled_normed with a workspace).
 
 With the workspace, the row groups of a short last round run as single-wave
 k-quarter units merged through the workspace in the workgroup's own k order,
@@ -7,8 +7,10 @@ so the output must be the same bits as the call without a workspace (itself
 bit-identical to the row-major GEMM and within one bf16 rounding of fp32
 torch, tests/test_gpu_gemm.py).  Shapes are chosen from the device's CU count
 so that the split engages: the config-c4 gate|up (N = 18432: 576 groups, a
-last round of 64 on 256 CUs), one group past a whole round, every M tile
-count (1..4), and K of 2 k-steps (two of the four quarters empty).  The
+last round of 64 on 256 CUs), in_proj and q/k/v at 16 rows a wave, last
+rounds from one group to a quarter of the CUs with and without whole rounds
+before them, every wave width (16, 32, 64 rows), every M tile count (1..4),
+and K of 2 k-steps (two of the four quarters empty).  The
 workspace counters must be zero after every call, with stale partial sums
 (NaN) in the workspace before the first, across calls of shrinking M, and
 across graph replays.
@@ -30,16 +32,19 @@ def _cus(device):
     return torch.cuda.get_device_properties(device).multi_processor_count
 
 
+COUNT_BYTES = 1024  # the workspace's first 1 KB holds the row-group counters
+
+
 def _workspace(device, stale=True):
     lib = _lib.load()
     ws = torch.zeros(int(lib.dflash_gemm_tail_workspace_bytes()), dtype=torch.uint8, device=device)
     if stale:  # partial sums left by nobody: NaN, counters zero
-        ws[256:].view(torch.float32).fill_(float("nan"))
+        ws[COUNT_BYTES:].view(torch.float32).fill_(float("nan"))
     return ws
 
 
 def _counters_zero(ws):
-    return bool((ws[:256] == 0).all().item())
+    return bool((ws[:COUNT_BYTES] == 0).all().item())
 
 
 def _pairs_tiled(device, I, K, seed):
@@ -79,6 +84,46 @@ def test_tail_split_bit_identical(device):
         got = _swiglu(device, x, wt, I, K, ws)
         torch.cuda.synchronize()
         assert torch.equal(got, ref), (M, I, K)
+        assert _counters_zero(ws)
+
+
+def _plain_shapes(device):
+    """(M, N, K, rows_per_wave): last rounds of one group to a quarter of the
+    CUs, with and without whole rounds before them, every wave width, a
+    partial last group; and shapes past the quarter (no split engages)."""
+    cus = _cus(device)
+    q = min(cus // 4, 64)
+    return [(16, 12352, 2560, 16), (16, 5120, 2560, 16), (16, 12352, 2560, 32),
+            (16, 5120, 2560, 32), (37, 16 * q, 512, 16), (64, 64 * (cus + q), 256, 64),
+            (1, 32 * (2 * cus + 1), 128, 32), (20, 64 * q - 48, 640, 64)]
+
+
+@pytest.mark.parametrize("normed", [False, True])
+def test_tail_split_plain_bit_identical(device, normed):
+    ws = _workspace(device)
+    st = _lib.stream_handle(device)
+    for M, N, K, rpw in _plain_shapes(device):
+        print(f"[gemm tail plain] normed={normed} M={M} N={N} K={K} rpw={rpw}", flush=True)
+        g = torch.Generator(device=device).manual_seed(M * 13 + N + rpw)
+        x = torch.randn(M, K, generator=g, device=device).bfloat16()
+        wt = tile_weight((0.02 * torch.randn(N, K, generator=g, device=device)).bfloat16())
+        nw = (1.0 + 0.1 * torch.randn(K, generator=g, device=device)).bfloat16()
+        sumsq = (K / 16) * (0.5 + torch.rand(16, M, generator=g, device=device))
+        outs = []
+        for w in (None, ws):
+            out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=device)
+            wsp, wsn = (w.data_ptr(), w.numel()) if w is not None else (None, 0)
+            if normed:
+                _lib.call("dflash_gemm_bf16_tiled_normed", x.data_ptr(), K, nw.data_ptr(),
+                          sumsq.data_ptr(), 16, EPS, None, wt.data_ptr(), out.data_ptr(), N, M, N,
+                          K, 1, rpw, 4, wsp, wsn, st)
+            else:
+                _lib.call("dflash_gemm_bf16_tiled", x.data_ptr(), K, wt.data_ptr(), out.data_ptr(),
+                          N, M, N, K, 1, rpw, 4, wsp, wsn, st)
+            outs.append(out)
+        torch.cuda.synchronize()
+        assert not torch.isnan(outs[0].float()).any()
+        assert torch.equal(outs[1], outs[0]), (M, N, K, rpw)
         assert _counters_zero(ws)
 
 
@@ -162,7 +207,7 @@ def test_tail_split_graph_replays(device):
 def test_tail_workspace_validation(device):
     lib = _lib.load()
     need = int(lib.dflash_gemm_tail_workspace_bytes())
-    assert need >= 256 + 64 * 4 * 1024
+    assert need >= COUNT_BYTES + 64 * 4 * 16 * 1024
     x = torch.zeros(16, 128, dtype=torch.bfloat16, device=device)
     wt = torch.zeros(64 * 128, dtype=torch.bfloat16, device=device)
     out = torch.zeros(16, 32, dtype=torch.bfloat16, device=device)
