@@ -126,25 +126,45 @@ __device__ __forceinline__ u32x4 norm8(u32x4 h, u32x4 w, float inv) {
 
 __device__ __forceinline__ float bf16r(float x) { return bf16_bits_to_f32(f32_to_bf16_rne(x)); }
 
+// The fin epilogue's residual values, lane (r16, g) of tile (vt, mt):
+// resid[m = mt*16 + r16][n = nwave + vt*16 + 4g .. +3] (rows past M and
+// tiles past N read clamped addresses; those lanes store nothing).  Loaded
+// by wave 0 ahead of its weight ring, so the epilogue does not wait on a
+// memory round trip of its own.
+template <int MT, int VT>
+__device__ __forceinline__ void residual_load(const GemmParams& p, u32x2 (&rr)[MT][VT], int nwave,
+                                              int lane) {
+  const int r16 = lane & 15;
+  const int g = lane >> 4;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int mc = min(mt * 16 + r16, p.M - 1);
+#pragma unroll
+    for (int vt = 0; vt < VT; ++vt) {
+      const int n = min(nwave + vt * 16, p.N - 16) + 4 * g;
+      rr[mt][vt] = *reinterpret_cast<const u32x2*>(p.resid + (int64_t)mc * p.N + n);
+    }
+  }
+}
+
 // The fin epilogue (KW 8 or 16): wave 0 holds the workgroup's whole tile.
 // Lane (r16, g) of tile (vt, mt) holds out[m = mt*16 + r16][n = nwave +
 // vt*16 + 4g .. +3].
 template <int MT, int VT>
 __device__ __forceinline__ void residual_tile(const GemmParams& p, const f32x4 (&acc)[VT][MT],
-                                              int nwave, int lane) {
+                                              const u32x2 (&rres)[MT][VT], int nwave, int lane) {
   const int r16 = lane & 15;
   const int g = lane >> 4;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = mt * 16 + r16;
     const bool mv = m < p.M;
-    const int mc = mv ? m : p.M - 1;
 #pragma unroll
     for (int vt = 0; vt < VT; ++vt) {
       const int n = nwave + vt * 16 + 4 * g;
       if (n >= p.N) continue;  // N % 16 == 0: whole 16-column tiles
       float ss = 0.f;
-      const u32x2 rr = *reinterpret_cast<const u32x2*>(p.resid + (int64_t)mc * p.N + n);
+      const u32x2 rr = rres[mt][vt];
       float v[4] = {bf16_lo(rr.x), bf16_hi(rr.x), bf16_lo(rr.y), bf16_hi(rr.y)};
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = bf16r(v[i] + bf16r(acc[vt][mt][i]));
@@ -279,6 +299,9 @@ __global__ __launch_bounds__(KW >= 8 ? 64 * KW : kGThreads) void skinny_gemm_ker
     for (int mt = 0; mt < MT; ++mt) acc[vt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   unsigned char* tile = atile[wave];
 
+  u32x2 rres[MT][VT] = {};
+  if (KW >= 8 && p.fin && wave == 0) residual_load<MT, VT>(p, rres, nwave, lane);
+
   GStage<MT, VT> ring[D];
 #pragma unroll
   for (int d = 0; d < D; ++d)
@@ -408,7 +431,7 @@ __global__ __launch_bounds__(KW >= 8 ? 64 * KW : kGThreads) void skinny_gemm_ker
         for (int mt = 0; mt < MT; ++mt) acc[vt][mt] += red[q][vt * MT + mt][lane];
   }
   if (KW >= 8 && p.fin) {
-    residual_tile<MT, VT>(p, acc, nwave, lane);
+    residual_tile<MT, VT>(p, acc, rres, nwave, lane);
     return;
   }
   // Lane (r16, g) of tile (vt, mt) holds out[m = mt*16 + r16][n = nwave + vt*16 + 4g .. +3].
