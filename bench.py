@@ -89,7 +89,9 @@ def probe(torch, fused, explicit) -> int:
     for _ in range(3):
         explicit.scan()
     for _ in range(3):
-        if fused.argmax_in_scan:
+        if fused.single_launch:
+            fused.step_single()
+        elif fused.argmax_in_scan:
             fused.scan_rolled_argmax()
         else:
             fused.scan_rolled()
@@ -608,11 +610,17 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
 
     K = steps
     print(f"[bench] {cfg.name}: timing {K} fused + {K} explicit steps", file=sys.stderr, flush=True)
-    # The phases of run_fused(): with small logits the accept's argmax runs in
-    # the scan's launch, otherwise in a launch of its own after it.
+    # The phases of run_fused(): with small logits the whole step is one
+    # launch (the accept's argmax workgroups in the scan's launch, the last of
+    # each sequence finishing the accept and the conv windows), otherwise the
+    # argmax runs in a launch of its own after the scan.
+    single = fused.single_launch
     in_scan = fused.argmax_in_scan
-    lead = "scan_argmax" if in_scan else "scan"
-    if in_scan:
+    lead = "step" if single else ("scan_argmax" if in_scan else "scan")
+    if single:
+        tf = time_steps(torch, K, [(lead, fused.step_launch)] + (
+            [] if fused.conv_in_launch else [("conv_rollback", fused.conv_rollback)]))
+    elif in_scan:
         tf = time_steps(torch, K, [(lead, fused.scan_rolled_argmax),
                                    ("accept_rollback", fused.accept_keys_conv_rollback)])
     else:
@@ -623,7 +631,10 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
     # The same fused step as the device-driven serving loop launches it: captured
     # once as a HIP graph (no host work inside), W replays untimed, then K replays
     # between synchronizes.  The eager per-phase timing above is the breakdown.
-    print(f"[bench] {cfg.name}: timing {K} graph replays of the fused step", file=sys.stderr,
+    # The graph holds two steps: the keep counts alternate between two buffers
+    # (each step reads one and writes the other), so K steps are K / 2 replays.
+    K2 = max(1, K // 2)
+    print(f"[bench] {cfg.name}: timing {K2} graph replays of two fused steps", file=sys.stderr,
           flush=True)
     cap = torch.cuda.Stream(device=dev)
     cap.wait_stream(torch.cuda.current_stream(dev))
@@ -631,19 +642,20 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=cap):
         fused.run_fused()
+        fused.run_fused()
     torch.cuda.synchronize()
-    for _ in range(warmup):
+    for _ in range(max(1, warmup // 2)):
         graph.replay()
     torch.cuda.synchronize()
     g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     g0.record()
-    for _ in range(K):
+    for _ in range(K2):
         graph.replay()
     g1.record()
     torch.cuda.synchronize()
-    tg = {"ms_per_step": (time.perf_counter() - t0) * 1e3 / K,
-          "gpu_step": g0.elapsed_time(g1) * 1e3 / K}
+    tg = {"ms_per_step": (time.perf_counter() - t0) * 1e3 / (2 * K2),
+          "gpu_step": g0.elapsed_time(g1) * 1e3 / (2 * K2)}
     del graph
 
     # Algorithmic HBM bytes.  Scan: bf16 q,k,v,out + fp32 g,beta + fp32 state
@@ -661,12 +673,18 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
     tokens = B * T
 
     # The dominant launch: the scan + tape, with the accept's argmax workgroups
-    # (which read the verify logits once) when they share its launch.
-    launch_bytes = scan_fused_bytes + (accept_bytes if in_scan else 0)
+    # (which read the verify logits once) when they share its launch, and the
+    # conv windows when the whole step is that launch.
+    conv_inl = single and fused.conv_in_launch  # the conv windows copied in the step's launch
+    launch_bytes = (scan_fused_bytes + (accept_bytes if in_scan else 0)
+                    + (conv_bytes if conv_inl else 0))
     achieved = launch_bytes / (tf[lead] / 1e6) / 1e9
     roof = {
         "bound": "hbm",
-        "kernel": ("gdn_scan_kernel<DK,R> + accept argmax workgroups via "
+        "kernel": ("gdn_scan_kernel<DK,R> + accept argmax workgroups finishing the accept"
+                   + (" and the conv windows" if conv_inl else "") + " via dflash_gdn_verify_step")
+                  if single else
+                  ("gdn_scan_kernel<DK,R> + accept argmax workgroups via "
                    "dflash_gdn_verify_scan_rollback_argmax") if in_scan else
                   "gdn_scan_kernel<DK,R> via dflash_gdn_verify_scan_rollback",
         "achieved": round(achieved, 1),
@@ -691,13 +709,20 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
             "accept": "drafts block[1:] vs posterior rows 0..T-2, bonus = posterior[matched], "
                       "keep = matched + 1 (runtime.py:145-147)",
             "step": ("fused: scan+tape with the previous step's state rollback in its load, "
+                     "the greedy accept's argmax slices as extra workgroups, the last of each "
+                     "sequence's merging the keys and writing matched / bonus / keep"
+                     + (" and copying the conv windows (1 launch)" if conv_inl else
+                        " (1 launch) -> the conv-window copy (1 launch)")
+                     + "; HIP graph of two steps (keep buffers alternate), replayed K/2 times")
+                    if single else
+                    ("fused: scan+tape with the previous step's state rollback in its load, "
                      "with the greedy accept's argmax slices in the same launch -> the accept's "
                      "finalize inside the conv-window rollback copy, which also writes keep "
-                     "(2 launches), replayed as one HIP graph") if in_scan else
+                     "(2 launches); HIP graph of two steps, replayed K/2 times") if in_scan else
                     ("fused: scan+tape with the previous step's state rollback in its load -> "
                      "the greedy accept's argmax slices -> its finalize inside the conv-window "
                      "rollback copy, which also writes keep (3 launches; logits above "
-                     "ARGMAX_IN_SCAN_MAX_BYTES), replayed as one HIP graph"),
+                     "ARGMAX_IN_SCAN_MAX_BYTES); HIP graph of two steps, replayed K/2 times"),
         },
         "roofline": roof,
         "graph_step_us": round(tg["gpu_step"], 2),

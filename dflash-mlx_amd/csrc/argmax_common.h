@@ -63,11 +63,13 @@ __device__ __forceinline__ uint64_t key16<F16Tag>(u32x4 raw, int idx, uint64_t b
 }
 
 // One workgroup of kArgmaxThreads threads: the key of slice `split` of logits
-// row `row` (sequence row / N, position row % N) to keys[row * splits + split].
+// row `row` (sequence row / N, position row % N) to keys[row * splits + split],
+// stored by thread 0 (agent_store: with an agent-scope store, for a reader in
+// another workgroup of the same launch).
 template <typename T, bool VECTOR>
 __device__ __forceinline__ void argmax_partial_block(
     const T* __restrict__ logits, int64_t bstride, int64_t rstride, int N, int V, int chunk,
-    int splits, uint64_t* __restrict__ keys, int row, int split) {
+    int splits, uint64_t* __restrict__ keys, int row, int split, bool agent_store = false) {
   const int b = row / N;
   const int i = row - b * N;
   const T* base = logits + (int64_t)b * bstride + (int64_t)i * rstride;
@@ -107,7 +109,11 @@ __device__ __forceinline__ void argmax_partial_block(
     uint64_t m = wbest[0];
 #pragma unroll
     for (int w = 1; w < kArgmaxThreads / 64; ++w) m = u64_max(m, wbest[w]);
-    keys[(int64_t)row * splits + split] = m;
+    if (agent_store)
+      __hip_atomic_store(keys + (int64_t)row * splits + split, m, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    else
+      keys[(int64_t)row * splits + split] = m;
   }
 }
 

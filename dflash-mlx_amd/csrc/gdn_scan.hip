@@ -24,6 +24,7 @@
 #include <type_traits>
 
 #include "argmax_common.h"
+#include "conv_window.h"
 #include "dflash_gdn.h"
 #include "device_common.h"
 #include "gdn_prologue_math.h"
@@ -89,6 +90,21 @@ struct ScanParams {
   const void* acc_logits;
   int64_t acc_bs, acc_rs;
   uint64_t* acc_keys;
+  // The accept's finalize and the conv-window rollback in the same launch
+  // (fin_count null: off; see accept_finish).  Sequence b's accepted count
+  // a = clamp(matched + fin_offset, 0, fin_T) goes to fin_keep[b], which the
+  // scan of this launch does not read (sel_accepted is another buffer).
+  int* fin_count;  // [acc rows / acc_N] arrival counts, zero between calls
+  const int32_t* fin_draft;
+  int64_t fin_dstride;
+  int fin_ndraft, fin_offset, fin_T;
+  int32_t* fin_posterior;
+  int32_t* fin_matched;
+  int32_t* fin_bonus;
+  int32_t* fin_keep;
+  int fin_L, fin_K1;
+  int64_t fin_Cu, fin_qbs, fin_qrs;  // 16-byte units
+  ConvTable fin_conv;
 };
 
 // Tokens per block the on-the-fly prologue supports (its LDS is sized for it).
@@ -312,7 +328,136 @@ struct ProPhase {
 // own loads.
 // PRO: the layer prologue runs at each item's start (pro_phase) and the
 // token loop reads its inputs from LDS.
-template <int DK, int R, int PF, bool PRO = false, int KT = 0>
+// Rows of one sequence the in-launch accept finalize holds (its LDS), and
+// the conv window rows it copies at most.
+constexpr int kFinMaxRows = 64;
+constexpr int kFinConvRows = 4;
+
+// The accept's last step inside the scan's launch, run by each argmax
+// workgroup after it stored its key (agent-scope): the workgroup waits for
+// that store, counts itself in fin_count[b], and the last of sequence b's
+// N * splits argmax workgroups to arrive puts the count back to zero and
+// finishes the sequence alone, while the scan's workgroups run on:
+//   - merges the N x splits keys (agent-scope loads: the other workgroups'
+//     stores completed before they counted themselves), as
+//     accept_conv_rollback_kernel does (16 lanes per row, order-free max);
+//   - matched = the first position where the draft differs from the
+//     posterior, bonus = posterior[matched] (dflash_mlx/runtime.py:41-47,
+//     :145-147), posterior / matched / bonus and the keep count
+//     a = clamp(matched + fin_offset, 0, fin_T) stored;
+//   - the new conv window of every layer: rows a .. a+K1-1 of
+//     concat(conv_in, qkv) (custom_qwen35_model.py:1044-1051), 16-byte
+//     units, four units per lane loaded before any is stored.
+// No workgroup waits on another.
+__device__ __forceinline__ void accept_finish(const ScanParams& p, int row) {
+  __shared__ int fin_last, fin_first;
+  __shared__ int32_t post[kFinMaxRows];
+  const int N = p.acc_N;
+  const int b = row / N;
+  if (threadIdx.x == 0) {
+    __builtin_amdgcn_s_waitcnt(0);  // this workgroup's key store has completed
+    const int old = __hip_atomic_fetch_add(p.fin_count + b, 1, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    fin_last = old == N * p.acc_splits - 1;
+  }
+  __syncthreads();
+  if (!fin_last) return;
+  if (threadIdx.x == 0)
+    __hip_atomic_store(p.fin_count + b, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int mlen = min(p.fin_ndraft, N);
+  int draft0 = 0;  // draft token `lane` of the first 64 (wavefront 0)
+  if (wave == 0 && lane < mlen) draft0 = p.fin_draft[(int64_t)b * p.fin_dstride + lane];
+  const int sub = threadIdx.x & 15;
+  const int splits = p.acc_splits;
+  for (int r0 = 0; r0 < N; r0 += 16) {
+    const int r = r0 + (threadIdx.x >> 4);
+    uint64_t m = 0;
+    if (r < N) {
+      const uint64_t* kr = p.acc_keys + ((int64_t)b * N + r) * splits;
+      for (int s0 = sub; s0 < splits; s0 += 16 * 8) {
+        uint64_t v[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          v[i] = __hip_atomic_load(kr + min(s0 + 16 * i, splits - 1), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = u64_max(m, v[i]);
+      }
+    }
+#pragma unroll
+    for (int off = 8; off >= 1; off >>= 1) {
+      const uint32_t lo = __shfl_xor((unsigned)(m & 0xffffffffu), off, 16);
+      const uint32_t hi = __shfl_xor((unsigned)(m >> 32), off, 16);
+      m = u64_max(m, ((uint64_t)hi << 32) | lo);
+    }
+    if (sub == 0 && r < N) post[r] = argmax_key_index(m);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    int first = mlen;
+    for (int base0 = 0; base0 < mlen; base0 += 64) {
+      const int j = base0 + lane;
+      const int dj = base0 == 0 ? draft0 : (j < mlen ? p.fin_draft[(int64_t)b * p.fin_dstride + j] : 0);
+      const bool mismatch = (j < mlen) && (dj != post[j]);
+      const unsigned long long mask = __ballot(mismatch);
+      if (mask != 0ull) {
+        first = base0 + __ffsll(mask) - 1;
+        break;
+      }
+    }
+    if (lane == 0) fin_first = first;
+  }
+  __syncthreads();
+  const int first = fin_first;
+  const int a = min(max(first + p.fin_offset, 0), p.fin_T);
+  if (p.fin_posterior != nullptr)
+    for (int r = threadIdx.x; r < N; r += 256) p.fin_posterior[(int64_t)b * N + r] = post[r];
+  if (threadIdx.x == 0) {
+    if (p.fin_matched != nullptr) p.fin_matched[b] = first;
+    if (p.fin_bonus != nullptr) p.fin_bonus[b] = first < N ? post[first] : -1;
+    p.fin_keep[b] = a;
+  }
+  // conv windows: unit e of the flattened (layer, column unit) range
+  const int K1 = p.fin_K1;
+  const int64_t Cu = p.fin_Cu, units = (int64_t)p.fin_L * Cu;
+  constexpr int kU = 4;
+  for (int64_t e0 = threadIdx.x; e0 < units; e0 += 256 * kU) {
+    u32x4 vals[kU][kFinConvRows];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t e = min(e0 + 256 * u, units - 1);
+      const int l = (int)(e / Cu);
+      const int64_t c = e - (int64_t)l * Cu;
+      const u32x4* cin = reinterpret_cast<const u32x4*>(p.fin_conv.cin[l]) + (int64_t)b * K1 * Cu + c;
+      const u32x4* qkv = reinterpret_cast<const u32x4*>(p.fin_conv.qkv[l]) + (int64_t)b * p.fin_qbs + c;
+#pragma unroll
+      for (int r = 0; r < kFinConvRows; ++r) {
+        if (r < K1) {
+          const int j = a + r;
+          vals[u][r] = j < K1 ? cin[(int64_t)j * Cu] : qkv[(int64_t)(j - K1) * p.fin_qrs];
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int64_t e = e0 + 256 * u;
+      if (e < units) {
+        const int l = (int)(e / Cu);
+        const int64_t c = e - (int64_t)l * Cu;
+        u32x4* cout = reinterpret_cast<u32x4*>(p.fin_conv.cout[l]) + (int64_t)b * K1 * Cu + c;
+#pragma unroll
+        for (int r = 0; r < kFinConvRows; ++r)
+          if (r < K1) cout[(int64_t)r * Cu] = vals[u][r];
+      }
+    }
+  }
+}
+
+// FIN: the argmax workgroups finish the accept (accept_finish); its own
+// instantiations, so the other scans keep their register budget.
+template <int DK, int R, int PF, bool PRO = false, int KT = 0, bool FIN = false>
 __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
   constexpr int VEC = (DK % 64 == 0) ? 4 : 2;
   constexpr int NCH = DK / (16 * VEC);
@@ -330,14 +475,18 @@ __global__ __launch_bounds__(256) void gdn_scan_kernel(const ScanParams p) {
     const int a = bid - nblk;
     const int row = a / p.acc_splits;
     const int split = a - row * p.acc_splits;
+    const bool fin = FIN && p.fin_count != nullptr;
     if (p.acc_bf16)
       argmax_partial_block<uint16_t, true>(static_cast<const uint16_t*>(p.acc_logits), p.acc_bs,
                                            p.acc_rs, p.acc_N, p.acc_V, p.acc_chunk, p.acc_splits,
-                                           p.acc_keys, row, split);
+                                           p.acc_keys, row, split, fin);
     else
       argmax_partial_block<float, true>(static_cast<const float*>(p.acc_logits), p.acc_bs,
                                         p.acc_rs, p.acc_N, p.acc_V, p.acc_chunk, p.acc_splits,
-                                        p.acc_keys, row, split);
+                                        p.acc_keys, row, split, fin);
+    if constexpr (FIN && !PRO) {
+      if (fin) accept_finish(p, row);
+    }
     return;
   }
   int item_begin = bid, item_end = p.items, item_step = nblk;
@@ -557,6 +706,12 @@ hipError_t launch_dk(const ScanParams& base, int R, int grid, int xcd, hipStream
     }
     return hipGetLastError();
   }
+  if (p.fin_count != nullptr) {
+    if (R != 1) return hipErrorInvalidValue;
+    if (deep) hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 4, false, 0, true>), dim3(total), dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 1, false, 0, true>), dim3(total), dim3(256), 0, s, p);
+    return hipGetLastError();
+  }
   switch (R * (deep ? 10 : 1)) {
     case 1: hipLaunchKernelGGL((gdn_scan_kernel<DK, 1, 1>), dim3(total), dim3(256), 0, s, p); break;
     case 2: hipLaunchKernelGGL((gdn_scan_kernel<DK, 2, 1>), dim3(total), dim3(256), 0, s, p); break;
@@ -608,11 +763,24 @@ struct AcceptArgs {
   uint64_t* keys;
 };
 
+// The accept's finalize + conv rollback run in the launch (ScanParams::fin_*).
+struct FinishArgs {
+  int* count;
+  const int32_t* draft;
+  int64_t dstride;
+  int n_draft, offset, T;
+  int32_t *posterior, *matched, *bonus, *keep;
+  int L, K1;
+  int64_t Cu, qbs, qrs;
+  ConvTable conv;
+};
+
 int scan_impl(const void* q, const void* k, const void* v, const float* g,
               const float* beta, const float* state_in, void* out,
               float* final_state, float* tape, const int32_t* lengths, int B,
               int T, int Hk, int Hv, int Dk, int Dv, const int64_t* strides,
-              const Select* sel, void* stream, const AcceptArgs* acc = nullptr) {
+              const Select* sel, void* stream, const AcceptArgs* acc = nullptr,
+              const FinishArgs* fin = nullptr) {
   if (B < 0 || T < 0 || Hk <= 0 || Hv <= 0 || Dk <= 0 || Dv <= 0) return DFLASH_ERR_SHAPE;
   if (Hv % Hk != 0) return DFLASH_ERR_SHAPE;
   if (Dv % 16 != 0) return DFLASH_ERR_UNSUPPORTED;
@@ -706,6 +874,24 @@ int scan_impl(const void* q, const void* k, const void* v, const float* g,
     p.acc_bs = acc->bs;
     p.acc_rs = acc->rs;
     p.acc_keys = acc->keys;
+    if (fin != nullptr) {
+      p.fin_count = fin->count;
+      p.fin_draft = fin->draft;
+      p.fin_dstride = fin->dstride;
+      p.fin_ndraft = fin->n_draft;
+      p.fin_offset = fin->offset;
+      p.fin_T = fin->T;
+      p.fin_posterior = fin->posterior;
+      p.fin_matched = fin->matched;
+      p.fin_bonus = fin->bonus;
+      p.fin_keep = fin->keep;
+      p.fin_L = fin->L;
+      p.fin_K1 = fin->K1;
+      p.fin_Cu = fin->Cu;
+      p.fin_qbs = fin->qbs;
+      p.fin_qrs = fin->qrs;
+      p.fin_conv = fin->conv;
+    }
   }
   const int R = pick_rows(Dv);
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -852,6 +1038,84 @@ extern "C" int dflash_gdn_verify_scan_rollback_argmax(
   const Select sel{prev_tape, prev_accepted, state, prev_T, accepted_period};
   return scan_impl(q, k, v, g, beta, state, out, final_state, tape, nullptr, B, T, Hk, Hv, Dk, Dv,
                    strides, &sel, stream, &acc);
+}
+
+namespace dflash {
+namespace {
+// Bytes of the argmax keys in the single-launch step's workspace (the arrival
+// counts follow, 256-byte aligned).
+size_t step_keys_bytes(int B, int N, int V) {
+  return (size_t)ceil_div((int64_t)dflash_greedy_accept_workspace_bytes(B, N, V), 256) * 256;
+}
+}  // namespace
+}  // namespace dflash
+
+extern "C" size_t dflash_gdn_verify_step_workspace_bytes(int B, int N, int V) {
+  if (B <= 0 || N <= 0 || V <= 0) return 0;
+  return dflash::step_keys_bytes(B, N, V) + sizeof(int) * (size_t)B;
+}
+
+extern "C" int dflash_gdn_verify_step(
+    const void* q, const void* k, const void* v, const float* g, const float* beta,
+    float* state, const float* prev_tape, const int32_t* prev_accepted, int prev_T,
+    int accepted_period, void* out, float* final_state, float* tape, int B, int T, int Hk,
+    int Hv, int Dk, int Dv, const int64_t* strides, const void* logits, int logits_dtype,
+    int64_t logits_batch_stride, int64_t logits_row_stride, int accept_B, int N, int V,
+    const int32_t* draft, int64_t draft_stride, int n_draft, int32_t* posterior,
+    int32_t* matched, int32_t* bonus, int accepted_offset, int32_t* accepted_out,
+    const void* const* conv_in, const void* const* qkv, void* const* conv_out, int L, int K1,
+    int64_t C, int64_t qkv_batch_stride, int64_t qkv_row_stride, void* workspace,
+    size_t workspace_bytes, void* stream) {
+  using namespace dflash;
+  if (state == nullptr || accepted_out == nullptr) return DFLASH_ERR_NULL;
+  if (final_state != nullptr && final_state == state) return DFLASH_ERR_SHAPE;
+  if (accept_B <= 0 || N <= 0 || V <= 0 || (int64_t)accept_B * N > 16384 || n_draft < 0)
+    return DFLASH_ERR_SHAPE;
+  if (B <= 0 || T <= 0 || L < 0 || (L > 0 && (K1 <= 0 || C <= 0))) return DFLASH_ERR_SHAPE;
+  // the keep count this launch writes must not be the one its scan reads
+  if (prev_T > 0 && accepted_out == prev_accepted) return DFLASH_ERR_SHAPE;
+  if (N > kFinMaxRows || K1 > kFinConvRows || L > kMaxLayersPerLaunch) return DFLASH_ERR_UNSUPPORTED;
+  if (logits == nullptr || workspace == nullptr) return DFLASH_ERR_NULL;
+  if (n_draft > 0 && draft == nullptr) return DFLASH_ERR_NULL;
+  if (logits_dtype != DFLASH_DTYPE_F32 && logits_dtype != DFLASH_DTYPE_BF16)
+    return DFLASH_ERR_UNSUPPORTED;
+  if (workspace_bytes < dflash_gdn_verify_step_workspace_bytes(accept_B, N, V))
+    return DFLASH_ERR_WORKSPACE;
+  const int per = logits_dtype == DFLASH_DTYPE_F32 ? 4 : 8;
+  if (((uintptr_t)logits & 15) || (logits_batch_stride % per) || (logits_row_stride % per) ||
+      ((uintptr_t)workspace & 255) || ((uintptr_t)accepted_out & 3))
+    return DFLASH_ERR_ALIGN;
+  // conv windows (L > 0): bf16 rows copied as 16-byte units
+  ConvPlan pl{16, 0, 0, 0};
+  if (L > 0) {
+    const int cst = conv_plan(conv_in, qkv, conv_out, L, T, K1, C, qkv_batch_stride,
+                              qkv_row_stride, 2, &pl);
+    if (cst != DFLASH_OK) return cst;
+    if (pl.unit != 16) return DFLASH_ERR_ALIGN;
+  }
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  const AcceptArgs acc{logits, logits_dtype == DFLASH_DTYPE_BF16 ? 1 : 0, logits_batch_stride,
+                       logits_row_stride, accept_B, N, V, reinterpret_cast<uint64_t*>(ws)};
+  FinishArgs fin{};
+  fin.count = reinterpret_cast<int*>(ws + step_keys_bytes(accept_B, N, V));
+  fin.draft = draft;
+  fin.dstride = draft_stride;
+  fin.n_draft = n_draft;
+  fin.offset = accepted_offset;
+  fin.T = T;
+  fin.posterior = posterior;
+  fin.matched = matched;
+  fin.bonus = bonus;
+  fin.keep = accepted_out;
+  fin.L = L;
+  fin.K1 = K1;
+  fin.Cu = pl.Cu;
+  fin.qbs = pl.qbs;
+  fin.qrs = pl.qrs;
+  if (L > 0) fin.conv = conv_table(conv_in, qkv, conv_out, 0, L);
+  const Select sel{prev_tape, prev_accepted, state, prev_T, accepted_period};
+  return scan_impl(q, k, v, g, beta, state, out, final_state, tape, nullptr, B, T, Hk, Hv, Dk, Dv,
+                   strides, &sel, stream, &acc, &fin);
 }
 
 extern "C" int dflash_gdn_replay(const void* k, const void* v, const float* g,

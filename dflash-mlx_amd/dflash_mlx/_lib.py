@@ -43,6 +43,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I,
          _VP, _VP, _I, _I64, _I64, _I, _I, _I, _VP, _SZ, _VP],
     ),
+    "dflash_gdn_verify_step_workspace_bytes": (_SZ, [_I, _I, _I]),
+    "dflash_gdn_verify_step": (
+        _I,
+        [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I,
+         _VP, _VP, _I, _I64, _I64, _I, _I, _I,  # scan, logits
+         _VP, _I64, _I, _VP, _VP, _VP, _I, _VP,  # accept
+         _VP, _VP, _VP, _I, _I, _I64, _I64, _I64,  # conv windows
+         _VP, _SZ, _VP],
+    ),
     "dflash_gdn_replay": (
         _I,
         [_VP, _VP, _VP, _VP, _VP, _VP, _VP, _I, _I, _I, _I, _I, _I, _VP, _VP],
@@ -136,7 +145,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_VP, _VP, _VP, _VP, _I, _I, _I, _I, _I64, _I64, _I64, _I, _VP],
     ),
 }
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -31,6 +31,18 @@ import torch
 from . import _lib
 
 
+# The fused step runs as one launch (dflash_gdn_verify_step: the accept's
+# last argmax workgroup of each sequence finishes the accept and copies the
+# conv windows while the scan runs) while the windows are at most this many
+# bytes.  One workgroup streams at one CU's rate (~25-30 GB/s): at c0's 48 KB
+# the copy hides behind the scan (graph step 10.7-12.4 against 14.5-15.5 us
+# in two launches); at c1's 1.2 MB (24 layers of 3 x 8192 bf16) it outlasted
+# the scan (194 against 143 us), and with the copy in a launch of its own
+# the step launch's finishing argmax workgroups (agent-scope stores and
+# counts, fewer of them resident beside the scan) cost more than the launch
+# they save (145 against 143 us).  Larger windows keep the two-launch form.
+SINGLE_LAUNCH_MAX_CONV_BYTES = 256 << 10
+
 # The fused step runs the accept's argmax as extra workgroups of the scan's
 # launch while the verify logits are at most this many bytes: there a launch
 # of its own would be bound by the ~5 us launch floor rather than by reading
@@ -67,6 +79,15 @@ class StepShape:
         launch (conv windows present and logits within ARGMAX_IN_SCAN_MAX_BYTES)."""
         return bool(self.conv_dim) and 4 * self.B * self.T * self.V <= ARGMAX_IN_SCAN_MAX_BYTES
 
+    def single_launch(self) -> bool:
+        """Whether the fused step runs as one launch (dflash_gdn_verify_step):
+        the argmax in the scan's launch, bf16 windows of 16-byte rows within
+        SINGLE_LAUNCH_MAX_CONV_BYTES, at most 32 layers, 64 rows, 4 window
+        rows."""
+        return (self.fuse_argmax() and self.conv_dim % 8 == 0 and self.L <= 32 and self.T <= 64
+                and self.K1 <= 4
+                and 2 * self.L * self.B * self.K1 * self.conv_dim <= SINGLE_LAUNCH_MAX_CONV_BYTES)
+
     def rollback_bytes(self) -> int:
         """Upper bound (every sequence accepts >= 1 token): state read + write,
         conv window read + write."""
@@ -79,7 +100,15 @@ class VerifyStepRunner:
     """Holds the step's device buffers; ``run()`` enqueues one verify step on
     torch's current stream.  Inputs are written into the ``q, k, v, g, beta,
     state, logits, block, conv_in, qkv`` buffers by the caller (``block``:
-    the verify block, the last accepted token then T-1 drafts)."""
+    the verify block, the last accepted token then T-1 drafts).
+
+    The keep counts (accepted_inputs = matched + 1) live in two device
+    buffers used in turn: a fused step reads the current one (its scan rolls
+    each sequence's state back to it) and writes the other, which then
+    becomes current (``keep``).  The single-launch form needs that (its
+    accept runs while its scan still reads the previous count); the other
+    forms follow the same rule so that they can be mixed.  A HIP graph of
+    the fused step therefore captures two steps (``run_fused`` twice)."""
 
     def __init__(self, shape: StepShape, device: torch.device):
         s = shape
@@ -88,8 +117,9 @@ class VerifyStepRunner:
         Bt = s.L * s.B
         bf, f32, i32 = torch.bfloat16, torch.float32, torch.int32
         # Inputs are written by the caller and outputs by the kernels, so the
-        # buffers start uninitialised; only `keep` must start at zero (the
-        # first fused step then starts every sequence from `state`).
+        # buffers start uninitialised; only the keep counts and the step's
+        # arrival counts must start at zero (the first fused step then starts
+        # every sequence from `state`).
         z = lambda *shp, dt: torch.empty(shp, dtype=dt, device=device)
         self.q = z(Bt, s.T, s.Hk, s.Dk, dt=bf)
         self.k = z(Bt, s.T, s.Hk, s.Dk, dt=bf)
@@ -105,76 +135,112 @@ class VerifyStepRunner:
         self.block = z(s.B, s.T, dt=i32)  # the verify block: last token, then T-1 drafts
         self.posterior = z(s.B, s.T, dt=i32)
         self.matched = torch.zeros(s.B, dtype=i32, device=device)
-        self.keep = torch.zeros(s.B, dtype=i32, device=device)  # accepted_inputs = matched + 1
+        self._keeps = torch.zeros(2, s.B, dtype=i32, device=device)
+        self._pp = 0  # index of the current keep buffer
         self.bonus = z(s.B, dt=i32)
         self.argmax_in_scan = s.fuse_argmax()
         lib = _lib.load()
-        ws = int(lib.dflash_greedy_accept_workspace_bytes(s.B, s.T, s.V))
-        self.workspace = z(max(ws, 8), dt=torch.uint8)
         if s.conv_dim:
             self.conv_in = [z(s.B, s.K1, s.conv_dim, dt=bf) for _ in range(s.L)]
             self.qkv = [z(s.B, s.T, s.conv_dim, dt=bf) for _ in range(s.L)]
             self.conv_out = [z(s.B, s.K1, s.conv_dim, dt=bf) for _ in range(s.L)]
+        # The whole fused step in one launch (dflash_gdn_verify_step) where its
+        # limits allow and pay: argmax in the scan's launch, bf16 windows
+        # copied as 16-byte units, at most SINGLE_LAUNCH_MAX_CONV_BYTES of
+        # them, 32 layers, 64 rows, 4 window rows.  conv_in_launch False (a
+        # form kept for tests and callers with their own measurements): the
+        # step launch leaves the windows to a dflash_conv_rollback after it.
+        self.conv_in_launch = True
+        self.single_launch = s.single_launch()
+        ws = max(int(lib.dflash_greedy_accept_workspace_bytes(s.B, s.T, s.V)),
+                 int(lib.dflash_gdn_verify_step_workspace_bytes(s.B, s.T, s.V)))
+        # zeroed: the single-launch step's arrival counts follow the keys
+        self.workspace = torch.zeros(max(ws, 8), dtype=torch.uint8, device=device)
         self._build_args()
 
-    def _build_args(self) -> None:
+    @property
+    def keep(self) -> torch.Tensor:
+        """The current keep counts (int32 [B]): what the next fused step's scan
+        rolls back to."""
+        return self._keeps[self._pp]
+
+    def _args(self, p: int) -> dict:
+        """Launch arguments with keep buffer p current (read by the scans and
+        the explicit rollback) and 1 - p the one a fused step writes."""
         s = self.shape
         Bt = s.L * s.B
         S = s.Hv * s.Dv * s.Dk
-        self._scan_args = (
+        kin, kout = self._keeps[p].data_ptr(), self._keeps[1 - p].data_ptr()
+        a = {}
+        a["scan"] = (
             self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.g.data_ptr(),
             self.beta.data_ptr(), self.state.data_ptr(), self.out.data_ptr(),
             self.final.data_ptr(), self.tape.data_ptr(), None,
             Bt, s.T, s.Hk, s.Hv, s.Dk, s.Dv, None,
         )
         # Fused form: the scan starts each sequence from the previous step's
-        # tape at its keep count (self.keep), updating self.state in place, and
-        # rewrites the same tape buffer; the final state is tape[T-1].
-        self._scan_rb_args = (
+        # tape at its keep count, updating self.state in place, and rewrites
+        # the same tape buffer; the final state is tape[T-1].
+        a["scan_rb"] = (
             self.q.data_ptr(), self.k.data_ptr(), self.v.data_ptr(), self.g.data_ptr(),
             self.beta.data_ptr(), self.state.data_ptr(), self.tape.data_ptr(),
-            self.keep.data_ptr(), s.T, s.B, self.out.data_ptr(), None,
+            kin, s.T, s.B, self.out.data_ptr(), None,
             self.tape.data_ptr(), Bt, s.T, s.Hk, s.Hv, s.Dk, s.Dv, None,
         )
         # drafts = block[1:] (row stride T, T-1 of them) against all T
         # posterior rows: the bonus may come from row T-1
-        self._accept_args = (
+        a["accept"] = (
             self.logits.data_ptr(), _lib.DFLASH_DTYPE_F32, s.T * s.V, s.V,
             self.block.data_ptr() + 4, s.T, s.T - 1, self.posterior.data_ptr(),
             self.matched.data_ptr(), self.bonus.data_ptr(), s.B, s.T, s.V,
             self.workspace.data_ptr(), self.workspace.numel(),
         )
-        self._commit_args = (self.matched.data_ptr(), self.keep.data_ptr(), None, s.B, s.T)
+        a["commit"] = (self.matched.data_ptr(), kin, None, s.B, s.T)
         esz = 4
         tapes = (ctypes.c_void_p * s.L)(*[self.tape.data_ptr() + l * s.B * S * esz for l in range(s.L)])
         sins = (ctypes.c_void_p * s.L)(*[self.state.data_ptr() + l * s.B * S * esz for l in range(s.L)])
         souts = (ctypes.c_void_p * s.L)(*[self.new_state.data_ptr() + l * s.B * S * esz
                                           for l in range(s.L)])
-        self._tape_args = (tapes, sins, souts, self.keep.data_ptr(), s.L, s.B, s.T, S, Bt * S)
+        a["tape"] = (tapes, sins, souts, kin, s.L, s.B, s.T, S, Bt * S)
         if s.conv_dim:
             cins = _lib.ptr_array(self.conv_in)
             qkvs = _lib.ptr_array(self.qkv)
             couts = _lib.ptr_array(self.conv_out)
-            self._conv_args = (cins, qkvs, couts, self.keep.data_ptr(), s.L, s.B, s.T, s.K1,
-                               s.conv_dim, s.T * s.conv_dim, s.conv_dim, 2)
+            a["conv"] = (cins, qkvs, couts, kin, s.L, s.B, s.T, s.K1,
+                         s.conv_dim, s.T * s.conv_dim, s.conv_dim, 2)
             # accept + conv rollback in two launches (finalize inside the copy),
-            # which also writes keep = matched + 1 for the next scan
-            self._accept_conv_args = self._accept_args + (
-                cins, qkvs, couts, 1, self.keep.data_ptr(), s.L, s.T, s.K1, s.conv_dim,
+            # which also writes the next keep = matched + 1
+            a["accept_conv"] = a["accept"] + (
+                cins, qkvs, couts, 1, kout, s.L, s.T, s.K1, s.conv_dim,
                 s.T * s.conv_dim, s.conv_dim, 2)
             # the same with the argmax already run by the scan's launch
-            self._scan_rb_argmax_args = self._scan_rb_args + (
+            a["scan_rb_argmax"] = a["scan_rb"] + (
                 self.logits.data_ptr(), _lib.DFLASH_DTYPE_F32, s.T * s.V, s.V, s.B, s.T, s.V,
                 self.workspace.data_ptr(), self.workspace.numel())
-            self._keys_conv_args = (
+            a["keys_conv"] = (
                 self.block.data_ptr() + 4, s.T, s.T - 1, self.posterior.data_ptr(),
                 self.matched.data_ptr(), self.bonus.data_ptr(), s.B, s.T, s.V,
                 self.workspace.data_ptr(), self.workspace.numel(), cins, qkvs, couts, 1,
-                self.keep.data_ptr(), s.L, s.T, s.K1, s.conv_dim, s.T * s.conv_dim, s.conv_dim, 2)
+                kout, s.L, s.T, s.K1, s.conv_dim, s.T * s.conv_dim, s.conv_dim, 2)
+            # everything in one launch (step), or all but the conv windows (step_noconv)
+            step = a["scan_rb"] + (
+                self.logits.data_ptr(), _lib.DFLASH_DTYPE_F32, s.T * s.V, s.V, s.B, s.T, s.V,
+                self.block.data_ptr() + 4, s.T, s.T - 1, self.posterior.data_ptr(),
+                self.matched.data_ptr(), self.bonus.data_ptr(), 1, kout)
+            tail = (self.workspace.data_ptr(), self.workspace.numel())
+            a["step"] = step + (cins, qkvs, couts, s.L, s.K1, s.conv_dim, s.T * s.conv_dim,
+                                s.conv_dim) + tail
+            a["step_noconv"] = step + (None, None, None, 0, 0, 0, 0, 0) + tail
+            a["_keep_alive"] = (tapes, sins, souts, cins, qkvs, couts)
+        return a
+
+    def _build_args(self) -> None:
+        self._argsets = [self._args(0), self._args(1)]
         lib = _lib.load()
         self._accept_conv = lib.dflash_greedy_accept_conv_rollback
         self._scan_rb_argmax = lib.dflash_gdn_verify_scan_rollback_argmax
         self._keys_conv = lib.dflash_accept_keys_conv_rollback
+        self._step = lib.dflash_gdn_verify_step
         self._scan = lib.dflash_gdn_verify_scan
         self._scan_rb = lib.dflash_gdn_verify_scan_rollback
         self._accept = lib.dflash_greedy_accept
@@ -182,53 +248,80 @@ class VerifyStepRunner:
         self._conv = lib.dflash_conv_rollback
         self._commit = lib.dflash_commit_accept
 
+    def _a(self, name):
+        return self._argsets[self._pp][name]
+
+    def _flip(self) -> None:
+        """The keep buffer a fused step wrote becomes the current one."""
+        self._pp ^= 1
+
     def _stream(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
 
     def scan(self, stream: int | None = None) -> None:
-        _lib.check("dflash_gdn_verify_scan", self._scan(*self._scan_args, stream or self._stream()))
+        _lib.check("dflash_gdn_verify_scan", self._scan(*self._a("scan"), stream or self._stream()))
 
     def accept(self, stream: int | None = None) -> None:
-        """Greedy accept, then keep = matched + 1 (two launches)."""
+        """Greedy accept, then keep = matched + 1 into the current keep
+        buffer (two launches)."""
         st = stream or self._stream()
-        _lib.check("dflash_greedy_accept", self._accept(*self._accept_args, st))
-        _lib.check("dflash_commit_accept", self._commit(*self._commit_args, st))
+        _lib.check("dflash_greedy_accept", self._accept(*self._a("accept"), st))
+        _lib.check("dflash_commit_accept", self._commit(*self._a("commit"), st))
 
     def rollback(self, stream: int | None = None) -> None:
         st = stream or self._stream()
-        _lib.check("dflash_tape_select", self._tsel(*self._tape_args, st))
+        _lib.check("dflash_tape_select", self._tsel(*self._a("tape"), st))
         if self.shape.conv_dim:
-            _lib.check("dflash_conv_rollback", self._conv(*self._conv_args, st))
+            _lib.check("dflash_conv_rollback", self._conv(*self._a("conv"), st))
 
     def scan_rolled(self, stream: int | None = None) -> None:
         _lib.check("dflash_gdn_verify_scan_rollback",
-                   self._scan_rb(*self._scan_rb_args, stream or self._stream()))
+                   self._scan_rb(*self._a("scan_rb"), stream or self._stream()))
 
     def conv_rollback(self, stream: int | None = None) -> None:
         if self.shape.conv_dim:
-            _lib.check("dflash_conv_rollback", self._conv(*self._conv_args, stream or self._stream()))
+            _lib.check("dflash_conv_rollback", self._conv(*self._a("conv"), stream or self._stream()))
 
     def accept_conv_rollback(self, stream: int | None = None) -> None:
         """accept() then conv_rollback(), as two launches instead of four (the
-        window copy also writes keep)."""
+        window copy writes the other keep buffer, which becomes current)."""
         st = stream or self._stream()
         if not self.shape.conv_dim:
             self.accept(st)
             return
         _lib.check("dflash_greedy_accept_conv_rollback",
-                   self._accept_conv(*self._accept_conv_args, st))
+                   self._accept_conv(*self._a("accept_conv"), st))
+        self._flip()
 
     def scan_rolled_argmax(self, stream: int | None = None) -> None:
         """scan_rolled() with the accept's argmax (per-slice keys of the
         verify logits) run by extra workgroups of the same launch."""
         _lib.check("dflash_gdn_verify_scan_rollback_argmax",
-                   self._scan_rb_argmax(*self._scan_rb_argmax_args, stream or self._stream()))
+                   self._scan_rb_argmax(*self._a("scan_rb_argmax"), stream or self._stream()))
 
     def accept_keys_conv_rollback(self, stream: int | None = None) -> None:
         """The accept's finalize inside the conv-window rollback, from the keys
-        scan_rolled_argmax() left in the workspace (one launch)."""
+        scan_rolled_argmax() left in the workspace (one launch); the keep it
+        writes becomes current."""
         _lib.check("dflash_accept_keys_conv_rollback",
-                   self._keys_conv(*self._keys_conv_args, stream or self._stream()))
+                   self._keys_conv(*self._a("keys_conv"), stream or self._stream()))
+        self._flip()
+
+    def step_launch(self, stream: int | None = None) -> None:
+        """dflash_gdn_verify_step: the scan with the rollback load and the
+        accept's argmax workgroups, the last of which finishes the accept
+        and, with ``conv_in_launch``, copies the conv windows."""
+        name = "step" if self.conv_in_launch else "step_noconv"
+        _lib.check("dflash_gdn_verify_step", self._step(*self._a(name), stream or self._stream()))
+        self._flip()
+
+    def step_single(self, stream: int | None = None) -> None:
+        """The fused step in one launch, or two when the conv windows are
+        copied apart (dflash_conv_rollback of the keep the step wrote)."""
+        st = stream or self._stream()
+        self.step_launch(st)
+        if not self.conv_in_launch:
+            self.conv_rollback(st)
 
     def run(self) -> None:
         """Explicit form: scan (with final state) -> accept -> gather rollback."""
@@ -243,11 +336,14 @@ class VerifyStepRunner:
         the call, the state after keeping keep[b] = matched[b] + 1 tokens of
         this block is tape[keep[b]-1, b], which the next run_fused() picks up
         on the device.  Start with keep zeroed (the first scan then starts
-        from state).  With conv windows and small logits
-        (``argmax_in_scan``): two launches, the scan with the accept's argmax,
-        then the finalize inside the window copy; otherwise three."""
+        from state).  With conv windows and small logits: one launch
+        (``single_launch``; two with large windows, the copy apart), else
+        two with the argmax in the scan's launch (``argmax_in_scan``), else
+        three."""
         st = self._stream()
-        if self.argmax_in_scan:
+        if self.single_launch:
+            self.step_single(st)
+        elif self.argmax_in_scan:
             self.scan_rolled_argmax(st)
             self.accept_keys_conv_rollback(st)
         else:

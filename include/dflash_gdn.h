@@ -34,7 +34,7 @@
 extern "C" {
 #endif
 
-#define DFLASH_ABI_VERSION 3
+#define DFLASH_ABI_VERSION 4
 
 /* Argument-validation codes (negative).  Positive values are hipError_t. */
 #define DFLASH_OK 0
@@ -150,6 +150,45 @@ int dflash_gdn_verify_scan_rollback_argmax(
     int Dv, const int64_t* strides, const void* logits, int logits_dtype,
     int64_t logits_batch_stride, int64_t logits_row_stride, int accept_B,
     int N, int V, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The whole fused verify step in one launch: dflash_gdn_verify_scan_rollback_argmax
+ * followed by dflash_accept_keys_conv_rollback (the reference's
+ * verify_block_parallel_replay after the target forward: greedy accept, keep
+ * = matched + accepted_offset, conv-window rollback; dflash_mlx/runtime.py:
+ * 117-163, adapters.py:505-560), with the same outputs bit for bit.  The last
+ * of each sequence's argmax workgroups to finish (counted in the workspace)
+ * merges that sequence's keys, writes posterior / matched / bonus and
+ * accepted_out[b] = clamp(matched + accepted_offset, 0, T), and copies its
+ * conv windows of all L layers, while the scan's workgroups run on; no
+ * workgroup waits on another.  accepted_out must not be prev_accepted (the
+ * scan of the same launch reads that one): a serving loop alternates two
+ * buffers.  Scan and logits arguments as dflash_gdn_verify_scan_rollback_argmax;
+ * draft / draft_stride / n_draft / posterior / matched / bonus as
+ * dflash_greedy_accept (posterior, matched, bonus may be NULL); conv_in /
+ * qkv / conv_out as dflash_conv_rollback with bf16 elements whose rows and
+ * pointers are 16-byte aligned.  L = 0: no conv windows (the caller runs
+ * dflash_conv_rollback with accepted_out after it: one workgroup copies
+ * the windows here, at one CU's streaming rate, which only pays while the
+ * copy is small).  Supported: N <= 64, K1 <= 4, L <= 32.
+ * workspace: dflash_gdn_verify_step_workspace_bytes(accept_B, N, V) bytes,
+ * 256-byte aligned, zeroed once before the first call (every call leaves its
+ * counts zeroed again); calls sharing it must not overlap (one stream).
+ */
+size_t dflash_gdn_verify_step_workspace_bytes(int B, int N, int V);
+int dflash_gdn_verify_step(
+    const void* q, const void* k, const void* v, const float* g,
+    const float* beta, float* state, const float* prev_tape,
+    const int32_t* prev_accepted, int prev_T, int accepted_period, void* out,
+    float* final_state, float* tape, int B, int T, int Hk, int Hv, int Dk,
+    int Dv, const int64_t* strides, const void* logits, int logits_dtype,
+    int64_t logits_batch_stride, int64_t logits_row_stride, int accept_B,
+    int N, int V, const int32_t* draft, int64_t draft_stride, int n_draft,
+    int32_t* posterior, int32_t* matched, int32_t* bonus, int accepted_offset,
+    int32_t* accepted_out, const void* const* conv_in, const void* const* qkv,
+    void* const* conv_out, int L, int K1, int64_t C, int64_t qkv_batch_stride,
+    int64_t qkv_row_stride, void* workspace, size_t workspace_bytes,
+    void* stream);
 
 /*
  * State-only replay of the first n_b tokens: the same recurrence without q,

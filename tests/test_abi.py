@@ -39,6 +39,7 @@ def test_header_declares_expected_entry_points():
         "dflash_gdn_prologue_scan_rollback", "dflash_lm_head_greedy_accept_tiled",
         "dflash_greedy_accept_conv_rollback", "dflash_gdn_verify_scan_rollback_argmax",
         "dflash_accept_keys_conv_rollback",
+        "dflash_gdn_verify_step_workspace_bytes", "dflash_gdn_verify_step",
         "dflash_gdn_chunked_prefill_workspace_bytes", "dflash_gdn_chunked_prefill",
         "dflash_add_rmsnorm", "dflash_swiglu", "dflash_attn_prep",
         "dflash_attn_verify_workspace_bytes", "dflash_attn_verify", "dflash_commit_accept",
@@ -69,7 +70,7 @@ def test_library_targets_gfx950_only():
 
 
 def test_abi_version_and_strerror(lib):
-    assert lib.dflash_abi_version() == 3
+    assert lib.dflash_abi_version() == 4
     assert lib.dflash_strerror(0) == b"ok"
     assert b"NULL" in lib.dflash_strerror(-1)
     assert lib.dflash_strerror(-999) == b"unknown dflash error"

@@ -70,8 +70,11 @@ def test_layer_verify_and_accept_graph_replays(device):
     assert int(outs[5][0]) == 9
 
 
-@pytest.mark.parametrize("argmax_in_scan", [True, False])
-def test_fused_step_runner_graph_replays(device, argmax_in_scan):
+@pytest.mark.parametrize("single_launch,argmax_in_scan,conv_in_launch", [
+    (True, True, True), (True, True, False), (False, True, True), (False, False, True)])
+def test_fused_step_runner_graph_replays(device, single_launch, argmax_in_scan, conv_in_launch):
+    """Two fused steps captured as one graph (the keep counts alternate
+    between two buffers), replayed against two eager steps each time."""
     cfg = ScanConfig(**{**CONFIGS[2].__dict__, "B": 2, "V": 3000})
     x = make_scan_inputs(cfg)
     acc = make_accept_inputs(cfg, gen=x["_gen"])
@@ -79,13 +82,14 @@ def test_fused_step_runner_graph_replays(device, argmax_in_scan):
     runners = []
     for _ in range(2):
         r = VerifyStepRunner(shape, device)
-        r.argmax_in_scan = argmax_in_scan
+        r.single_launch, r.argmax_in_scan = single_launch, argmax_in_scan
+        r.conv_in_launch = conv_in_launch
         for n in ("q", "k", "v", "g", "beta", "state"):
             getattr(r, n).copy_(x[n])
         r.logits.copy_(acc["logits"])
         r.block.copy_(make_verify_block(acc))
-        for t in r.conv_in + r.qkv:
-            t.zero_()
+        for i, t in enumerate(r.conv_in + r.qkv):
+            t.copy_(torch.randn(t.shape, generator=torch.Generator().manual_seed(i)).bfloat16())
         runners.append(r)
     eager, graphed = runners
     torch.cuda.synchronize()
@@ -95,11 +99,14 @@ def test_fused_step_runner_graph_replays(device, argmax_in_scan):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         graphed.run_fused()
-    # Capture does not execute: reset the graphed runner's carried state.
+        graphed.run_fused()
+    # Capture does not execute: reset the graphed runner's carried state (the
+    # capture flipped the current keep buffer twice: back to the first).
     graphed.state.copy_(x["state"])
     graphed.keep.zero_()
     torch.cuda.synchronize()
     for step in range(4):
+        eager.run_fused()
         eager.run_fused()
         torch.cuda.synchronize()
         graph.replay()
@@ -110,3 +117,5 @@ def test_fused_step_runner_graph_replays(device, argmax_in_scan):
         assert torch.equal(graphed.tape, eager.tape)
         assert torch.equal(graphed.state, eager.state)
         assert torch.equal(graphed.out, eager.out)
+        for a, b in zip(graphed.conv_out, eager.conv_out):
+            assert torch.equal(a, b)

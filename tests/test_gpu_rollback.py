@@ -238,11 +238,23 @@ def test_fused_rollback_scan_equals_gather_then_scan(device, in_place):
     del tape_e
 
 
-@pytest.mark.parametrize("argmax_in_scan", [True, False])
-def test_step_runner_fused_matches_explicit(device, argmax_in_scan):
+FORMS = {"single": (True, True, True), "single_conv_apart": (True, True, False),
+         "argmax_in_scan": (False, True, True), "separate": (False, False, True)}
+
+
+def _set_form(r, form):
+    """single_launch, argmax_in_scan, conv_in_launch of a VerifyStepRunner by
+    form name."""
+    r.single_launch, r.argmax_in_scan, r.conv_in_launch = FORMS[form]
+
+
+@pytest.mark.parametrize("form", list(FORMS))
+def test_step_runner_fused_matches_explicit(device, form):
     """VerifyStepRunner: run_fused (rollback folded into the next scan) and run
     (explicit gather) leave the same rolled-back state and the same tape, with
-    the accept's argmax in the scan's launch or in its own."""
+    the whole fused step in one launch (the conv windows copied in it or in
+    a launch of their own), the accept's argmax in the scan's launch, or in
+    its own."""
     from dflash_mlx.step import StepShape, VerifyStepRunner
     from dflash_mlx.workloads import (CONFIGS, ScanConfig, make_accept_inputs, make_scan_inputs,
                                       make_verify_block)
@@ -254,12 +266,15 @@ def test_step_runner_fused_matches_explicit(device, argmax_in_scan):
     runs = []
     for fused in (False, True):
         r = VerifyStepRunner(shape, device)
-        assert r.argmax_in_scan  # 1.3 MB of logits: the default places it in the scan
-        r.argmax_in_scan = argmax_in_scan
+        # 1.3 MB of logits and 32 KB of windows: the default is one launch
+        assert r.argmax_in_scan and r.single_launch and r.conv_in_launch
+        _set_form(r, form)
         for n in ("q", "k", "v", "g", "beta", "state"):
             getattr(r, n).copy_(x[n])
         r.logits.copy_(acc["logits"])
         r.block.copy_(make_verify_block(acc))
+        for i, t in enumerate(r.conv_in + r.qkv):
+            t.copy_(torch.randn(t.shape, generator=torch.Generator().manual_seed(i)).bfloat16())
         (r.run_fused if fused else r.run)()
         torch.cuda.synchronize()
         # drafts block[1:] against posterior rows 0..14 (the reference's wiring)
@@ -268,6 +283,8 @@ def test_step_runner_fused_matches_explicit(device, argmax_in_scan):
         assert r.keep.cpu().tolist() == [m + 1 for m in matched]
         runs.append(r)
     explicit, fused = runs
+    for a, b in zip(explicit.conv_out, fused.conv_out):
+        assert torch.equal(a, b)
     assert torch.equal(explicit.tape, fused.tape)
     assert torch.equal(explicit.out, fused.out)
     assert torch.equal(fused.rolled_back_state(), explicit.new_state)
@@ -398,3 +415,128 @@ def test_scan_with_argmax_matches_separate_launches(device, B, Hk, Hv, D, V, dty
         results.append(got)
     for a, b in zip(*results):
         assert torch.equal(a, b)
+
+
+def _one_launch_inputs(L, B, T, V, C, Hk, Hv, K1, seed, device):
+    g = torch.Generator().manual_seed(seed)
+    Bt, D = L * B, 128
+    x = dict(
+        q=torch.randn(Bt, T, Hk, D, generator=g).bfloat16(),
+        k=(torch.randn(Bt, T, Hk, D, generator=g) / D ** 0.5).bfloat16(),
+        v=torch.randn(Bt, T, Hv, D, generator=g).bfloat16(),
+        g=torch.rand(Bt, T, Hv, generator=g) * 0.5 + 0.5,
+        beta=torch.rand(Bt, T, Hv, generator=g),
+        state=0.05 * torch.randn(Bt, Hv, D, D, generator=g),
+        logits=torch.randn(B, T, V, generator=g),
+        conv=[torch.randn(B, K1, C, generator=g).bfloat16() for _ in range(L)],
+        qkv=[torch.randn(B, T, C, generator=g).bfloat16() for _ in range(L)],
+    )
+    am = x["logits"].argmax(-1).to(torch.int32)
+    accept = torch.randint(0, T, (B,), generator=g, dtype=torch.int32)
+    block = torch.zeros(B, T, dtype=torch.int32)
+    pos = torch.arange(T - 1, dtype=torch.int32)[None, :]
+    block[:, 1:] = torch.where(pos < accept[:, None], am[:, :-1], (am[:, :-1] + 1) % V)
+    x["block"] = block
+    return {k: ([t.to(device) for t in v] if isinstance(v, list) else v.to(device))
+            for k, v in x.items()}
+
+
+@pytest.mark.parametrize("L,B,T,V,C,Hk,Hv,K1", [
+    (3, 2, 16, 3000, 256, 2, 4, 3),
+    (24, 1, 16, 20000, 8192, 2, 4, 3),    # c1's 24 layers of 8192-channel windows
+    (2, 3, 5, 1000, 64, 1, 2, 2),         # short block, two window rows
+    (1, 1, 1, 512, 128, 1, 1, 3),         # one token
+])
+def test_single_launch_step_matches_two_launches(device, L, B, T, V, C, Hk, Hv, K1):
+    """dflash_gdn_verify_step (scan + rollback load + argmax, the last argmax
+    workgroup of each sequence finishing the accept and the conv windows)
+    gives the bits of dflash_gdn_verify_scan_rollback_argmax then
+    dflash_accept_keys_conv_rollback over two steps (the second rolling back
+    to the first one's keep): out, tape, state, posterior, matched, bonus,
+    keep and every window; the arrival counts are zero after each call."""
+    from dflash_mlx import _lib
+
+    print(f"[single-launch step L={L} B={B} T={T} V={V} C={C} Hk={Hk} Hv={Hv} K1={K1}]",
+          flush=True)
+    x = _one_launch_inputs(L, B, T, V, C, Hk, Hv, K1, seed=L * 7 + B + T, device=device)
+    lib = _lib.load()
+    st = _lib.stream_handle(device)
+    Bt, D, i32 = L * B, 128, torch.int32
+    runs = []
+    for single in (False, True):
+        state = x["state"].clone()
+        tape = torch.zeros(T, Bt, Hv, D, D, device=device)
+        out = torch.empty(Bt, T, Hv, D, dtype=torch.bfloat16, device=device)
+        post = torch.full((B, T), -7, dtype=i32, device=device)
+        matched = torch.full((B,), -7, dtype=i32, device=device)
+        bonus = torch.full((B,), -7, dtype=i32, device=device)
+        keeps = [torch.zeros(B, dtype=i32, device=device) for _ in range(3)]
+        couts = [torch.full_like(c, float("nan")) for c in x["conv"]]
+        nws = (int(lib.dflash_gdn_verify_step_workspace_bytes(B, T, V)) if single
+               else int(lib.dflash_greedy_accept_workspace_bytes(B, T, V)))
+        ws = torch.zeros(nws, dtype=torch.uint8, device=device)
+        cin, qkv, cout = (_lib.ptr_array(t) for t in (x["conv"], x["qkv"], couts))
+        got = []
+        for step in range(2):
+            kin, kout = keeps[step], keeps[step + 1]
+            scan = (x["q"].data_ptr(), x["k"].data_ptr(), x["v"].data_ptr(), x["g"].data_ptr(),
+                    x["beta"].data_ptr(), state.data_ptr(), tape.data_ptr(), kin.data_ptr(), T, B,
+                    out.data_ptr(), None, tape.data_ptr(), Bt, T, Hk, Hv, D, D, None,
+                    x["logits"].data_ptr(), _lib.DFLASH_DTYPE_F32, T * V, V, B, T, V)
+            acc = (x["block"].data_ptr() + 4, T, T - 1, post.data_ptr(), matched.data_ptr(),
+                   bonus.data_ptr())
+            if single:
+                _lib.call("dflash_gdn_verify_step", *scan, *acc, 1, kout.data_ptr(), cin, qkv,
+                          cout, L, K1, C, T * C, C, ws.data_ptr(), ws.numel(), st)
+            else:
+                _lib.call("dflash_gdn_verify_scan_rollback_argmax", *scan, ws.data_ptr(),
+                          ws.numel(), st)
+                _lib.call("dflash_accept_keys_conv_rollback", *acc, B, T, V, ws.data_ptr(),
+                          ws.numel(), cin, qkv, cout, 1, kout.data_ptr(), L, T, K1, C, T * C, C,
+                          2, st)
+            torch.cuda.synchronize()
+            got.append([t.clone() for t in (out, tape, state, post, matched, bonus, kout, *couts)])
+            if single:
+                counts = ws[int(lib.dflash_gdn_verify_step_workspace_bytes(B, T, V)) - 4 * B:]
+                assert bool((counts == 0).all().item()), step
+        runs.append(got)
+    for step in range(2):
+        for i, (a, b) in enumerate(zip(runs[0][step], runs[1][step])):
+            assert torch.equal(a, b), (step, i)
+    keep = runs[1][0][6].cpu()
+    assert bool(((keep >= 1) & (keep <= T)).all())
+
+
+def test_single_launch_step_validation(device):
+    from dflash_mlx import _lib
+
+    lib = _lib.load()
+    f = lib.dflash_gdn_verify_step
+    B, T, V, L, C, Hv = 1, 16, 1000, 1, 256, 2
+    x = _one_launch_inputs(L, B, T, V, C, 1, Hv, 3, seed=1, device=device)
+    st = _lib.stream_handle(device)
+    tape = torch.zeros(T, B, Hv, 128, 128, device=device)
+    out = torch.empty(B, T, Hv, 128, dtype=torch.bfloat16, device=device)
+    keep = torch.zeros(2, B, dtype=torch.int32, device=device)
+    nws = int(lib.dflash_gdn_verify_step_workspace_bytes(B, T, V))
+    ws = torch.zeros(nws + 512, dtype=torch.uint8, device=device)
+    couts = [torch.empty_like(c) for c in x["conv"]]
+    cin, qkv, cout = (_lib.ptr_array(t) for t in (x["conv"], x["qkv"], couts))
+
+    def call(kout=keep[1], N=T, K1=3, conv_out=cout, wsp=ws.data_ptr(), wsn=nws, cv=cin):
+        return f(x["q"].data_ptr(), x["k"].data_ptr(), x["v"].data_ptr(), x["g"].data_ptr(),
+                 x["beta"].data_ptr(), x["state"].data_ptr(), tape.data_ptr(),
+                 keep[0].data_ptr(), T, B, out.data_ptr(), None, tape.data_ptr(), B, T, 1, Hv,
+                 128, 128, None, x["logits"].data_ptr(), _lib.DFLASH_DTYPE_F32, T * V, V, B, N, V,
+                 x["block"].data_ptr() + 4, T, T - 1, None, None, None, 1, kout.data_ptr(),
+                 cv, qkv, conv_out, L, K1, C, T * C, C, wsp, wsn, st)
+
+    assert call(kout=keep[0]) == -2          # writes the count its scan reads
+    assert call(N=65) == -3                  # more rows than the finisher holds
+    assert call(K1=5) == -3                  # more window rows than it copies
+    assert call(wsn=nws - 1) == -5           # workspace too small
+    assert call(wsp=ws.data_ptr() + 16) == -4  # workspace not 256-byte aligned
+    odd = [c[..., 1:] for c in x["conv"]]    # rows not 16-byte aligned: 2-byte units
+    assert call(cv=_lib.ptr_array(odd)) == -4
+    assert call() == 0
+    torch.cuda.synchronize()

@@ -81,6 +81,28 @@ def test_argmax_placement_follows_logit_size():
     assert not StepShape(**{**edge.__dict__, "V": edge.V + 1}).fuse_argmax()
 
 
+def test_single_launch_follows_window_size():
+    """The whole fused step is one launch at c0 (48 KB of conv windows), two
+    at c1 (1.2 MB: one workgroup would copy them slower than the scan runs)
+    and three at c2 (logits too large for the scan's launch)."""
+    from dflash_mlx.step import SINGLE_LAUNCH_MAX_CONV_BYTES, StepShape
+    from dflash_mlx.workloads import CONFIGS
+
+    def shape(c, **kw):
+        return StepShape(**{**dict(L=c.layers, B=c.B, T=c.T, Hk=c.Hk, Hv=c.Hv, Dk=c.Dk, Dv=c.Dv,
+                                   V=c.V, conv_dim=8192), **kw})
+
+    assert shape(CONFIGS[0]).single_launch()
+    assert not shape(CONFIGS[1]).single_launch()
+    assert not shape(CONFIGS[2]).single_launch()
+    assert not shape(CONFIGS[0], conv_dim=8190).single_launch()  # rows not 16-byte multiples
+    assert not shape(CONFIGS[0], K1=5).single_launch()
+    edge = shape(CONFIGS[0],
+                 conv_dim=SINGLE_LAUNCH_MAX_CONV_BYTES // (2 * 3 * CONFIGS[0].layers) // 8 * 8)
+    assert edge.single_launch()
+    assert not StepShape(**{**edge.__dict__, "conv_dim": edge.conv_dim + 8}).single_launch()
+
+
 def test_workload_inputs_follow_the_recipe():
     x = make_scan_inputs(CONFIGS[0])
     import torch
