@@ -441,13 +441,13 @@ def _one_launch_inputs(L, B, T, V, C, Hk, Hv, K1, seed, device):
             for k, v in x.items()}
 
 
-@pytest.mark.parametrize("L,B,T,V,C,Hk,Hv,K1", [
-    (3, 2, 16, 3000, 256, 2, 4, 3),
-    (24, 1, 16, 20000, 8192, 2, 4, 3),    # c1's 24 layers of 8192-channel windows
-    (2, 3, 5, 1000, 64, 1, 2, 2),         # short block, two window rows
-    (1, 1, 1, 512, 128, 1, 1, 3),         # one token
+@pytest.mark.parametrize("L,B,T,V,C,Hk,Hv,K1,bf16", [
+    (3, 2, 16, 3000, 256, 2, 4, 3, False),
+    (24, 1, 16, 20000, 8192, 2, 4, 3, False),  # c1's 24 layers of 8192-channel windows
+    (2, 3, 5, 1000, 64, 1, 2, 2, True),        # short block, two window rows, bf16 logits
+    (1, 1, 1, 512, 128, 1, 1, 3, True),        # one token
 ])
-def test_single_launch_step_matches_two_launches(device, L, B, T, V, C, Hk, Hv, K1):
+def test_single_launch_step_matches_two_launches(device, L, B, T, V, C, Hk, Hv, K1, bf16):
     """dflash_gdn_verify_step (scan + rollback load + argmax, the last argmax
     workgroup of each sequence finishing the accept and the conv windows)
     gives the bits of dflash_gdn_verify_scan_rollback_argmax then
@@ -459,6 +459,10 @@ def test_single_launch_step_matches_two_launches(device, L, B, T, V, C, Hk, Hv, 
     print(f"[single-launch step L={L} B={B} T={T} V={V} C={C} Hk={Hk} Hv={Hv} K1={K1}]",
           flush=True)
     x = _one_launch_inputs(L, B, T, V, C, Hk, Hv, K1, seed=L * 7 + B + T, device=device)
+    ltag = _lib.DFLASH_DTYPE_F32
+    if bf16:
+        x["logits"] = x["logits"].bfloat16()
+        ltag = _lib.DFLASH_DTYPE_BF16
     lib = _lib.load()
     st = _lib.stream_handle(device)
     Bt, D, i32 = L * B, 128, torch.int32
@@ -482,7 +486,7 @@ def test_single_launch_step_matches_two_launches(device, L, B, T, V, C, Hk, Hv, 
             scan = (x["q"].data_ptr(), x["k"].data_ptr(), x["v"].data_ptr(), x["g"].data_ptr(),
                     x["beta"].data_ptr(), state.data_ptr(), tape.data_ptr(), kin.data_ptr(), T, B,
                     out.data_ptr(), None, tape.data_ptr(), Bt, T, Hk, Hv, D, D, None,
-                    x["logits"].data_ptr(), _lib.DFLASH_DTYPE_F32, T * V, V, B, T, V)
+                    x["logits"].data_ptr(), ltag, T * V, V, B, T, V)
             acc = (x["block"].data_ptr() + 4, T, T - 1, post.data_ptr(), matched.data_ptr(),
                    bonus.data_ptr())
             if single:
