@@ -632,10 +632,11 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
     # once as a HIP graph (no host work inside), W replays untimed, then K replays
     # between synchronizes.  The eager per-phase timing above is the breakdown.
     # The graph holds two steps: the keep counts alternate between two buffers
-    # (each step reads one and writes the other), so K steps are K / 2 replays.
-    K2 = max(1, K // 2)
-    print(f"[bench] {cfg.name}: timing {K2} graph replays of two fused steps", file=sys.stderr,
-          flush=True)
+    # (each step reads one and writes the other), so K steps are K // 2
+    # replays, plus one eager step when K is odd (the same for the warmup).
+    K2 = K // 2
+    print(f"[bench] {cfg.name}: timing {K} fused steps as {K2} graph replays of two"
+          + (" + 1 eager step" if K % 2 else ""), file=sys.stderr, flush=True)
     cap = torch.cuda.Stream(device=dev)
     cap.wait_stream(torch.cuda.current_stream(dev))
     torch.cuda.synchronize()
@@ -644,18 +645,22 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
         fused.run_fused()
         fused.run_fused()
     torch.cuda.synchronize()
-    for _ in range(max(1, warmup // 2)):
+    for _ in range(warmup // 2):
         graph.replay()
+    if warmup % 2:
+        fused.run_fused()
     torch.cuda.synchronize()
     g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     g0.record()
     for _ in range(K2):
         graph.replay()
+    if K % 2:
+        fused.run_fused()
     g1.record()
     torch.cuda.synchronize()
-    tg = {"ms_per_step": (time.perf_counter() - t0) * 1e3 / (2 * K2),
-          "gpu_step": g0.elapsed_time(g1) * 1e3 / (2 * K2)}
+    tg = {"ms_per_step": (time.perf_counter() - t0) * 1e3 / K,
+          "gpu_step": g0.elapsed_time(g1) * 1e3 / K}
     del graph
 
     # Algorithmic HBM bytes.  Scan: bf16 q,k,v,out + fp32 g,beta + fp32 state
@@ -713,16 +718,16 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
                      "sequence's merging the keys and writing matched / bonus / keep"
                      + (" and copying the conv windows (1 launch)" if conv_inl else
                         " (1 launch) -> the conv-window copy (1 launch)")
-                     + "; HIP graph of two steps (keep buffers alternate), replayed K/2 times")
+                     + "; HIP graph of two steps (keep buffers alternate), replayed K // 2 times, one eager step more for odd K")
                     if single else
                     ("fused: scan+tape with the previous step's state rollback in its load, "
                      "with the greedy accept's argmax slices in the same launch -> the accept's "
                      "finalize inside the conv-window rollback copy, which also writes keep "
-                     "(2 launches); HIP graph of two steps, replayed K/2 times") if in_scan else
+                     "(2 launches); HIP graph of two steps, replayed K // 2 times, one eager step more for odd K") if in_scan else
                     ("fused: scan+tape with the previous step's state rollback in its load -> "
                      "the greedy accept's argmax slices -> its finalize inside the conv-window "
                      "rollback copy, which also writes keep (3 launches; logits above "
-                     "ARGMAX_IN_SCAN_MAX_BYTES); HIP graph of two steps, replayed K/2 times"),
+                     "ARGMAX_IN_SCAN_MAX_BYTES); HIP graph of two steps, replayed K // 2 times, one eager step more for odd K"),
         },
         "roofline": roof,
         "graph_step_us": round(tg["gpu_step"], 2),
@@ -755,6 +760,9 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
 
 def main() -> int:
     args = parse_args()
+    if args.steps < 1 or args.warmup < 0:
+        print("bench.py needs --steps >= 1 and --warmup >= 0", file=sys.stderr)
+        return 2
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}, "
