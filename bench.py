@@ -637,6 +637,11 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
     K2 = K // 2
     print(f"[bench] {cfg.name}: timing {K} fused steps as {K2} graph replays of two"
           + (" + 1 eager step" if K % 2 else ""), file=sys.stderr, flush=True)
+    # The graph bakes in the keep buffers current at capture, so the odd
+    # eager warmup step runs before it: replays then always start from the
+    # buffer they were captured with (the odd timed step comes after them).
+    if warmup % 2:
+        fused.run_fused()
     cap = torch.cuda.Stream(device=dev)
     cap.wait_stream(torch.cuda.current_stream(dev))
     torch.cuda.synchronize()
@@ -647,8 +652,6 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
     torch.cuda.synchronize()
     for _ in range(warmup // 2):
         graph.replay()
-    if warmup % 2:
-        fused.run_fused()
     torch.cuda.synchronize()
     g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()

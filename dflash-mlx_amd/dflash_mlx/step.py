@@ -108,7 +108,10 @@ class VerifyStepRunner:
     becomes current (``keep``).  The single-launch form needs that (its
     accept runs while its scan still reads the previous count); the other
     forms follow the same rule so that they can be mixed.  A HIP graph of
-    the fused step therefore captures two steps (``run_fused`` twice)."""
+    the fused step therefore captures two steps (``run_fused`` twice); it
+    holds the buffers that were current at capture, so eager steps between
+    its replays come in pairs (``keep`` is the same buffer before and after
+    each replay)."""
 
     def __init__(self, shape: StepShape, device: torch.device):
         s = shape
