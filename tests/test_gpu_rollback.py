@@ -446,6 +446,7 @@ def _one_launch_inputs(L, B, T, V, C, Hk, Hv, K1, seed, device):
     (24, 1, 16, 20000, 8192, 2, 4, 3, False),  # c1's 24 layers of 8192-channel windows
     (2, 3, 5, 1000, 64, 1, 2, 2, True),        # short block, two window rows, bf16 logits
     (1, 1, 1, 512, 128, 1, 1, 3, True),        # one token
+    (2, 2, 64, 700, 64, 1, 2, 3, False),       # 64 rows, the most one finisher holds
 ])
 def test_single_launch_step_matches_two_launches(device, L, B, T, V, C, Hk, Hv, K1, bf16):
     """dflash_gdn_verify_step (scan + rollback load + argmax, the last argmax
