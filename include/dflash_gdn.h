@@ -624,8 +624,10 @@ int dflash_gemm_bf16_swiglu_tiled(const void* x, int64_t x_row_stride,
 /*
  * Workspace of the tiled GEMMs' tail split (dflash_gemm_bf16_tiled,
  * _swiglu_tiled, _tiled_normed, _swiglu_tiled_normed; k_waves 4, one
- * K split): bytes to pass, 256-byte aligned, zeroed once before the first
- * call (every call leaves it zeroed again).  With it, when the row groups
+ * K split): bytes to pass, 256-byte aligned.  Its first 1 KB holds arrival
+ * counters: zero them once before the first call (every call leaves them
+ * zero again); the rest holds partial sums and needs no clearing.  With it,
+ * when the row groups
  * (N / rows_per_wave; 32 rows for the SwiGLU forms) leave a last round of
  * T groups on the device's compute units with 4T <= CUs (and T <= 64),
  * those T groups run as 4T single-wavefront units of a k-quarter each,
