@@ -22,6 +22,11 @@ inputs resident in HBM:
   explicit             scan (+ final state) -> greedy accept + keep ->
                        tape gather of all 24 layers' states -> conv rollback.
                        Eager.
+Each launch of the headline starts after the launch whose output it reads,
+as in a decode, where the verify logits come out of the block's own scan.
+Beside it, "synthetic_logits_step" times the overlapped forms (the accept's
+argmax in the scan's launch), which only a benchmark with logits given
+before the scan can schedule; it is labelled and never the value.
 The c1 line also carries configs c0 (the reference's tiny CPU-runnable case)
 and c2 (B = 32 serving batch) under "configs", each with its own roofline and
 CPU baseline.  Prints one JSON line.
@@ -559,6 +564,43 @@ def cpu_baseline(cfg, x, acc, block, conv, seconds: float):
     }
 
 
+def graph_steps(torch, dev, run, K: int, warmup: int) -> dict:
+    """K fused steps of a VerifyStepRunner as HIP graph replays.  The graph
+    holds two steps: the keep counts alternate between two buffers (each
+    step reads one and writes the other), so K steps are K // 2 replays,
+    plus one eager step when K is odd (the same for the warmup).  The graph
+    bakes in the keep buffers current at capture, so the odd eager warmup
+    step runs before it: replays then always start from the buffer they
+    were captured with (the odd timed step comes after them)."""
+    K2 = K // 2
+    if warmup % 2:
+        run.run_fused()
+    cap = torch.cuda.Stream(device=dev)
+    cap.wait_stream(torch.cuda.current_stream(dev))
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=cap):
+        run.run_fused()
+        run.run_fused()
+    torch.cuda.synchronize()
+    for _ in range(warmup // 2):
+        graph.replay()
+    torch.cuda.synchronize()
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    g0.record()
+    for _ in range(K2):
+        graph.replay()
+    if K % 2:
+        run.run_fused()
+    g1.record()
+    torch.cuda.synchronize()
+    out = {"ms_per_step": (time.perf_counter() - t0) * 1e3 / K,
+           "gpu_step": g0.elapsed_time(g1) * 1e3 / K}
+    del graph
+    return out
+
+
 def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
                    probe_only: bool = False):
     """One config's verify step (scan + tape, greedy accept with the
@@ -580,8 +622,15 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
     qkv = [torch.randn(B, T, CONV_DIM, generator=gen).to(torch.bfloat16) for _ in range(L)]
 
     runners = {}
-    for form in ("fused", "explicit"):
-        run = VerifyStepRunner(shape, dev)
+    # "overlap": the fused step with the accept's argmax in the scan's launch
+    # (and, with small windows, the whole step in one launch).  The verify
+    # logits are synthetic inputs here; in a decode they come out of the
+    # block's own scan, so that schedule exists only in this benchmark: it is
+    # reported beside the headline, never as it.
+    overlap_differs = shape.fuse_argmax()
+    forms = ("fused", "explicit") + (("overlap",) if overlap_differs else ())
+    for form in forms:
+        run = VerifyStepRunner(shape, dev, overlap_accept=(form == "overlap"))
         for name in ("q", "k", "v", "g", "beta", "state"):
             getattr(run, name).copy_(x[name])
         run.logits.copy_(acc["logits"])
@@ -593,10 +642,13 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
     torch.cuda.synchronize()
 
     fused, explicit = runners["fused"], runners["explicit"]
+    overlap = runners.get("overlap")
     print(f"[bench] {cfg.name}: warmup {warmup}", file=sys.stderr, flush=True)
     for _ in range(max(warmup, 1)):
         fused.run_fused()
         explicit.run()
+        if overlap is not None:
+            overlap.run_fused()
     torch.cuda.synchronize()
     # The drafts agree with the argmax on exactly the drawn accept length
     # (capped at the T - 1 drafts a block holds).
@@ -631,41 +683,9 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
     # The same fused step as the device-driven serving loop launches it: captured
     # once as a HIP graph (no host work inside), W replays untimed, then K replays
     # between synchronizes.  The eager per-phase timing above is the breakdown.
-    # The graph holds two steps: the keep counts alternate between two buffers
-    # (each step reads one and writes the other), so K steps are K // 2
-    # replays, plus one eager step when K is odd (the same for the warmup).
-    K2 = K // 2
-    print(f"[bench] {cfg.name}: timing {K} fused steps as {K2} graph replays of two"
-          + (" + 1 eager step" if K % 2 else ""), file=sys.stderr, flush=True)
-    # The graph bakes in the keep buffers current at capture, so the odd
-    # eager warmup step runs before it: replays then always start from the
-    # buffer they were captured with (the odd timed step comes after them).
-    if warmup % 2:
-        fused.run_fused()
-    cap = torch.cuda.Stream(device=dev)
-    cap.wait_stream(torch.cuda.current_stream(dev))
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=cap):
-        fused.run_fused()
-        fused.run_fused()
-    torch.cuda.synchronize()
-    for _ in range(warmup // 2):
-        graph.replay()
-    torch.cuda.synchronize()
-    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    g0.record()
-    for _ in range(K2):
-        graph.replay()
-    if K % 2:
-        fused.run_fused()
-    g1.record()
-    torch.cuda.synchronize()
-    tg = {"ms_per_step": (time.perf_counter() - t0) * 1e3 / K,
-          "gpu_step": g0.elapsed_time(g1) * 1e3 / K}
-    del graph
-
+    print(f"[bench] {cfg.name}: timing {K} fused steps as graph replays of two",
+          file=sys.stderr, flush=True)
+    tg = graph_steps(torch, dev, fused, K, warmup)
     # Algorithmic HBM bytes.  Scan: bf16 q,k,v,out + fp32 g,beta + fp32 state
     # read + tape (T states per head).  The fused scan also writes the
     # rolled-back state for sequences that kept >= 1 token (every sequence:
@@ -729,8 +749,10 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
                      "(2 launches); HIP graph of two steps, replayed K // 2 times, one eager step more for odd K") if in_scan else
                     ("fused: scan+tape with the previous step's state rollback in its load -> "
                      "the greedy accept's argmax slices -> its finalize inside the conv-window "
-                     "rollback copy, which also writes keep (3 launches; logits above "
-                     "ARGMAX_IN_SCAN_MAX_BYTES); HIP graph of two steps, replayed K // 2 times, one eager step more for odd K"),
+                     "rollback copy, which also writes keep (3 launches, each after the one "
+                     "whose output it reads, as in a decode where the logits come out of the "
+                     "block's scan); HIP graph of two steps, replayed K // 2 times, one eager "
+                     "step more for odd K"),
         },
         "roofline": roof,
         "graph_step_us": round(tg["gpu_step"], 2),
@@ -750,7 +772,25 @@ def measure_verify(torch, dev, cfg, steps: int, warmup: int, cpu_seconds: float,
                                    / (te["gpu_step"] / 1e6) / 1e9, 1),
         },
     }
-    del runners, fused, explicit
+    if overlap is not None:
+        # Labelled apart from the headline: the argmax reads the synthetic
+        # logits while the scan that would produce them in a decode still runs.
+        print(f"[bench] {cfg.name}: timing {K} overlapped-accept steps (synthetic logits)",
+              file=sys.stderr, flush=True)
+        to = graph_steps(torch, dev, overlap, K, warmup)
+        res["synthetic_logits_step"] = {
+            "value": round(tokens / (to["ms_per_step"] / 1e3), 1),
+            "ms_per_step": round(to["ms_per_step"], 4),
+            "graph_step_us": round(to["gpu_step"], 2),
+            "form": ("the whole step in one launch (dflash_gdn_verify_step)"
+                     if overlap.single_launch else
+                     "the accept's argmax in the scan's launch "
+                     "(dflash_gdn_verify_scan_rollback_argmax) -> finalize inside the conv copy"),
+            "note": "not a decode schedule: the accept reads logits given before the scan, "
+                    "which in a decode come out of that scan through the later layers and "
+                    "the LM head; not the headline",
+        }
+    del runners, fused, explicit, overlap
     torch.cuda.empty_cache()
     if cpu_seconds > 0:
         print(f"[bench] {cfg.name}: cpu baseline (~{cpu_seconds:.0f} s)", file=sys.stderr,

@@ -6,9 +6,7 @@ allocation), in the order of the reference's verify_block_parallel_replay
 (dflash_mlx/runtime.py:117-163) with the rollback moved onto the device:
 
   1. gated-delta scan of all linear layers' inputs, writing out, the final
-     state and the per-token state tape       (dflash_gdn_verify_scan; in the
-     fused form with small logits the accept's argmax runs in the same
-     launch)
+     state and the per-token state tape       (dflash_gdn_verify_scan)
   2. greedy accept on the verify logits       (dflash_greedy_accept): the
      block's drafts block[1:] against the posterior rows 0..T-2, bonus =
      posterior[matched] (runtime.py:145-147), then keep = matched + 1
@@ -113,7 +111,14 @@ class VerifyStepRunner:
     its replays come in pairs (``keep`` is the same buffer before and after
     each replay)."""
 
-    def __init__(self, shape: StepShape, device: torch.device):
+    def __init__(self, shape: StepShape, device: torch.device, overlap_accept: bool = False):
+        """overlap_accept: let the fused step run the accept's argmax inside
+        the scan's launch (and, where the windows are small, the whole step in
+        one launch).  In a decode the verify logits come out of this block's
+        scan (through the later layers and the LM head), so the accept cannot
+        start before the scan ends; those forms are schedulable only when the
+        logits are given ahead of the scan, as in a synthetic benchmark, and
+        are off by default."""
         s = shape
         self.shape = s
         self.device = device
@@ -141,20 +146,20 @@ class VerifyStepRunner:
         self._keeps = torch.zeros(2, s.B, dtype=i32, device=device)
         self._pp = 0  # index of the current keep buffer
         self.bonus = z(s.B, dt=i32)
-        self.argmax_in_scan = s.fuse_argmax()
+        self.argmax_in_scan = bool(overlap_accept) and s.fuse_argmax()
         lib = _lib.load()
         if s.conv_dim:
             self.conv_in = [z(s.B, s.K1, s.conv_dim, dt=bf) for _ in range(s.L)]
             self.qkv = [z(s.B, s.T, s.conv_dim, dt=bf) for _ in range(s.L)]
             self.conv_out = [z(s.B, s.K1, s.conv_dim, dt=bf) for _ in range(s.L)]
-        # The whole fused step in one launch (dflash_gdn_verify_step) where its
-        # limits allow and pay: argmax in the scan's launch, bf16 windows
+        # With overlap_accept, the whole fused step in one launch
+        # (dflash_gdn_verify_step) where its limits allow and pay: argmax in the scan's launch, bf16 windows
         # copied as 16-byte units, at most SINGLE_LAUNCH_MAX_CONV_BYTES of
         # them, 32 layers, 64 rows, 4 window rows.  conv_in_launch False (a
         # form kept for tests and callers with their own measurements): the
         # step launch leaves the windows to a dflash_conv_rollback after it.
         self.conv_in_launch = True
-        self.single_launch = s.single_launch()
+        self.single_launch = bool(overlap_accept) and s.single_launch()
         ws = max(int(lib.dflash_greedy_accept_workspace_bytes(s.B, s.T, s.V)),
                  int(lib.dflash_gdn_verify_step_workspace_bytes(s.B, s.T, s.V)))
         # zeroed: the single-launch step's arrival counts follow the keys
@@ -339,10 +344,12 @@ class VerifyStepRunner:
         the call, the state after keeping keep[b] = matched[b] + 1 tokens of
         this block is tape[keep[b]-1, b], which the next run_fused() picks up
         on the device.  Start with keep zeroed (the first scan then starts
-        from state).  With conv windows and small logits: one launch
-        (``single_launch``; two with large windows, the copy apart), else
-        two with the argmax in the scan's launch (``argmax_in_scan``), else
-        three."""
+        from state).  Three launches: the scan, then the accept's argmax,
+        then its finalize inside the conv-window copy.  With overlap_accept
+        (logits given before the scan) and conv windows and small logits:
+        one launch (``single_launch``; two with large windows, the copy
+        apart), else two with the argmax in the scan's launch
+        (``argmax_in_scan``)."""
         st = self._stream()
         if self.single_launch:
             self.step_single(st)

@@ -265,8 +265,10 @@ def test_step_runner_fused_matches_explicit(device, form):
     shape = StepShape(L=1, B=4, T=16, Hk=16, Hv=32, Dk=128, Dv=128, V=5000, conv_dim=512)
     runs = []
     for fused in (False, True):
-        r = VerifyStepRunner(shape, device)
-        # 1.3 MB of logits and 32 KB of windows: the default is one launch
+        assert not VerifyStepRunner(shape, device).argmax_in_scan  # dependent schedule by default
+        r = VerifyStepRunner(shape, device, overlap_accept=True)
+        # 1.3 MB of logits and 32 KB of windows: with the logits given before
+        # the scan, one launch
         assert r.argmax_in_scan and r.single_launch and r.conv_in_launch
         _set_form(r, form)
         for n in ("q", "k", "v", "g", "beta", "state"):
