@@ -10,9 +10,10 @@
 //   forward_full_attention_layer_explicit (:487-540): q/k RMSNorm, partial
 //   rotary embedding at the cache offset, KV-cache append, causal SDPA over the
 //   cache, output * sigmoid(gate).
-// The projections themselves are plain GEMMs (hipBLASLt) and stay with the
-// caller.  Cache lengths live in device memory, so a whole verify step
-// (append, attend, accept, commit) runs without a host round trip.
+// The projections are this package's GEMMs (skinny_gemm.hip at verify
+// sizes, prefill_gemm.hip over a prompt) and stay with the caller.  Cache
+// lengths live in device memory, so a whole verify step (append, attend,
+// accept, commit) runs without a host round trip.
 #include <hip/hip_runtime.h>
 #include <math.h>
 
@@ -495,6 +496,166 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const AttnParams p) {
       pack2(o0 * inv * g0, o1 * inv * g1);
 }
 
+// ------------------------------------------------ attention over a prompt
+// The same causal SDPA + gate for the P rows of a prompt pass (one sequence,
+// cache length lens[0] before the prompt; prompt row i sees keys 0 ..
+// lens[0] + i).  One workgroup per (16-row query block, kv head), one wave
+// per query head of the group, as the verify kernel; instead of one key
+// split per workgroup, the workgroup walks every 64-key tile its block can
+// see, keeping a running max m, sum l and unnormalised O per row in
+// registers (rescaled by exp(m_old - m_new) when the max grows), so nothing
+// goes through a workspace.  Each tile's K and V^T are loaded once per
+// workgroup into LDS (the next tile's loads issued before this tile's
+// products), shared by the REP waves.  Query blocks are launched last block
+// first: later blocks see more keys and set the launch's end.
+struct AttnPrefillParams {
+  const uint16_t* q;         // [P, Hq, D]
+  const uint16_t* k_cache;   // [Hkv, Smax, D]
+  const uint16_t* vt_cache;  // [Hkv, D, Smax]
+  const int32_t* lens;       // [1]
+  const uint16_t* gate_src;  // prompt row i's gate of head qh at i*gate_row_stride + qh*2D + D
+  int64_t gate_row_stride;
+  uint16_t* out;             // [P, Hq*D]
+  int P, Hq, Hkv, Smax, nblk;
+  float scale;
+};
+
+template <int REP>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(const AttnPrefillParams p) {
+  constexpr int NT = 64 * REP;
+  constexpr int PIECES = KC * kHD * 2 / 16;
+  constexpr int PER = (PIECES + NT - 1) / NT;
+  __shared__ __attribute__((aligned(16))) uint16_t sK[KC][kHD + 8];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[kHD][KC + 8];
+  __shared__ __attribute__((aligned(16))) uint16_t sP[REP][16][KC + 8];
+  const int blk = p.nblk - 1 - (int)blockIdx.x;
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int qh = h * REP + wave;
+  const int base = min(max(p.lens[0], 0), p.Smax);
+  const int t0 = blk * 16;
+  const int Tb = min(16, p.P - t0);  // live rows of this block
+  const int L = min(base + t0 + Tb, p.Smax);  // keys the block's last row sees
+  const int ntiles = (L + KC - 1) / KC;
+  const uint16_t* kbase = p.k_cache + (int64_t)h * p.Smax * kHD;
+  const uint16_t* vbase = p.vt_cache + (int64_t)h * kHD * p.Smax;
+  u32x4 kv[PER], vv[PER];
+  auto load_tile = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = min(tid + NT * i, PIECES - 1);
+      kv[i] = ld16(kbase + (int64_t)(k0 + (e >> 4)) * kHD + (e & 15) * 8);
+      vv[i] = ld16(vbase + (int64_t)(e >> 3) * p.Smax + k0 + (e & 7) * 8);
+    }
+  };
+  load_tile(0);
+  const int tq = r16 < Tb ? r16 : Tb - 1;
+  const uint16_t* qr = p.q + ((int64_t)(t0 + tq) * p.Hq + qh) * kHD + g4 * 8;
+  u32x4 qa[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const u32x4 v = ld16(qr + 32 * k);
+    qa[k] = r16 < Tb ? v : u32x4{0u, 0u, 0u, 0u};
+  }
+  float m[4], l[4];
+  f32x4 o[8];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    m[e] = -INFINITY;
+    l[e] = 0.f;
+  }
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int j = 0; j < ntiles; ++j) {
+    const int k0 = j * KC;
+    __syncthreads();  // every wave is done with the previous tile's K and V^T
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int e = tid + NT * i;
+      if (e < PIECES) {
+        *reinterpret_cast<u32x4*>(&sK[e >> 4][(e & 15) * 8]) = kv[i];
+        *reinterpret_cast<u32x4*>(&sV[e >> 3][(e & 7) * 8]) = vv[i];
+      }
+    }
+    __syncthreads();
+    if (j + 1 < ntiles) load_tile(k0 + KC);  // in flight during this tile's products
+    f32x4 sacc[4];
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, qa[k]),
+            __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&sK[16 * n + r16][32 * k + 8 * g4])),
+            acc, 0, 0, 0);
+      sacc[n] = acc;
+    }
+    float sv[4][4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = 4 * g4 + e;
+      const int last = base + t0 + t;  // the last key row t sees
+      float mx = -INFINITY;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const int key = k0 + 16 * n + r16;
+        const bool ok = (t < Tb) && (key <= last) && (key < L);
+        sv[n][e] = ok ? sacc[n][e] * p.scale : -INFINITY;
+        mx = fmaxf(mx, sv[n][e]);
+      }
+      const float mn = fmaxf(m[e], row16_max(mx));
+      const float alpha = (m[e] == -INFINITY) ? 0.f : __expf(m[e] - mn);
+      const float ms = mn == -INFINITY ? 0.f : mn;
+      float sum = 0.f;
+#pragma unroll
+      for (int n = 0; n < 4; ++n) {
+        const float pe = __expf(sv[n][e] - ms);
+        sv[n][e] = pe;
+        sum += pe;
+      }
+      l[e] = l[e] * alpha + row16_sum(sum);
+      m[e] = mn;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) o[dt][e] *= alpha;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int n = 0; n < 4; ++n) sP[wave][4 * g4 + e][16 * n + r16] = f32_to_bf16_rne(sv[n][e]);
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's P writes are visible to it
+    u32x4 pa[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) pa[k] = *reinterpret_cast<const u32x4*>(&sP[wave][r16][32 * k + 8 * g4]);
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, pa[k]),
+            __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(&sV[16 * dt + r16][32 * k + 8 * g4])),
+            o[dt], 0, 0, 0);
+  }
+  // out = O / l * sigmoid(gate); lane (r16, g4) holds row 4 g4 + e, feature 16 dt + r16.
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int t = 4 * g4 + e;
+    if (t >= Tb) continue;
+    const int64_t row = t0 + t;
+    const float inv = 1.f / l[e];
+    const uint16_t* gr = p.gate_src + row * p.gate_row_stride + qh * 2 * kHD + kHD;
+    uint16_t* orow = p.out + (row * p.Hq + qh) * kHD;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const float gt = bf16_bits_to_f32(gr[16 * dt + r16]);
+      orow[16 * dt + r16] = f32_to_bf16_rne(o[dt][e] * inv * (1.f / (1.f + __expf(-gt))));
+    }
+  }
+}
+
 // --------------------------------------------------------- commit an accept
 // keep[b] = matched[b] + 1 (the block's first token plus the accepted drafts,
 // runtime.py:146), lens[b] += keep[b] (the KV trim of adapters.py:505-508
@@ -692,6 +853,43 @@ extern "C" int dflash_attn_verify(const void* q, const void* k_cache, const void
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   hipLaunchKernelGGL(attn_combine_kernel, dim3(B * T, Hq), dim3(256), 0, s, p);
+  return to_status(hipGetLastError());
+}
+
+extern "C" int dflash_attn_prefill(const void* q, const void* k_cache, const void* vt_cache,
+                                   const int32_t* lens, const void* gate_src,
+                                   int64_t gate_row_stride, void* out, int P, int Hq, int Hkv,
+                                   int D, int Smax, float scale, void* stream) {
+  if (P < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || Hq / Hkv > 4) return DFLASH_ERR_SHAPE;
+  if (D != kHD) return DFLASH_ERR_UNSUPPORTED;
+  if (Smax <= 0 || Smax % KC != 0 || Hkv > 65535) return DFLASH_ERR_SHAPE;
+  if (gate_row_stride < (int64_t)2 * Hq * D) return DFLASH_ERR_SHAPE;
+  if (P == 0) return DFLASH_OK;
+  if (q == nullptr || k_cache == nullptr || vt_cache == nullptr || lens == nullptr ||
+      gate_src == nullptr || out == nullptr)
+    return DFLASH_ERR_NULL;
+  if (((uintptr_t)q & 15) || ((uintptr_t)k_cache & 15) || ((uintptr_t)vt_cache & 15) ||
+      ((uintptr_t)gate_src & 1) || ((uintptr_t)out & 1))
+    return DFLASH_ERR_ALIGN;
+  AttnPrefillParams p{};
+  p.q = static_cast<const uint16_t*>(q);
+  p.k_cache = static_cast<const uint16_t*>(k_cache);
+  p.vt_cache = static_cast<const uint16_t*>(vt_cache);
+  p.lens = lens;
+  p.gate_src = static_cast<const uint16_t*>(gate_src);
+  p.gate_row_stride = gate_row_stride;
+  p.out = static_cast<uint16_t*>(out);
+  p.P = P; p.Hq = Hq; p.Hkv = Hkv; p.Smax = Smax;
+  p.nblk = (int)ceil_div(P, 16);
+  p.scale = scale;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)p.nblk, (unsigned)Hkv);
+  switch (Hq / Hkv) {
+    case 1: hipLaunchKernelGGL(attn_prefill_kernel<1>, grid, dim3(64), 0, s, p); break;
+    case 2: hipLaunchKernelGGL(attn_prefill_kernel<2>, grid, dim3(128), 0, s, p); break;
+    case 3: hipLaunchKernelGGL(attn_prefill_kernel<3>, grid, dim3(192), 0, s, p); break;
+    default: hipLaunchKernelGGL(attn_prefill_kernel<4>, grid, dim3(256), 0, s, p); break;
+  }
   return to_status(hipGetLastError());
 }
 

@@ -19,7 +19,7 @@ LIB_NAME = "libdflash_gfx950.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 
 SOURCES = ["gdn_scan.hip", "gdn_layer_ops.hip", "gdn_chunked.hip", "greedy_accept.hip", "lm_head_argmax.hip",
-           "rollback.hip", "model_ops.hip", "skinny_gemm.hip", "abi.cpp"]
+           "rollback.hip", "model_ops.hip", "skinny_gemm.hip", "prefill_gemm.hip", "abi.cpp"]
 HEADERS = ["device_common.h", "host_common.h", "accept_common.h"]
 
 # -packed-fp32-ops off: v_pk_{add,mul,fma}_f32 have given silent wrong results

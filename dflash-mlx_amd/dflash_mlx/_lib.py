@@ -85,6 +85,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dflash_gemm_bf16_swiglu_tiled_normed": (
         _I, [_VP, _I64, _VP, _VP, _I, ctypes.c_float, _VP, _VP, _VP, _I64, _I, _I, _I, _I, _VP,
              _SZ, _VP]),
+    "dflash_gemm_bf16_tiled_prefill": (_I, [_VP, _I64, _VP, _VP, _I64, _I, _I, _I, _VP]),
+    "dflash_gemm_bf16_swiglu_tiled_prefill": (_I, [_VP, _I64, _VP, _VP, _I64, _I, _I, _I, _VP]),
     "dflash_splitk_reduce": (_I, [_VP, _I, _I, _I, _VP, _I64, _VP]),
     "dflash_swiglu": (_I, [_VP, _VP, _I, _I, _VP]),
     "dflash_attn_prep": (
@@ -97,6 +99,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I,
         [_VP, _VP, _VP, _VP, _VP, _I64, _VP, _I, _I, _I, _I, _I, _I, _I, ctypes.c_float, _VP,
          _SZ, _VP],
+    ),
+    "dflash_attn_prefill": (
+        _I,
+        [_VP, _VP, _VP, _VP, _VP, _I64, _VP, _I, _I, _I, _I, _I, ctypes.c_float, _VP],
     ),
     "dflash_commit_accept": (_I, [_VP, _VP, _VP, _I, _I, _VP]),
     "dflash_greedy_accept_workspace_bytes": (_SZ, [_I, _I, _I]),

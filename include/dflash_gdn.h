@@ -687,6 +687,34 @@ int dflash_gemm_bf16_swiglu_tiled_normed(const void* h, int64_t h_row_stride,
                                          size_t workspace_bytes, void* stream);
 
 /*
+ * Prompt-sized projection GEMMs over the same fragment-tiled weights:
+ * out[M, N] = bf16(x[M, K] . w[N, K]^T) for M = the rows of a prompt pass
+ * (any M >= 0; built for hundreds to thousands of rows), fp32 accumulation
+ * with one chain per output in k order.
+ *
+ * Replaces every nn.Linear of the target's layers during the prompt pass
+ * (Qwen3_5TextModel over the whole prompt, dflash_mlx/runtime.py:384-390 ->
+ * forward_dflash, custom_qwen35_model.py:883-1001; the Linears of :726-736
+ * and mlx-lm Qwen3NextAttention / Qwen3NextMLP), where each weight is
+ * contracted against all P rows at once on the matrix cores instead of
+ * being streamed once per 16-row verify block.
+ * w_tiled is dflash_weight_tile_bf16's layout (N % 16 == 0, K % 64 == 0).
+ * dflash_gemm_bf16_swiglu_tiled_prefill takes the tiled w_pairs of
+ * dflash_gemm_bf16_swiglu (N % 32 == 0) and writes out[M, N/2] =
+ * bf16(silu(x . G^T) * (x . U^T)).  x: 16-byte aligned, row stride a
+ * multiple of 8 elements (>= K); out: 8-byte aligned, row stride a multiple
+ * of 4 (>= N, or N/2).
+ */
+int dflash_gemm_bf16_tiled_prefill(const void* x, int64_t x_row_stride,
+                                   const void* w_tiled, void* out,
+                                   int64_t out_row_stride, int M, int N, int K,
+                                   void* stream);
+int dflash_gemm_bf16_swiglu_tiled_prefill(const void* x, int64_t x_row_stride,
+                                          const void* w_pairs_tiled, void* out,
+                                          int64_t out_row_stride, int M, int N,
+                                          int K, void* stream);
+
+/*
  * out[m, n] = bf16(sum_s partials[s, m, n]) for partials fp32 [nsplit, M, N]
  * (N % 4 == 0), out bf16 with row stride out_row_stride.
  */
@@ -747,6 +775,26 @@ int dflash_attn_verify(const void* q, const void* k_cache,
                        void* out, int B, int T, int Hq, int Hkv, int D,
                        int Smax, int max_len, float scale, void* workspace,
                        size_t workspace_bytes, void* stream);
+
+/*
+ * The same gated attention over a prompt pass of one sequence (the SDPA +
+ * sigmoid gate of custom_qwen35_model.py:524-534 with the whole prompt as
+ * queries, reached from the prefill at dflash_mlx/runtime.py:384-390): the
+ * prompt's keys and values are already in the cache (dflash_attn_prep with
+ * B = 1, T = P), and prompt row i attends to cache positions 0 .. lens[0] + i.
+ *   out[i, h*D .. h*D+D) = bf16(softmax(scale * q_i k^T) v * sigmoid(gate_i))
+ * q: [P, Hq, D] bf16 (dflash_attn_prep's q_out); k_cache [Hkv, Smax, D] and
+ * vt_cache [Hkv, D, Smax] of the sequence; lens: device int32 [1], the
+ * cache length before the prompt (the kernel clamps it to [0, Smax] and reads
+ * no position at or past Smax); gate_src: the projection rows (row i's gate of
+ * head h at i * gate_row_stride + h*2D + D); out [P, Hq*D] bf16.  Online
+ * softmax over 64-key tiles on MFMA, no workspace.
+ * Supported: D == 128, Hq / Hkv <= 4, Smax % 64 == 0.
+ */
+int dflash_attn_prefill(const void* q, const void* k_cache, const void* vt_cache,
+                        const int32_t* lens, const void* gate_src,
+                        int64_t gate_row_stride, void* out, int P, int Hq,
+                        int Hkv, int D, int Smax, float scale, void* stream);
 
 /*
  * Commit a greedy accept on the device: keep[b] = clamp(matched[b], 0, T-1)

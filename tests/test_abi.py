@@ -49,6 +49,8 @@ def test_header_declares_expected_entry_points():
         "dflash_gemm_tail_workspace_bytes",
         "dflash_gemm_bf16_tiled_residual_norm",
         "dflash_gemm_bf16_tiled_normed", "dflash_gemm_bf16_swiglu_tiled_normed",
+        "dflash_gemm_bf16_tiled_prefill", "dflash_gemm_bf16_swiglu_tiled_prefill",
+        "dflash_attn_prefill",
     ])
 
 
@@ -194,3 +196,92 @@ def test_scan_with_argmax_and_keys_accept_validation(lib):
     assert keys(K1=9) == -3                     # more window rows than one lane holds
     assert keys(elem=3) == -3
     assert keys(N=0) == -2
+
+
+def test_verify_step_validation(lib):
+    """The single-launch verify step refuses, before any launch: more accept
+    rows than one finishing workgroup holds (N > 64), more window rows than
+    it copies (K1 > 4), more layers than one launch's tables (L > 32), the
+    next keep buffer equal to the one the scan reads, a workspace off a
+    256-byte boundary, and conv rows that are not whole 16-byte units."""
+    d = ctypes.c_void_p(0x1000)
+    keep_in, keep_out = ctypes.c_void_p(0x3000), ctypes.c_void_p(0x4000)
+    f = lib.dflash_gdn_verify_step
+    ws = lib.dflash_gdn_verify_step_workspace_bytes(1, 16, 1024)
+    assert ws > 0
+
+    def step(N=16, K1=3, L=1, out_keep=keep_out, work=ctypes.c_void_p(0x100000), C=8192):
+        tab = (ctypes.c_void_p * max(L, 1))(*([0x1000] * max(L, 1)))
+        return f(d, d, d, d, d, d, d, keep_in, 16, 1, d, None, d, 1, 16, 4, 4, 64, 64, None,
+                 d, 0, 16 * 1024, 1024, 1, N, 1024,
+                 d, 16, 15, d, d, d, 1, out_keep,
+                 tab, tab, tab, L, K1, C, 16 * C, C,
+                 work, ws * 8, None)
+
+    assert step(N=65) == -3
+    assert step(K1=5) == -3
+    assert step(L=33) == -3
+    assert step(out_keep=keep_in) == -2
+    assert step(work=ctypes.c_void_p(0x100008)) == -4
+    assert step(C=8190) == -4          # 16 380-byte rows: not 16-byte units
+    assert step(out_keep=None) == -1
+
+
+def test_gemm_tail_workspace_and_normed_validation(lib):
+    """The tiled GEMMs' tail-split workspace must hold
+    dflash_gemm_tail_workspace_bytes() bytes on a 256-byte boundary; the
+    normed forms take K <= 16384 (their LDS copy of the norm weight)."""
+    d = ctypes.c_void_p(0x1000)
+    tail = lib.dflash_gemm_tail_workspace_bytes()
+    assert tail > 1024
+    aligned, odd = ctypes.c_void_p(0x200000), ctypes.c_void_p(0x200080)
+    tiled = lib.dflash_gemm_bf16_tiled
+    assert tiled(d, 2560, d, d, 2560, 16, 2560, 2560, 1, 32, 4, aligned, tail - 1, None) == -5
+    assert tiled(d, 2560, d, d, 2560, 16, 2560, 2560, 1, 32, 4, odd, tail, None) == -4
+    sw = lib.dflash_gemm_bf16_swiglu_tiled
+    assert sw(d, 2560, d, d, 9216, 16, 18432, 2560, 4, aligned, tail - 1, None) == -5
+    assert sw(d, 2560, d, d, 9216, 16, 18432, 2560, 4, odd, tail, None) == -4
+    normed = lib.dflash_gemm_bf16_tiled_normed
+    assert normed(d, 2560, d, d, 160, 1e-6, None, d, d, 2560, 16, 2560, 2560, 1, 32, 4,
+                  aligned, tail - 1, None) == -5
+    assert normed(d, 20480, d, d, 160, 1e-6, None, d, d, 2560, 16, 2560, 20480, 1, 32, 4,
+                  aligned, tail, None) == -2
+    sw_normed = lib.dflash_gemm_bf16_swiglu_tiled_normed
+    assert sw_normed(d, 2560, d, d, 160, 1e-6, None, d, d, 9216, 16, 18432, 2560, 4,
+                     odd, tail, None) == -4
+    assert sw_normed(d, 20480, d, d, 160, 1e-6, None, d, d, 9216, 16, 18432, 20480, 4,
+                     aligned, tail, None) == -2
+
+
+def test_prefill_gemm_validation(lib):
+    """The prompt-sized GEMMs refuse shapes the fragment layout cannot hold
+    and misaligned rows before any launch; M = 0 is a no-op."""
+    d = ctypes.c_void_p(0x1000)
+    f = lib.dflash_gemm_bf16_tiled_prefill
+    assert f(d, 2560, d, d, 2560, 0, 2560, 2560, None) == 0
+    assert f(d, 2560, d, d, 2560, 100, 2568, 2560, None) == -2     # N % 16
+    assert f(d, 2560, d, d, 2560, 100, 2560, 2592, None) == -2     # K % 64
+    assert f(d, 2000, d, d, 2560, 100, 2560, 2560, None) == -2     # x rows shorter than K
+    assert f(d, 2560, d, d, 2000, 100, 2560, 2560, None) == -2     # out rows shorter than N
+    assert f(None, 2560, d, d, 2560, 100, 2560, 2560, None) == -1
+    assert f(ctypes.c_void_p(0x1008), 2560, d, d, 2560, 100, 2560, 2560, None) == -4
+    assert f(d, 2564, d, d, 2560, 100, 2560, 2560, None) == -4     # x stride % 8
+    assert f(d, 2560, d, ctypes.c_void_p(0x1004), 2560, 100, 2560, 2560, None) == -4
+    g = lib.dflash_gemm_bf16_swiglu_tiled_prefill
+    assert g(d, 2560, d, d, 9216, 100, 18448, 2560, None) == -2   # N % 32
+    assert g(d, 2560, d, d, 9000, 100, 18432, 2560, None) == -2   # out rows shorter than N/2
+    assert g(d, 2560, d, d, 9218, 100, 18432, 2560, None) == -4   # out stride % 4
+
+
+def test_attn_prefill_validation(lib):
+    d = ctypes.c_void_p(0x1000)
+    f = lib.dflash_attn_prefill
+    assert f(d, d, d, d, d, 5120, d, 16, 16, 4, 64, 4096, 0.09, None) == -3    # D != 128
+    assert f(d, d, d, d, d, 5120, d, 16, 20, 4, 128, 4096, 0.09, None) == -2   # Hq % Hkv
+    assert f(d, d, d, d, d, 5120, d, 16, 16, 2, 128, 4096, 0.09, None) == -2   # Hq / Hkv > 4
+    assert f(d, d, d, d, d, 5120, d, 16, 16, 4, 128, 4000, 0.09, None) == -2   # Smax % 64
+    assert f(d, d, d, d, d, 100, d, 16, 16, 4, 128, 4096, 0.09, None) == -2    # gate stride
+    assert f(d, d, d, None, d, 5120, d, 16, 16, 4, 128, 4096, 0.09, None) == -1
+    assert f(d, ctypes.c_void_p(0x1008), d, d, d, 5120, d, 16, 16, 4, 128, 4096, 0.09,
+             None) == -4
+    assert f(None, None, None, None, None, 5120, None, 0, 16, 4, 128, 4096, 0.09, None) == 0

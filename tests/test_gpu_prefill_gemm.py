@@ -1,0 +1,133 @@
+"""GPU parity of the prompt-sized GEMMs (dflash_gemm_bf16_tiled_prefill,
+dflash_gemm_bf16_swiglu_tiled_prefill) over the fragment-tiled weights.
+
+* Against an fp32 torch reference of the same bf16 inputs: out within one
+  bf16 rounding of the reference (|err| <= 2^-8 |ref| + 1e-3 * rms(ref)); the
+  gated form against silu(x.G^T) * (x.U^T) in fp32 with the same bound.
+* Bit for bit against the verify-sized tiled GEMM with one wave per k-range
+  and one split (dflash_gemm_bf16_tiled, k_waves 1, nsplit 1): both keep one
+  fp32 chain per output over the k-steps in order, so at M <= 64 their sums
+  are the same bits — a check that pins the k-slot order of the activation
+  operand, which the fp32 bound would not catch at small K.
+Shapes: every projection of the config-c4 layers at prompt lengths, M and N
+tails (M not a multiple of 128, N not a multiple of 256), K = 64.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from dflash_mlx import _lib
+
+pytestmark = pytest.mark.gpu
+
+C4_PROJ = [(12352, 2560), (2560, 4096), (5120, 2560), (2560, 2048), (2560, 9216)]
+
+
+def _tile(w, device):
+    n, k = w.shape
+    lib = _lib.load()
+    t = torch.empty(int(lib.dflash_weight_tile_bytes(n, k)) // 2, dtype=torch.bfloat16,
+                    device=device)
+    _lib.call("dflash_weight_tile_bf16", w.data_ptr(), w.stride(0), t.data_ptr(), n, k,
+              _lib.stream_handle(device))
+    return t
+
+
+def _inputs(device, M, N, K, seed):
+    g = torch.Generator(device=device).manual_seed(seed)
+    x = torch.randn(M, K, generator=g, device=device).bfloat16()
+    w = (0.02 * torch.randn(N, K, generator=g, device=device)).bfloat16()
+    return x, w
+
+
+def _prefill(device, x, wt, M, N, K, swiglu=False):
+    n_out = N // 2 if swiglu else N
+    out = torch.full((M, n_out), float("nan"), dtype=torch.bfloat16, device=device)
+    name = "dflash_gemm_bf16_swiglu_tiled_prefill" if swiglu else "dflash_gemm_bf16_tiled_prefill"
+    _lib.call(name, x.data_ptr(), x.stride(0), wt.data_ptr(), out.data_ptr(), out.stride(0), M, N,
+              K, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    return out
+
+
+def _check(out, ref):
+    scale = ref.pow(2).mean().sqrt().item()
+    assert torch.isfinite(out).all()
+    err = ((out.float() - ref).abs() - (2 ** -8) * ref.abs()).max().item()
+    assert err <= 1e-3 * scale, (err, scale)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 16, 64), (17, 272, 128), (128, 256, 64),
+                                   (300, 1040, 640), (129, 4112, 192), (1000, 48, 2560)])
+def test_prefill_gemm_ragged(device, M, N, K):
+    print(f"[prefill gemm] M={M} N={N} K={K}", flush=True)
+    x, w = _inputs(device, M, N, K, seed=M + 3 * N + K)
+    out = _prefill(device, x, _tile(w, device), M, N, K)
+    _check(out, x.float() @ w.float().t())
+
+
+@pytest.mark.parametrize("N,K", C4_PROJ)
+def test_prefill_gemm_c4_projections(device, N, K):
+    M = 1100
+    print(f"[prefill gemm] c4 projection M={M} N={N} K={K}", flush=True)
+    x, w = _inputs(device, M, N, K, seed=N + K)
+    out = _prefill(device, x, _tile(w, device), M, N, K)
+    _check(out, x.float() @ w.float().t())
+
+
+@pytest.mark.parametrize("M,N,K", [(16, 2560, 2560), (37, 1040, 640), (64, 18432, 256),
+                                   (1, 16, 64)])
+def test_prefill_gemm_matches_verify_gemm_bits(device, M, N, K):
+    """The same bits as the verify-sized tiled GEMM with one k-range per wave
+    and one split, which adds the same products in the same order."""
+    print(f"[prefill gemm] vs verify gemm M={M} N={N} K={K}", flush=True)
+    x, w = _inputs(device, M, N, K, seed=7 * M + N)
+    wt = _tile(w, device)
+    out = _prefill(device, x, wt, M, N, K)
+    ref = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=device)
+    _lib.call("dflash_gemm_bf16_tiled", x.data_ptr(), K, wt.data_ptr(), ref.data_ptr(), N, M, N, K,
+              1, 16, 1, None, 0, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("M,I,K", [(300, 9216, 2560), (5, 16, 64), (129, 272, 192)])
+def test_prefill_gemm_swiglu(device, M, I, K):
+    """Gated form over the w_pairs layout (32-row blocks: 16 gate rows, then
+    the 16 matching up rows)."""
+    print(f"[prefill gemm] swiglu M={M} I={I} K={K}", flush=True)
+    g = torch.Generator(device=device).manual_seed(M + I)
+    x = torch.randn(M, K, generator=g, device=device).bfloat16()
+    gate = (0.02 * torch.randn(I, K, generator=g, device=device)).bfloat16()
+    up = (0.02 * torch.randn(I, K, generator=g, device=device)).bfloat16()
+    pairs = torch.stack([gate.view(I // 16, 16, K), up.view(I // 16, 16, K)], 1).reshape(2 * I, K)
+    out = _prefill(device, x, _tile(pairs.contiguous(), device), M, 2 * I, K, swiglu=True)
+    gf, uf = x.float() @ gate.float().t(), x.float() @ up.float().t()
+    _check(out, torch.nn.functional.silu(gf) * uf)
+    # the same bits as the verify-sized gated GEMM at M <= 64 rows (one k-range per wave)
+    if M <= 64:
+        wt = _tile(pairs.contiguous(), device)
+        ref = torch.full((M, I), float("nan"), dtype=torch.bfloat16, device=device)
+        _lib.call("dflash_gemm_bf16_swiglu_tiled", x.data_ptr(), K, wt.data_ptr(), ref.data_ptr(),
+                  I, M, 2 * I, K, 1, None, 0, _lib.stream_handle(device))
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
+
+
+def test_prefill_gemm_strided_rows(device):
+    """Activation and output rows with strides larger than K and N (views
+    into wider buffers)."""
+    M, N, K = 200, 528, 320
+    x, w = _inputs(device, M, N, K, seed=11)
+    xw = torch.zeros(M, K + 64, dtype=torch.bfloat16, device=device)
+    xw[:, 8:8 + K] = x
+    xv = xw[:, 8:8 + K]
+    wt = _tile(w, device)
+    ow = torch.full((M, N + 12), float("nan"), dtype=torch.bfloat16, device=device)
+    ov = ow[:, 4:4 + N]
+    _lib.call("dflash_gemm_bf16_tiled_prefill", xv.data_ptr(), xv.stride(0), wt.data_ptr(),
+              ov.data_ptr(), ov.stride(0), M, N, K, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    _check(ov, x.float() @ w.float().t())
+    assert torch.isnan(ow[:, :4].float()).all() and torch.isnan(ow[:, 4 + N:].float()).all()
