@@ -1,0 +1,246 @@
+"""The prompt pass of the hybrid target on MI355X.
+
+The reference runs the prompt through the target in one forward
+(dflash_mlx/runtime.py:384-390 -> forward_with_hidden_states ->
+Qwen3_5TextModel.forward_dflash, custom_qwen35_model.py:883-1001): every
+decoder layer sees all P prompt rows at once, each gated-delta layer runs
+gated_delta_update over the P tokens (:790-801) from the cached state, and
+each attention layer appends P keys and attends causally (:487-540).
+
+``HybridPrefill`` does the same over the caches of a ``HybridVerifyRunner``
+(one sequence), with launches sized to the prompt:
+
+* the projections on the prompt-sized MFMA GEMMs
+  (``dflash_gemm_bf16_tiled_prefill``, the MLP gating fused:
+  ``dflash_gemm_bf16_swiglu_tiled_prefill``) over the verify GEMMs'
+  fragment-tiled weights (a stacked projection whose row count is not a
+  multiple of 16 gets a zero-padded tiled copy of its own);
+* per gated-delta layer: the prologue over the P tokens
+  (``dflash_gdn_prologue``: conv1d + silu from the cached window, q/k norms,
+  g and beta, the new window), the chunked WY-form scan on the matrix cores
+  (``dflash_gdn_chunked_prefill``) from the cached state, the gated RMSNorm;
+* per attention layer: q/k norm + rotary + KV append at the cached length
+  (``dflash_attn_prep`` with T = P), causal attention over cache + prompt
+  (``dflash_attn_prefill``);
+* residual adds and norms (``dflash_embed_rmsnorm``, ``dflash_add_rmsnorm``,
+  ``dflash_add_rmsnorm_capture`` for the target hidden states at the
+  runner's capture layers).
+
+Before the pass the recurrent states the runner would roll back on its next
+load (tape[keep - 1] when keep >= 1) are gathered into its state buffers
+(``dflash_tape_select``); each layer's final state is written to its tape's
+slab 0 and keep becomes 1, so the next verify scan starts from it with no
+copy.  Prompts longer than ``max_rows`` run as consecutive passes over the
+caches the previous one left.  No launch here has a CPU counterpart: every
+call goes to this package's gfx950 library.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .gdn_layer import QK_NORM_EPS
+
+
+class HybridPrefill:
+    """Prompt pass over the caches of ``runner`` (B = 1)."""
+
+    def __init__(self, runner, max_rows: int = 8192):
+        if runner.B != 1:
+            raise ValueError("the prompt pass runs one sequence (runner.B == 1)")
+        cfg = runner.cfg
+        lc = cfg.linear
+        if lc.linear_key_head_dim != 128 or lc.linear_value_head_dim != 128 or cfg.head_dim != 128:
+            raise ValueError("the prompt pass needs 128-wide gated-delta and attention heads")
+        self.run, self.cfg = runner, cfg
+        self.max_rows = int(max_rows)
+        self.rows_cap = 0
+        self._lib = _lib.load()
+        self._weights()
+
+    # ------------------------------------------------------------ weights
+    def _tiled(self, lw, name):
+        """(fragment-tiled weight, its row count): the verify GEMMs' copy when
+        there is one, else a tiled copy zero-padded to whole 16-row tiles."""
+        w = lw[name]
+        n, k = w.shape
+        if n % 16 == 0:
+            key = name + "_tiled"
+            src = w
+        else:
+            key = name + "_ptiled"
+            src = None
+        if key not in lw:
+            if src is None:
+                src = torch.zeros(-(-n // 16) * 16, k, dtype=w.dtype, device=w.device)
+                src[:n].copy_(w)
+            npad = src.shape[0]
+            t = torch.empty(int(self._lib.dflash_weight_tile_bytes(npad, k)) // 2,
+                            dtype=torch.bfloat16, device=w.device)
+            _lib.call("dflash_weight_tile_bf16", src.data_ptr(), src.stride(0), t.data_ptr(), npad,
+                      k, _lib.stream_handle(w.device))
+            lw[key] = t
+        return lw[key], -(-n // 16) * 16
+
+    def _weights(self):
+        cfg = self.cfg
+        self.w = []
+        for i, lw in enumerate(self.run.w.layers):
+            names = ["w_gu_pairs", "w_down"] + (["w_in", "w_out"] if cfg.is_linear(i)
+                                                else ["w_qkv", "w_o"])
+            self.w.append({n: self._tiled(lw, n) for n in names})
+        torch.cuda.synchronize(self.run.device)
+        # the stacked gated-delta projection's (padded) row count: the row
+        # stride of its output
+        self.in_stride = max((d["w_in"][1] for d in self.w if "w_in" in d), default=0)
+
+    # ------------------------------------------------------------ buffers
+    def _ensure(self, P: int) -> None:
+        if P <= self.rows_cap:
+            return
+        cfg, lc, dev = self.cfg, self.cfg.linear, self.run.device
+        H, I = cfg.hidden_size, cfg.intermediate_size
+        Hv, Dv, C = lc.linear_num_value_heads, lc.linear_value_head_dim, lc.conv_dim
+        Hq, D = cfg.num_attention_heads, cfg.head_dim
+        bf, f32 = torch.bfloat16, torch.float32
+        e = lambda *s, dt=bf: torch.empty(*s, dtype=dt, device=dev)  # noqa: E731
+        self.tokens = e(P, dt=torch.int32)
+        self.h, self.xn, self.r = e(P, H), e(P, H), e(P, H)
+        self.mlp_act = e(P, I)
+        self.proj = e(P, max(self.in_stride, 16))
+        self.act = e(P, C)
+        self.g, self.beta = e(P, Hv, dt=f32), e(P, Hv, dt=f32)
+        self.scan_out, self.gnorm = e(P, Hv, Dv), e(P, Hv, Dv)
+        self.aproj = e(P, cfg.attn_proj_rows)
+        self.q = e(P, Hq, D)
+        self.attn_out = e(P, Hq * D)
+        self.conv_new = e(1, lc.linear_conv_kernel_dim - 1, C)
+        ws = int(self._lib.dflash_gdn_chunked_prefill_workspace_bytes(
+            1, P, Hv, lc.linear_key_head_dim, Dv))
+        self.chunk_ws = e(max(ws, 16), dt=torch.uint8)
+        self.rows_cap = P
+
+    # ------------------------------------------------------------ the pass
+    def resolve_states(self, stream) -> None:
+        """state[l] = tape[l][keep - 1] where keep >= 1 (the rollback the next
+        verify scan would have done on load), then keep = 0."""
+        run = self.run
+        n = len(run.state)
+        if n == 0:
+            return
+        lc = self.cfg.linear
+        S = lc.linear_num_value_heads * lc.linear_value_head_dim * lc.linear_key_head_dim
+        for l0 in range(0, n, 32):
+            m = min(32, n - l0)
+            states = _lib.ptr_array(run.state[l0:l0 + m])
+            _lib.call("dflash_tape_select", _lib.ptr_array(run.tape[l0:l0 + m]), states, states,
+                      run.keep.data_ptr(), m, 1, run.T, S, 0, stream)
+        run.keep.zero_()
+
+    def forward(self, tokens: torch.Tensor, norm_out: torch.Tensor,
+                capture_out: torch.Tensor | None) -> None:
+        """Run the prompt `tokens` (int32 [P] on the device) from the caches at
+        the runner's device-side length (run.lens[0]); write the normed hidden
+        states to norm_out [P, H] and, with capture layers set on the runner,
+        the residual stream after each of them to capture_out [P, n * H].
+        Leaves run.lens advanced by P, keep = 1 (state = tape[0]), the conv
+        windows advanced."""
+        P = int(tokens.numel())
+        stream = _lib.stream_handle(self.run.device)
+        self.resolve_states(stream)
+        for p0 in range(0, P, self.max_rows):
+            Pp = min(self.max_rows, P - p0)
+            cap = None if capture_out is None else capture_out[p0:p0 + Pp]
+            self._pass(tokens[p0:p0 + Pp], Pp, cap, stream)
+            norm_out[p0:p0 + Pp].copy_(self.xn[:Pp])
+            if p0 + Pp < P:
+                self._carry(stream)
+            self.run.lens.add_(Pp)
+
+    def _carry(self, stream) -> None:
+        """Between passes: the states the last pass wrote to tape slab 0
+        (keep = 1) become the next pass's initial states."""
+        self.resolve_states(stream)
+
+    def _pass(self, tokens, P, capture, stream):
+        run, cfg, lc = self.run, self.cfg, self.cfg.linear
+        self._ensure(P)
+        H, I = cfg.hidden_size, cfg.intermediate_size
+        C, Hk, Hv = lc.conv_dim, lc.linear_num_key_heads, lc.linear_num_value_heads
+        Dk, Dv, K = lc.linear_key_head_dim, lc.linear_value_head_dim, lc.linear_conv_kernel_dim
+        Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+        eps = float(cfg.rms_norm_eps)
+        call = _lib.call
+        L = cfg.num_hidden_layers
+        h, xn, r = self.h.data_ptr(), self.xn.data_ptr(), self.r.data_ptr()
+        self.tokens[:P].copy_(tokens)
+        layers = run.w.layers
+        call("dflash_embed_rmsnorm", run.w.embed.data_ptr(), self.tokens.data_ptr(), cfg.vocab_size,
+             layers[0]["ln_in"].data_ptr(), h, xn, P, H, eps, stream)
+        cap_ids = {layer: j for j, layer in enumerate(run.capture_layers)}
+        n_cap = len(run.capture_layers)
+        rs = self.in_stride
+        base = self.proj.data_ptr()
+        ab = (ctypes.c_int64 * 4)(P * rs, rs, P * rs, rs)
+        zs = (ctypes.c_int64 * 3)(P * rs, rs, Dv)
+        act = self.act.data_ptr()
+        scan_strides = (ctypes.c_int64 * 13)(P * C, C, Dk, P * C, C, Dk, P * C, C, Dv,
+                                             P * Hv, Hv, P * Hv, Hv)
+        arows = cfg.attn_proj_rows
+        gi = ai = 0
+        for i in range(L):
+            lw, tw = layers[i], self.w[i]
+            if cfg.is_linear(i):
+                gw = lw["gdn"]
+                wt, n = tw["w_in"]
+                call("dflash_gemm_bf16_tiled_prefill", xn, H, wt.data_ptr(), base, rs, P, n, H, stream)
+                a_ptr, b_ptr = base + 2 * (C + Hv * Dv + Hv), base + 2 * (C + Hv * Dv)
+                call("dflash_gdn_prologue", base, P * rs, rs, run.conv[gi].data_ptr(),
+                     gw.conv_weight.data_ptr(), a_ptr, b_ptr, ab, gw.A_log.data_ptr(),
+                     gw.dt_bias.data_ptr(), act, self.g.data_ptr(), self.beta.data_ptr(),
+                     self.conv_new.data_ptr(), 1, P, K, Hk, Hv, Dk, Dv, QK_NORM_EPS, stream)
+                run.conv[gi].copy_(self.conv_new)
+                call("dflash_gdn_chunked_prefill", act, act + 2 * Hk * Dk, act + 4 * Hk * Dk,
+                     self.g.data_ptr(), self.beta.data_ptr(), run.state[gi].data_ptr(),
+                     self.scan_out.data_ptr(), run.tape[gi][0].data_ptr(), 1, P, Hk, Hv, Dk, Dv,
+                     scan_strides, self.chunk_ws.data_ptr(), self.chunk_ws.numel(), stream)
+                call("dflash_gdn_gated_rmsnorm", self.scan_out.data_ptr(), base + 2 * C, zs,
+                     gw.norm_weight.data_ptr(), self.gnorm.data_ptr(), 1, P, Hv, Dv, eps, stream)
+                wt, n = tw["w_out"]
+                call("dflash_gemm_bf16_tiled_prefill", self.gnorm.data_ptr(), Hv * Dv, wt.data_ptr(),
+                     r, H, P, n, Hv * Dv, stream)
+                gi += 1
+            else:
+                wt, n = tw["w_qkv"]
+                ap = self.aproj.data_ptr()
+                call("dflash_gemm_bf16_tiled_prefill", xn, H, wt.data_ptr(), ap, arows, P, n, H,
+                     stream)
+                call("dflash_attn_prep", ap, arows, lw["q_norm"].data_ptr(), lw["k_norm"].data_ptr(),
+                     run.lens.data_ptr(), run.k_cache[ai].data_ptr(), run.vt_cache[ai].data_ptr(),
+                     self.q.data_ptr(), run.overflow.data_ptr(), 1, P, Hq, Hkv, D, run.Smax,
+                     cfg.rot_dims, float(cfg.rope_theta), eps, stream)
+                call("dflash_attn_prefill", self.q.data_ptr(), run.k_cache[ai].data_ptr(),
+                     run.vt_cache[ai].data_ptr(), run.lens.data_ptr(), ap, arows,
+                     self.attn_out.data_ptr(), P, Hq, Hkv, D, run.Smax, float(D ** -0.5), stream)
+                wt, n = tw["w_o"]
+                call("dflash_gemm_bf16_tiled_prefill", self.attn_out.data_ptr(), Hq * D,
+                     wt.data_ptr(), r, H, P, n, Hq * D, stream)
+                ai += 1
+            call("dflash_add_rmsnorm", h, r, lw["ln_post"].data_ptr(), h, xn, P, H, eps, stream)
+            wt, n = tw["w_gu_pairs"]
+            call("dflash_gemm_bf16_swiglu_tiled_prefill", xn, H, wt.data_ptr(),
+                 self.mlp_act.data_ptr(), I, P, n, H, stream)
+            wt, n = tw["w_down"]
+            call("dflash_gemm_bf16_tiled_prefill", self.mlp_act.data_ptr(), I, wt.data_ptr(), r, H,
+                 P, n, I, stream)
+            nw = layers[i + 1]["ln_in"] if i + 1 < L else run.w.final_norm
+            j = cap_ids.get(i)
+            if j is None:
+                call("dflash_add_rmsnorm", h, r, nw.data_ptr(), h, xn, P, H, eps, stream)
+            else:
+                call("dflash_add_rmsnorm_capture", h, r, None, 0, nw.data_ptr(), h,
+                     capture.data_ptr() + 2 * j * H, n_cap * H, xn, P, H, eps, stream)
+        # every layer's final state is in its tape's slab 0
+        run.keep.fill_(1)

@@ -14,10 +14,14 @@ LoadedTargetModel facade (adapters.py:341-570, :729-826).
   per gated-delta layer and a ``DeviceKVCache`` per attention layer, all views
   of the runner's device buffers.
 * ``forward_dflash(inputs, cache, layer_ids, return_rollback_records)`` runs
-  the inputs through the runner in pieces of at most ``block_size`` tokens
-  (prompts) or one piece (verify blocks) and leaves the caches as after
-  accepting every input, like the reference.  It returns the normed hidden
-  states, the target hidden states at ``layer_ids`` (the residual stream
+  a verify block (at most ``block_size`` tokens) through the runner, and a
+  longer input (a prompt) in one pass with launches sized to it
+  (``prefill.HybridPrefill``: prompt-sized MFMA projections, the chunked
+  gated-delta scan, causal prompt attention; ``prompt_pass="blocks"`` runs
+  it through the runner ``block_size`` tokens at a time instead), and
+  leaves the caches as after accepting every input, like the reference.
+  It returns the normed hidden states, the target hidden states at
+  ``layer_ids`` (the residual stream
   after each of those layers, concatenated in layer order on the feature
   axis) and, for one block, the rollback records: {initial_conv_state,
   initial_state, qkv, state_tape} per gated-delta layer.  Records, like the
@@ -43,6 +47,7 @@ from . import _lib
 from .adapters import make_rollback_record
 from .cache import ArraysCache, KVCache
 from .hybrid_model import HybridConfig, HybridVerifyRunner, HybridWeights
+from .prefill import HybridPrefill
 
 
 class DeviceKVCache(KVCache):
@@ -87,11 +92,20 @@ class HybridTargetModel:
 
     def __init__(self, cfg: HybridConfig, weights: HybridWeights, device: torch.device,
                  max_seq_len: int = 4096, block_size: int = 16, weight_layout: str = "tiled",
-                 eos_token_ids: set[int] | None = None):
+                 eos_token_ids: set[int] | None = None, prompt_pass: str = "prefill",
+                 prefill_rows: int = 8192):
+        """prompt_pass: "prefill" runs inputs longer than block_size in one
+        pass (prefill.HybridPrefill, up to prefill_rows rows per pass);
+        "blocks" runs them through the verify runner block_size tokens at a
+        time."""
+        if prompt_pass not in ("prefill", "blocks"):
+            raise ValueError(f"prompt_pass must be 'prefill' or 'blocks', got {prompt_pass!r}")
         self.cfg, self.weights, self.device = cfg, weights, torch.device(device)
         self.block_size = int(block_size)
         self.max_seq_len = int(max_seq_len)
         self.weight_layout = weight_layout
+        self.prompt_pass = prompt_pass
+        self.prefill_rows = int(prefill_rows)
         self.eos_token_ids = set(eos_token_ids or ())
         self._smax = -(-(self.max_seq_len + self.block_size) // 64) * 64
 
@@ -185,6 +199,8 @@ class HybridTargetModel:
         off = self._sync_in(cache, P)
         run.set_capture(layer_ids)
         H = self.cfg.hidden_size
+        if P > run.T and self.prompt_pass == "prefill":
+            return self._forward_prompt(cache, run, toks[0], off)
         norm_parts, hid_parts = [], []
         pos = 0
         while pos < P:
@@ -222,6 +238,27 @@ class HybridTargetModel:
         cache._records = records
         cache._block = P
         return norm_hidden, target_hidden, records
+
+    def _forward_prompt(self, cache: HybridCache, run: HybridVerifyRunner, toks: torch.Tensor,
+                        off: int):
+        """forward_dflash of a prompt in one pass (prefill.HybridPrefill):
+        the caches end as after accepting every token (states in tape slab 0
+        with keep = 1, windows advanced, KV lengths += P)."""
+        pre = getattr(cache, "_prefill", None)
+        if pre is None:
+            pre = cache._prefill = HybridPrefill(run, max_rows=self.prefill_rows)
+        P, H = toks.numel(), self.cfg.hidden_size
+        run.lens.fill_(off)
+        norm = torch.empty(P, H, dtype=torch.bfloat16, device=self.device)
+        n_cap = len(run.capture_layers)
+        cap = torch.empty(P, n_cap * H, dtype=torch.bfloat16, device=self.device) if n_cap else None
+        pre.forward(toks, norm, cap)
+        for i in cache.attn_idx:
+            cache[i].offset = off + P
+        self._install(cache, [run.tape[gi][0, 0:1] for gi in range(len(cache.linear_idx))])
+        cache._records = None
+        target_hidden = cap.view(1, P, -1) if cap is not None else norm.new_empty((1, P, 0))
+        return norm.view(1, P, H), target_hidden
 
     def rollback_linear_caches(self, cache: HybridCache, rollback_records: dict[int, dict[str, Any]],
                                accepted_inputs: int) -> None:
@@ -264,7 +301,9 @@ class HybridTargetModel:
 
     def lm_head_logits(self, hidden: torch.Tensor) -> torch.Tensor:
         """lm_head(hidden) (custom_qwen35_model.py:1090-1097): bf16 logits
-        [..., V] from this package's verify-sized GEMM, 64 rows a launch."""
+        [..., V] from this package's GEMMs: the prompt-sized GEMM over the
+        fragment-tiled head for more than 64 rows, else the verify-sized
+        GEMM, 64 rows a launch."""
         H, V = self.cfg.hidden_size, self.cfg.vocab_size
         lead = hidden.shape[:-1]
         x = hidden.reshape(-1, H).to(torch.bfloat16)
@@ -273,6 +312,10 @@ class HybridTargetModel:
         out = torch.empty((x.shape[0], V), dtype=torch.bfloat16, device=self.device)
         w = self.weights
         stream = _lib.stream_handle(self.device)
+        if x.shape[0] > 64 and w.lm_head_tiled is not None:
+            _lib.call("dflash_gemm_bf16_tiled_prefill", x.data_ptr(), x.stride(0),
+                      w.lm_head_tiled.data_ptr(), out.data_ptr(), V, x.shape[0], V, H, stream)
+            return out.view(*lead, V)
         for m0 in range(0, x.shape[0], 64):
             m = min(64, x.shape[0] - m0)
             xp, op = x[m0:].data_ptr(), out[m0:].data_ptr()
