@@ -32,7 +32,8 @@ and c2 (B = 32 serving batch) under "configs", each with its own roofline and
 CPU baseline.  Prints one JSON line.
 
 python bench.py [--steps K] [--warmup W] [--config 0|1|2] [--cpu-seconds S]
-                [--no-configs] [--no-extras] [--only lm_head|layer|prefill|hybrid|gemm]
+                [--no-configs] [--no-extras]
+                [--only lm_head|layer|prefill|hybrid|gemm|prompt]
 """
 from __future__ import annotations
 
@@ -72,7 +73,7 @@ def parse_args():
                          "and c2 under 'configs')")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the measurements of the next-row kernels (fused LM head)")
-    ap.add_argument("--only", choices=("lm_head", "layer", "prefill", "hybrid", "gemm"),
+    ap.add_argument("--only", choices=("lm_head", "layer", "prefill", "hybrid", "gemm", "prompt"),
                     default=None,
                     help="measure one next-row kernel alone and print its JSON (for profiling)")
     ap.add_argument("--probe", action="store_true",
@@ -418,6 +419,176 @@ def measure_hybrid(torch, dev, steps=40):
         "note": "random-init bf16 weights ~N(0,0.02), synthetic caches; reference figure: "
                 "benchmarks/qwen35-results.md, 21.59 s verifier forward+logits over the "
                 "~381 verify steps of a 2048-token decode on an M4 Max (other hardware)",
+    }
+
+
+def measure_prompt(torch, dev, P=4096, reps=3):
+    """The drop-in's prompt pass at the config-c4 shape (the random-init
+    Qwen3.5-4B-shaped target, 32 layers) over a P-token prompt from empty
+    caches: HybridTargetModel.forward_dflash (the reference's prefill,
+    runtime.py:384-390) through prefill.HybridPrefill.  Timed with HIP events
+    around whole calls; then its parts alone on the same buffers (every
+    projection on the prompt-sized MFMA GEMM, the 24 chunked gated-delta
+    scans, the 8 prompt attentions), hipBLASLt on the same GEMM shapes
+    (torch F.linear, row-major weights) for context, the all-row bf16 logits
+    the reference's prefill also computes, and the same prompt through the
+    verify runner 16 tokens at a time."""
+    from dflash_mlx import _lib
+    from dflash_mlx.hybrid_model import HybridConfig, HybridWeights
+    from dflash_mlx.target import HybridTargetModel
+
+    cfg = HybridConfig()
+    lc = cfg.linear
+    w = HybridWeights.random(cfg, dev, seed=0, on_device=True)
+    toks = torch.randint(0, cfg.vocab_size, (1, P), generator=torch.Generator().manual_seed(3),
+                         dtype=torch.int32).to(dev)
+    layer_ids = [1, 15, 31]
+
+    def setup(mode):
+        model = HybridTargetModel(cfg, w, dev, max_seq_len=P + 64, block_size=16, prompt_pass=mode)
+        return model, model.make_cache()
+
+    def reset(model, cache):
+        run = cache.runner
+        for i in cache.attn_idx:
+            cache[i].offset = 0
+        run.keep.zero_()
+        for st in run.state:
+            st.zero_()
+        run.conv_all.zero_()
+        model._install(cache, run.state)
+
+    def ev_time(fn, n=1):
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    model, cache = setup("prefill")
+    reset(model, cache)
+    norm, _ = model.forward_dflash(toks, cache, layer_ids)  # buffers, tiled copies, first clocks
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        reset(model, cache)
+        times.append(ev_time(lambda: model.forward_dflash(toks, cache, layer_ids)))
+    prompt_ms = sorted(times)[len(times) // 2]
+
+    # the parts alone, on the prompt pass's own buffers and weights
+    pre, run = cache._prefill, cache.runner
+    stream = _lib.stream_handle(dev)
+    H, I = cfg.hidden_size, cfg.intermediate_size
+    Hv, Dv, Hk, Dk = lc.linear_num_value_heads, lc.linear_value_head_dim, \
+        lc.linear_num_key_heads, lc.linear_key_head_dim
+    Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    gemms = []  # (name, x, x_stride, weight, out, out_stride, N, K, swiglu)
+    for i in range(cfg.num_hidden_layers):
+        t = pre.w[i]
+        if cfg.is_linear(i):
+            gemms.append(("w_in", pre.xn, H, t["w_in"], pre.proj, pre.in_stride, H, False))
+            gemms.append(("w_out", pre.gnorm, Hv * Dv, t["w_out"], pre.r, H, Hv * Dv, False))
+        else:
+            gemms.append(("w_qkv", pre.xn, H, t["w_qkv"], pre.aproj, cfg.attn_proj_rows, H, False))
+            gemms.append(("w_o", pre.attn_out, Hq * D, t["w_o"], pre.r, H, Hq * D, False))
+        gemms.append(("w_gu", pre.xn, H, t["w_gu_pairs"], pre.mlp_act, I, H, True))
+        gemms.append(("w_down", pre.mlp_act, I, t["w_down"], pre.r, H, I, False))
+
+    def run_gemms():
+        for _, x, xs, (wt, n), out, os_, k, sw in gemms:
+            _lib.call("dflash_gemm_bf16_swiglu_tiled_prefill" if sw else
+                      "dflash_gemm_bf16_tiled_prefill", x.data_ptr(), xs, wt.data_ptr(),
+                      out.data_ptr(), os_, P, n, k, stream)
+
+    gemm_flops = sum(2 * P * n * k for _, _, _, (_, n), _, _, k, _ in gemms)
+    run_gemms()
+    gemm_ms = ev_time(run_gemms, 2)
+    C = lc.conv_dim
+    import ctypes
+    strides = (ctypes.c_int64 * 13)(P * C, C, Dk, P * C, C, Dk, P * C, C, Dv, P * Hv, Hv, P * Hv, Hv)
+    act = pre.act.data_ptr()
+
+    def run_chunked():
+        for gi in range(cfg.n_linear):
+            _lib.call("dflash_gdn_chunked_prefill", act, act + 2 * Hk * Dk, act + 4 * Hk * Dk,
+                      pre.g.data_ptr(), pre.beta.data_ptr(), run.state[gi].data_ptr(),
+                      pre.scan_out.data_ptr(), run.tape[gi][0].data_ptr(), 1, P, Hk, Hv, Dk, Dv,
+                      strides, pre.chunk_ws.data_ptr(), pre.chunk_ws.numel(), stream)
+
+    chunk_ms = ev_time(run_chunked, 2)
+    run.lens.zero_()
+
+    def run_attn():
+        for ai in range(cfg.n_attention):
+            _lib.call("dflash_attn_prefill", pre.q.data_ptr(), run.k_cache[ai].data_ptr(),
+                      run.vt_cache[ai].data_ptr(), run.lens.data_ptr(), pre.aproj.data_ptr(),
+                      cfg.attn_proj_rows, pre.attn_out.data_ptr(), P, Hq, Hkv, D, run.Smax,
+                      float(D ** -0.5), stream)
+
+    attn_ms = ev_time(run_attn, 2)
+    attn_flops = cfg.n_attention * Hq * 2 * 2 * D * (P * (P + 1) // 2)
+
+    # hipBLASLt on the same shapes (row-major weights), for context
+    xs_ = {}
+    lib_gemms = []
+    for i, lw in enumerate(w.layers):
+        names = (("w_in", H), ("w_out", Hv * Dv)) if cfg.is_linear(i) else (("w_qkv", H),
+                                                                          ("w_o", Hq * D))
+        for name, k in names + (("w_gu", H), ("w_down", I)):
+            if k not in xs_:
+                xs_[k] = torch.randn(P, k, device=dev).bfloat16()
+            lib_gemms.append((xs_[k], lw[name]))
+
+    def run_lib():
+        for x, wt in lib_gemms:
+            torch.nn.functional.linear(x, wt)
+
+    run_lib()
+    lib_ms = ev_time(run_lib, 2)
+    del xs_, lib_gemms
+    logits_ms = ev_time(lambda: model.lm_head_logits(norm), 2)
+    del model, cache, pre, run
+    torch.cuda.empty_cache()
+
+    print("[bench] prompt pass: the same prompt through the verify runner, 16 tokens a time",
+          file=sys.stderr, flush=True)
+    bmodel, bcache = setup("blocks")
+    reset(bmodel, bcache)
+    bmodel.forward_dflash(toks[:, :64], bcache, layer_ids)
+    reset(bmodel, bcache)
+    block_ms = ev_time(lambda: bmodel.forward_dflash(toks, bcache, layer_ids))
+    del bmodel, bcache
+    torch.cuda.empty_cache()
+    total_flops = gemm_flops + attn_flops
+    gemm_tflops = gemm_flops / (gemm_ms / 1e3) / 1e12
+    return {
+        "workload": "c4-hybrid-qwen35-4b-prompt",
+        "shape": {"layers": cfg.num_hidden_layers, "hidden": cfg.hidden_size,
+                  "intermediate": cfg.intermediate_size, "prompt_tokens": P, "B": 1},
+        "prompt_ms": round(prompt_ms, 3),
+        "prompt_tokens_per_s": round(P / (prompt_ms / 1e3), 1),
+        "breakdown_ms": {"projection_gemms": round(gemm_ms, 3),
+                         "chunked_gated_delta": round(chunk_ms, 3),
+                         "prompt_attention": round(attn_ms, 3),
+                         "other": round(prompt_ms - gemm_ms - chunk_ms - attn_ms, 3)},
+        "roofline": {"kernel": "prefill_gemm_kernel (dflash_gemm_bf16_tiled_prefill / _swiglu)",
+                     "bound": "mfma", "flops": gemm_flops,
+                     "achieved": round(gemm_tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
+                     "frac": round(gemm_tflops / 2500.0, 4)},
+        "pass_tflops": round(total_flops / (prompt_ms / 1e3) / 1e12, 1),
+        "hipblaslt_same_gemms_ms": round(lib_ms, 3),
+        "hipblaslt_tflops": round(gemm_flops / (lib_ms / 1e3) / 1e12, 1),
+        "attention_tflops": round(attn_flops / (attn_ms / 1e3) / 1e12, 1),
+        "all_row_logits_ms": round(logits_ms, 3),
+        "block_path_ms": round(block_ms, 3),
+        "speedup_vs_block_path": round(block_ms / prompt_ms, 2),
+        "mfma_counters": mfma_from_profiles("prompt_pass_c4-prompt-4k"),
+        "note": "random-init bf16 weights ~N(0,0.02); prompt_ms is forward_dflash from empty "
+                "caches (no logits); all_row_logits_ms is the [P, 151936] bf16 LM head the "
+                "reference's prefill also evaluates; hipBLASLt is context, not the product path",
     }
 
 
@@ -818,7 +989,7 @@ def main() -> int:
     if args.only is not None:
         dev = torch.device("cuda", 0)
         fn = {"lm_head": measure_lm_head, "layer": measure_layer, "prefill": measure_prefill,
-              "hybrid": measure_hybrid, "gemm": measure_gemm}
+              "hybrid": measure_hybrid, "gemm": measure_gemm, "prompt": measure_prompt}
         print(json.dumps({args.only: fn[args.only](torch, dev)}), flush=True)
         return 0
 
@@ -865,6 +1036,9 @@ def main() -> int:
         line["next_rows"]["chunked_prefill"] = measure_prefill(torch, dev)
         print("[bench] next rows: hybrid verify step (config c4)", file=sys.stderr, flush=True)
         line["next_rows"]["hybrid_verify_step"] = measure_hybrid(torch, dev)
+        print("[bench] next rows: prompt pass (config c4 shape, 4096 tokens)", file=sys.stderr,
+              flush=True)
+        line["next_rows"]["prompt_pass"] = measure_prompt(torch, dev)
     print(json.dumps(line), flush=True)
     return 0
 
