@@ -33,7 +33,7 @@ CPU baseline.  Prints one JSON line.
 
 python bench.py [--steps K] [--warmup W] [--config 0|1|2] [--cpu-seconds S]
                 [--no-configs] [--no-extras]
-                [--only lm_head|layer|prefill|hybrid|gemm|prompt]
+                [--only lm_head|layer|prefill|hybrid|gemm|prompt|decode]
 """
 from __future__ import annotations
 
@@ -73,7 +73,8 @@ def parse_args():
                          "and c2 under 'configs')")
     ap.add_argument("--no-extras", action="store_true",
                     help="skip the measurements of the next-row kernels (fused LM head)")
-    ap.add_argument("--only", choices=("lm_head", "layer", "prefill", "hybrid", "gemm", "prompt"),
+    ap.add_argument("--only", choices=("lm_head", "layer", "prefill", "hybrid", "gemm", "prompt",
+                                       "decode"),
                     default=None,
                     help="measure one next-row kernel alone and print its JSON (for profiling)")
     ap.add_argument("--probe", action="store_true",
@@ -592,6 +593,107 @@ def measure_prompt(torch, dev, P=4096, reps=3):
     }
 
 
+class _PlantedDrafter:
+    """The DFlash drafter interface (block_size, mask_token_id,
+    target_layer_ids, make_cache, __call__) proposing a known continuation
+    with one wrong token at block offset plan[k % len(plan)] of its k-th
+    block (None: none wrong), so a decode's acceptance lengths are fixed in
+    advance.  Its draft hidden rows are LM-head rows scaled by 8, whose
+    logits peak at the row's own token by a wide margin (w_i . w_i ~ 1 against
+    |w_i . w_j| ~ 0.02 at the c4 shape)."""
+
+    mask_token_id = 0
+    block_size = 16
+
+    def __init__(self, lm_head, continuation, prompt_len, plan, layer_ids):
+        self.lm_head, self.full, self.plan = lm_head, continuation, plan
+        self.target_layer_ids = layer_ids
+        self.prompt_len, self.start, self.calls = prompt_len, None, 0
+
+    def make_cache(self):
+        return []
+
+    def __call__(self, noise_embedding, target_hidden, cache=None):
+        import torch
+
+        rows = target_hidden.shape[1]
+        self.start = self.prompt_len if self.start is None else self.start + rows
+        wrong = self.plan[self.calls % len(self.plan)]
+        s = self.start
+        toks = [self.full[min(s + i, len(self.full) - 1)] for i in range(noise_embedding.shape[1])]
+        if wrong is not None:
+            toks[wrong] = (toks[wrong] + 1) % self.lm_head.shape[0]
+        self.calls += 1
+        return (self.lm_head[torch.tensor(toks, device=self.lm_head.device)] * 8)[None]
+
+
+def measure_decode(torch, dev, P=256, N=192):
+    """The drop-in decode step at the config-c4 shape: DFlashGenerator.
+    generate_from_tokens (runtime.py:360-589 -> LoadedTargetModel ->
+    HybridTargetModel) over a P-token prompt for N new tokens, with a drafter
+    that proposes the target's own greedy continuation with planted
+    mistakes (acceptance lengths known in advance), for the
+    parallel-replay and parallel-greedy-argmax verify modes.  Reports wall
+    time per verify step (host-synchronous, as the reference's loop) and the
+    runtime's own profile split."""
+    from dflash_mlx import DFlashGenerator, LoadedTargetModel, sample_tokens
+    from dflash_mlx.hybrid_model import HybridConfig, HybridWeights
+    from dflash_mlx.target import HybridTargetModel
+
+    cfg = HybridConfig()
+    w = HybridWeights.random(cfg, dev, seed=0, on_device=True)
+    layer_ids = [1, 8, 15, 22, 29]
+    model = HybridTargetModel(cfg, w, dev, max_seq_len=P + N + 64, block_size=16)
+    target = LoadedTargetModel(model=model)
+    prompt = torch.randint(0, cfg.vocab_size, (P,), generator=torch.Generator().manual_seed(5),
+                           dtype=torch.int32)
+    def greedy(fused):
+        """The target's greedy continuation through the same facade, one token
+        a forward: the first token from the prompt's bf16 logits (as the
+        decode loop takes it), the rest from the bf16 logits or, as the
+        parallel-greedy-argmax mode does, the fused LM-head argmax over fp32
+        logits (near ties in bf16 resolve differently)."""
+        cache = target.make_cache()
+        norm, _ = model.forward_dflash(prompt[None].to(dev), cache, layer_ids)
+        cont = prompt.tolist()
+        for j in range(N + 16):
+            if fused and j > 0:
+                tok = int(target.lm_head_argmax(norm[:, -1:])[0, 0])
+            else:
+                tok = int(sample_tokens(target.lm_head_logits(norm[:, -1:]), 0.0)[0, 0])
+            cont.append(tok)
+            norm, _ = model.forward_dflash(torch.tensor([[tok]], dtype=torch.int32, device=dev),
+                                           cache, layer_ids)
+        return cont
+
+    plan = [7, 5, 9, None, 6, 3, 11, 8]  # accepted inputs 7 5 9 16 6 3 11 8: mean 8.1
+    out = {}
+    for mode in ("parallel-replay", "parallel-greedy-argmax"):
+        cont = greedy(mode == "parallel-greedy-argmax")
+        for rep in range(2):  # the first run warms the graphs, buffers and clocks
+            drafter = _PlantedDrafter(w.lm_head, cont, P, plan, layer_ids)
+            gen = DFlashGenerator(target, drafter)
+            res = gen.generate_from_tokens(prompt, max_new_tokens=N, verify_mode=mode,
+                                           profile=True)
+        m = res.metrics
+        steps = len(m["acceptance_lengths"])
+        prof = {k: round(v * 1e3 / steps, 3) for k, v in m["profile"].items()
+                if k.endswith("_time_s")}
+        agree = res.generated_tokens == cont[P:P + len(res.generated_tokens)]
+        out[mode] = {"ms_per_verify_step": round(m["decode_time_s"] * 1e3 / steps, 3),
+                     "steps": steps, "avg_acceptance_length": round(m["avg_acceptance_length"], 2),
+                     "generation_tps": round(m["generation_tps"], 1),
+                     "prefill_ms": round(m["prefill_time_s"] * 1e3, 2),
+                     "ms_per_step_profile": prof, "tokens_equal_greedy": bool(agree)}
+    return {"workload": "c4-hybrid-qwen35-4b-decode", "prompt_tokens": P, "new_tokens": N,
+            "modes": out,
+            "note": "host-synchronous decode loop through DFlashGenerator -> LoadedTargetModel "
+                    "-> HybridTargetModel, one small device->host read per step as the "
+                    "reference's mx.eval; the drafter network itself is not timed (planted "
+                    "hidden rows); reference figure: ~57 ms a verify step on an M4 Max "
+                    "(benchmarks/qwen35-results.md:23, other hardware)"}
+
+
 def _graph_time_us(torch, fn, n=20):
     """Average replay time of a HIP graph capturing fn (µs)."""
     s = torch.cuda.Stream()
@@ -989,7 +1091,8 @@ def main() -> int:
     if args.only is not None:
         dev = torch.device("cuda", 0)
         fn = {"lm_head": measure_lm_head, "layer": measure_layer, "prefill": measure_prefill,
-              "hybrid": measure_hybrid, "gemm": measure_gemm, "prompt": measure_prompt}
+              "hybrid": measure_hybrid, "gemm": measure_gemm, "prompt": measure_prompt,
+              "decode": measure_decode}
         print(json.dumps({args.only: fn[args.only](torch, dev)}), flush=True)
         return 0
 
@@ -1039,6 +1142,9 @@ def main() -> int:
         print("[bench] next rows: prompt pass (config c4 shape, 4096 tokens)", file=sys.stderr,
               flush=True)
         line["next_rows"]["prompt_pass"] = measure_prompt(torch, dev)
+        print("[bench] next rows: decode through DFlashGenerator (config c4 shape)",
+              file=sys.stderr, flush=True)
+        line["next_rows"]["decode_step"] = measure_decode(torch, dev)
     print(json.dumps(line), flush=True)
     return 0
 
