@@ -152,6 +152,148 @@ __global__ __launch_bounds__(256) void gdn_prologue_kernel(const ProParams p) {
   }
 }
 
+// The same prologue for long inputs (a prompt pass): a workgroup covers a
+// tile of kPTile consecutive tokens of one sequence, and a wavefront owns a
+// unit's channels for the whole tile.  Its lanes load the tile's kPTile + K-1
+// stream rows of their channels once (every load issued before any use), so
+// the conv window slides in registers instead of every token re-reading its
+// K taps; the per-token arithmetic (tap order, silu, the head's butterfly sum
+// and scale) is the per-token kernel's, so the outputs are the same bits.
+// Units as there: 2*Hk q/k heads, value chunks of 256 channels, one unit for
+// g / beta of the tile's tokens, then 512-channel units of the new conv
+// window (written by the tiles that hold its rows).
+constexpr int kPTile = 16;
+// Inputs longer than this many tokens take the tiled kernel.
+constexpr int kPromptTokens = 32;
+
+// x[r] = stream row t0 + r of concat(conv_state, qkv) for r < kPTile + NT - 1
+// (rows past the input's last one are clamped to it and never used).
+template <int NC, int NT>
+__device__ __forceinline__ void load_tile_rows(const ProParams& p, int b, int t0, int c0,
+                                               float (&x)[kPTile + NT - 1][NC]) {
+  const int K1 = p.K - 1;
+#pragma unroll
+  for (int r = 0; r < kPTile + NT - 1; ++r) {
+    const int s = min(t0 + r, p.T + K1 - 1);
+    const uint16_t* src = s < K1 ? p.conv_state + ((int64_t)b * K1 + s) * p.C + c0
+                                 : p.qkv + b * p.qkv_sb + (int64_t)(s - K1) * p.qkv_st + c0;
+#pragma unroll
+    for (int i = 0; i < NC; ++i) x[r][i] = ldbf(src + i);
+  }
+}
+
+// silu(conv1d) of NC channels at tile token t from the tile's rows; taps in
+// the order of pro_conv_silu (the per-token kernel's).
+template <int NC, int NT>
+__device__ __forceinline__ void tile_conv_silu(const ProParams& p, int t,
+                                               const float (&x)[kPTile + NT - 1][NC],
+                                               const float (&w)[NC][NT], float* out) {
+#pragma unroll
+  for (int i = 0; i < NC; ++i) {
+    float xi[NT];
+#pragma unroll
+    for (int j = 0; j < NT; ++j) xi[j] = x[t + j][i];
+    out[i] = pro_conv_silu_n<NT>(w[i], xi, p.K);
+  }
+}
+
+template <int NC, int NT>
+__device__ __forceinline__ void load_taps(const ProParams& p, int c0, float (&w)[NC][NT]) {
+#pragma unroll
+  for (int i = 0; i < NC; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+      w[i][j] = (NT != kMaxConvTaps || j < p.K) ? ldbf(p.conv_w + (int64_t)(c0 + i) * p.K + j) : 0.f;
+}
+
+// NT: the tap count held in registers (K itself, or kMaxConvTaps for any K).
+template <int PER, int NT>
+__global__ __launch_bounds__(256) void gdn_prologue_tile_kernel(const ProParams p) {
+  const int tiles = (p.T + kPTile - 1) / kPTile;
+  const int b = blockIdx.x / tiles;
+  const int t0 = (blockIdx.x - b * tiles) * kPTile;
+  const int nt = min(kPTile, p.T - t0);
+  const int lane = threadIdx.x & 63;
+  const int unit = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int n_qk = 2 * p.Hk;
+  const int v0 = 2 * p.Hk * p.Dk;
+  const int n_v = (p.C - v0 + 255) / 256;
+  uint16_t* act = p.act + ((int64_t)b * p.T + t0) * p.C;
+
+  if (unit < n_qk) {
+    const int c0 = unit * p.Dk + lane * PER;
+    float x[kPTile + NT - 1][PER];
+    load_tile_rows<PER, NT>(p, b, t0, c0, x);
+    float w[PER][NT];
+    load_taps<PER, NT>(p, c0, w);
+    const float scale = unit < p.Hk ? p.q_scale : p.k_scale;
+#pragma unroll
+    for (int t = 0; t < kPTile; ++t) {
+      if (t >= nt) break;  // wave-uniform
+      float vals[PER];
+      tile_conv_silu<PER, NT>(p, t, x, w, vals);
+      float ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) ss = fmaf(vals[i], vals[i], ss);
+      ss = pro_wave_sum(ss);
+      const float r = pro_head_scale(ss, p.Dk, p.eps, scale);
+#pragma unroll
+      for (int i = 0; i < PER; ++i) act[(int64_t)t * p.C + c0 + i] = f32_to_bf16_rne(vals[i] * r);
+    }
+  } else if (unit < n_qk + n_v) {
+    const int c0 = v0 + (unit - n_qk) * 256 + lane * 4;
+    if (c0 + 4 <= p.C) {
+      float x[kPTile + NT - 1][4];
+      load_tile_rows<4, NT>(p, b, t0, c0, x);
+      float w[4][NT];
+      load_taps<4, NT>(p, c0, w);
+#pragma unroll
+      for (int t = 0; t < kPTile; ++t) {
+        if (t >= nt) break;
+        float vals[4];
+        tile_conv_silu<4, NT>(p, t, x, w, vals);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) act[(int64_t)t * p.C + c0 + i] = f32_to_bf16_rne(vals[i]);
+      }
+    } else {
+      for (int t = 0; t < nt; ++t)
+        for (int c = c0; c < p.C; ++c) {
+          float v1[1];
+          conv_silu<1>(p, b, t0 + t, c, v1);
+          act[(int64_t)t * p.C + c] = f32_to_bf16_rne(v1[0]);
+        }
+    }
+  } else if (unit == n_qk + n_v) {
+    for (int e = lane; e < nt * p.Hv; e += 64) {
+      const int t = t0 + e / p.Hv, h = e % p.Hv;
+      const float av = ldbf(p.a + b * p.a_sb + (int64_t)t * p.a_st + h);
+      const float bv = ldbf(p.b + b * p.b_sb + (int64_t)t * p.b_st + h);
+      const int64_t bt = (int64_t)b * p.T + t;
+      p.g[bt * p.Hv + h] = pro_decay(p.A_log[h], av, ldbf(p.dt_bias + h));
+      p.beta[bt * p.Hv + h] = pro_sigmoid(bv);
+    }
+  } else {
+    // New conv window row r is stream row T + r, i.e. qkv[T - K1 + r] (the
+    // tile path runs only when T >= K - 1): the tile holding that token
+    // copies it.
+    const int c0 = (unit - n_qk - n_v - 1) * 512 + lane * 8;
+    const int K1 = p.K - 1;
+    for (int r = 0; r < K1; ++r) {
+      const int t = p.T - K1 + r;
+      if (t < t0 || t >= t0 + nt) continue;
+      uint16_t* dst = p.new_conv_state + ((int64_t)b * K1 + r) * p.C;
+      const uint16_t* src = p.qkv + b * p.qkv_sb + (int64_t)t * p.qkv_st;
+      uint16_t tmp[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (c0 + i < p.C) tmp[i] = src[c0 + i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        if (c0 + i < p.C) dst[c0 + i] = tmp[i];
+    }
+  }
+}
+
 struct NormParams {
   const uint16_t* x;  // [rows, D] bf16 contiguous (scan out [B,T,Hv,Dv])
   const uint16_t* z;  // gate, [B, T, Hv, D] with strides
@@ -252,8 +394,17 @@ extern "C" int dflash_gdn_prologue(const void* qkv, int64_t qkv_batch_stride,
   p.k_scale = 1.0f / sqrtf((float)Dk);
   p.q_scale = p.k_scale * p.k_scale;
   const int64_t units = 2LL * Hk + ceil_div(C - 2LL * Hk * Dk, 256) + 1 + ceil_div(C, 512);
-  const dim3 grid(B * T, (unsigned)ceil_div(units, 4));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (T > kPromptTokens && Dk == 128) {
+    // a prompt: token tiles, each stream row read once (same bits)
+    const dim3 tgrid((unsigned)(B * ceil_div(T, kPTile)), (unsigned)ceil_div(units, 4));
+    if (K == 4)
+      hipLaunchKernelGGL((gdn_prologue_tile_kernel<2, 4>), tgrid, dim3(256), 0, s, p);
+    else
+      hipLaunchKernelGGL((gdn_prologue_tile_kernel<2, kMaxConvTaps>), tgrid, dim3(256), 0, s, p);
+    return to_status(hipGetLastError());
+  }
+  const dim3 grid(B * T, (unsigned)ceil_div(units, 4));
   switch (Dk / 64) {
     case 1: hipLaunchKernelGGL(gdn_prologue_kernel<1>, grid, dim3(256), 0, s, p); break;
     case 2: hipLaunchKernelGGL(gdn_prologue_kernel<2>, grid, dim3(256), 0, s, p); break;

@@ -237,3 +237,37 @@ def test_fused_prologue_scan_rejects_unsupported(device):
         run(GatedDeltaConfig(**small), 33)
     with pytest.raises(_lib.DFlashError):                               # qkv not 4-byte aligned
         run(GatedDeltaConfig(**small), 4, offset=1)
+
+
+@pytest.mark.parametrize("cfg,B,T", [
+    (GatedDeltaConfig(), 1, 300),                                       # K = 4: the 4-tap tile kernel
+    (GatedDeltaConfig(linear_num_key_heads=2, linear_num_value_heads=4,
+                      linear_conv_kernel_dim=6), 2, 77),               # any other K
+], ids=["qwen35-4b-T300", "K6-B2-T77"])
+def test_prompt_prologue_tiles(oracle, device, cfg, B, T):
+    """Inputs longer than 32 tokens take the tiled prologue (token tiles, each
+    stream row read once): against the oracle, and bit for bit against the
+    same tokens fed as consecutive calls of at most 32 tokens (the per-token
+    kernel), each starting from the window the previous one left."""
+    x, w = _inputs(cfg, B, T, seed=T)
+    print(f"[prompt prologue {cfg} B={B} T={T}]", flush=True)
+    wd = _w_dev(w, device)
+    d = {k: v.to(device) for k, v in x.items()}
+    q, k, v, g, beta, new_conv = gdn_prologue(d["qkv"], d["conv_state"], d["a"], d["b"], wd, cfg)
+    torch.cuda.synchronize()
+    rq, rk, rv, rg, rb, rst = _oracle_prologue(oracle, x, w, cfg)
+    for name, got, ref in (("q", q, rq), ("k", k, rk), ("v", v, rv)):
+        assert _rel_max(got.float().cpu().numpy(), ref) <= 1e-2, name
+    assert _rel_max(g.cpu().numpy(), rg) <= 1e-5
+    np.testing.assert_array_equal(new_conv.float().cpu().numpy(), rst)
+    parts, conv = [], d["conv_state"]
+    for t0 in range(0, T, 32):
+        t1 = min(T, t0 + 32)
+        part = gdn_prologue(d["qkv"][:, t0:t1].contiguous(), conv, d["a"][:, t0:t1].contiguous(),
+                            d["b"][:, t0:t1].contiguous(), wd, cfg)
+        parts.append(part)
+        conv = part[5]
+    torch.cuda.synchronize()
+    for i, whole in enumerate((q, k, v, g, beta)):
+        assert torch.equal(whole, torch.cat([p[i] for p in parts], dim=1)), i
+    assert torch.equal(new_conv, conv)
