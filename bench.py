@@ -486,23 +486,29 @@ def measure_prompt(torch, dev, P=4096, reps=3):
     Hv, Dv, Hk, Dk = lc.linear_num_value_heads, lc.linear_value_head_dim, \
         lc.linear_num_key_heads, lc.linear_key_head_dim
     Hq, Hkv, D = cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
-    gemms = []  # (name, x, x_stride, weight, out, out_stride, N, K, swiglu)
+    gemms = []  # (name, x, x_stride, weight, out, out_stride, N, K, kind)
     for i in range(cfg.num_hidden_layers):
         t = pre.w[i]
         if cfg.is_linear(i):
-            gemms.append(("w_in", pre.xn, H, t["w_in"], pre.proj, pre.in_stride, H, False))
-            gemms.append(("w_out", pre.gnorm, Hv * Dv, t["w_out"], pre.r, H, Hv * Dv, False))
+            gemms.append(("w_in", pre.xn, H, t["w_in"], pre.proj, pre.in_stride, H, "plain"))
+            gemms.append(("w_out", pre.gnorm, Hv * Dv, t["w_out"], None, H, Hv * Dv, "residual"))
         else:
-            gemms.append(("w_qkv", pre.xn, H, t["w_qkv"], pre.aproj, cfg.attn_proj_rows, H, False))
-            gemms.append(("w_o", pre.attn_out, Hq * D, t["w_o"], pre.r, H, Hq * D, False))
-        gemms.append(("w_gu", pre.xn, H, t["w_gu_pairs"], pre.mlp_act, I, H, True))
-        gemms.append(("w_down", pre.mlp_act, I, t["w_down"], pre.r, H, I, False))
+            gemms.append(("w_qkv", pre.xn, H, t["w_qkv"], pre.aproj, cfg.attn_proj_rows, H,
+                          "plain"))
+            gemms.append(("w_o", pre.attn_out, Hq * D, t["w_o"], None, H, Hq * D, "residual"))
+        gemms.append(("w_gu", pre.xn, H, t["w_gu_pairs"], pre.mlp_act, I, H, "swiglu"))
+        gemms.append(("w_down", pre.mlp_act, I, t["w_down"], None, H, I, "residual"))
 
     def run_gemms():
-        for _, x, xs, (wt, n), out, os_, k, sw in gemms:
-            _lib.call("dflash_gemm_bf16_swiglu_tiled_prefill" if sw else
-                      "dflash_gemm_bf16_tiled_prefill", x.data_ptr(), xs, wt.data_ptr(),
-                      out.data_ptr(), os_, P, n, k, stream)
+        # as the prompt pass runs them (projections into the residual stream
+        # split-K where their tiles would underfill the device)
+        for _, x, xs, (wt, n), out, os_, k, kind in gemms:
+            if kind == "residual":
+                pre._to_residual((wt, n), x.data_ptr(), k, P, stream)
+            else:
+                _lib.call("dflash_gemm_bf16_swiglu_tiled_prefill" if kind == "swiglu" else
+                          "dflash_gemm_bf16_tiled_prefill", x.data_ptr(), xs, wt.data_ptr(),
+                          out.data_ptr(), os_, P, n, k, stream)
 
     gemm_flops = sum(2 * P * n * k for _, _, _, (_, n), _, _, k, _ in gemms)
     run_gemms()

@@ -24,7 +24,10 @@ each attention layer appends P keys and attends causally (:487-540).
   (``dflash_attn_prefill``);
 * residual adds and norms (``dflash_embed_rmsnorm``, ``dflash_add_rmsnorm``,
   ``dflash_add_rmsnorm_capture`` for the target hidden states at the
-  runner's capture layers).
+  runner's capture layers); a projection into the residual stream whose
+  output tiles would leave most compute units idle in the last round runs
+  split-K (``dflash_gemm_bf16_tiled_prefill_splitk``) and the add + norm
+  sums its fp32 partials (``dflash_add_rmsnorm_splitk``).
 
 Before the pass the recurrent states the runner would roll back on its next
 load (tape[keep - 1] when keep >= 1) are gathered into its state buffers
@@ -44,6 +47,26 @@ from . import _lib
 from .gdn_layer import QK_NORM_EPS
 
 
+MAX_SPLITS = 4
+
+
+def residual_splits(N: int, P: int, cus: int) -> int:
+    """K splits for a prompt-sized projection of N output columns over P rows
+    (256 x 128 output tiles): 1 when the tiles fill at least two rounds of
+    the device's compute units, else the count up to MAX_SPLITS that fills
+    the last round best (the smallest such)."""
+    tiles = -(-N // 256) * -(-P // 128)
+    if tiles >= 2 * cus:
+        return 1
+    best, fill = 1, 0.0
+    for s in range(1, MAX_SPLITS + 1):
+        units = tiles * s
+        f = units / (-(-units // cus) * cus)
+        if f > fill + 1e-9:
+            best, fill = s, f
+    return best
+
+
 class HybridPrefill:
     """Prompt pass over the caches of ``runner`` (B = 1)."""
 
@@ -58,6 +81,7 @@ class HybridPrefill:
         self.max_rows = int(max_rows)
         self.rows_cap = 0
         self._lib = _lib.load()
+        self.cus = torch.cuda.get_device_properties(runner.device).multi_processor_count
         self._weights()
 
     # ------------------------------------------------------------ weights
@@ -120,6 +144,7 @@ class HybridPrefill:
         ws = int(self._lib.dflash_gdn_chunked_prefill_workspace_bytes(
             1, P, Hv, lc.linear_key_head_dim, Dv))
         self.chunk_ws = e(max(ws, 16), dt=torch.uint8)
+        self.part = e(MAX_SPLITS * P * H, dt=f32)
         self.rows_cap = P
 
     # ------------------------------------------------------------ the pass
@@ -174,7 +199,7 @@ class HybridPrefill:
         eps = float(cfg.rms_norm_eps)
         call = _lib.call
         L = cfg.num_hidden_layers
-        h, xn, r = self.h.data_ptr(), self.xn.data_ptr(), self.r.data_ptr()
+        h, xn = self.h.data_ptr(), self.xn.data_ptr()
         self.tokens[:P].copy_(tokens)
         layers = run.w.layers
         call("dflash_embed_rmsnorm", run.w.embed.data_ptr(), self.tokens.data_ptr(), cfg.vocab_size,
@@ -208,9 +233,7 @@ class HybridPrefill:
                      scan_strides, self.chunk_ws.data_ptr(), self.chunk_ws.numel(), stream)
                 call("dflash_gdn_gated_rmsnorm", self.scan_out.data_ptr(), base + 2 * C, zs,
                      gw.norm_weight.data_ptr(), self.gnorm.data_ptr(), 1, P, Hv, Dv, eps, stream)
-                wt, n = tw["w_out"]
-                call("dflash_gemm_bf16_tiled_prefill", self.gnorm.data_ptr(), Hv * Dv, wt.data_ptr(),
-                     r, H, P, n, Hv * Dv, stream)
+                branch = self._to_residual(tw["w_out"], self.gnorm.data_ptr(), Hv * Dv, P, stream)
                 gi += 1
             else:
                 wt, n = tw["w_qkv"]
@@ -224,23 +247,45 @@ class HybridPrefill:
                 call("dflash_attn_prefill", self.q.data_ptr(), run.k_cache[ai].data_ptr(),
                      run.vt_cache[ai].data_ptr(), run.lens.data_ptr(), ap, arows,
                      self.attn_out.data_ptr(), P, Hq, Hkv, D, run.Smax, float(D ** -0.5), stream)
-                wt, n = tw["w_o"]
-                call("dflash_gemm_bf16_tiled_prefill", self.attn_out.data_ptr(), Hq * D,
-                     wt.data_ptr(), r, H, P, n, Hq * D, stream)
+                branch = self._to_residual(tw["w_o"], self.attn_out.data_ptr(), Hq * D, P, stream)
                 ai += 1
-            call("dflash_add_rmsnorm", h, r, lw["ln_post"].data_ptr(), h, xn, P, H, eps, stream)
+            self._add_norm(branch, lw["ln_post"], None, P, stream)
             wt, n = tw["w_gu_pairs"]
             call("dflash_gemm_bf16_swiglu_tiled_prefill", xn, H, wt.data_ptr(),
                  self.mlp_act.data_ptr(), I, P, n, H, stream)
-            wt, n = tw["w_down"]
-            call("dflash_gemm_bf16_tiled_prefill", self.mlp_act.data_ptr(), I, wt.data_ptr(), r, H,
-                 P, n, I, stream)
+            branch = self._to_residual(tw["w_down"], self.mlp_act.data_ptr(), I, P, stream)
             nw = layers[i + 1]["ln_in"] if i + 1 < L else run.w.final_norm
             j = cap_ids.get(i)
-            if j is None:
-                call("dflash_add_rmsnorm", h, r, nw.data_ptr(), h, xn, P, H, eps, stream)
-            else:
-                call("dflash_add_rmsnorm_capture", h, r, None, 0, nw.data_ptr(), h,
-                     capture.data_ptr() + 2 * j * H, n_cap * H, xn, P, H, eps, stream)
+            cap = None if j is None else (capture.data_ptr() + 2 * j * H, n_cap * H)
+            self._add_norm(branch, nw, cap, P, stream)
         # every layer's final state is in its tape's slab 0
         run.keep.fill_(1)
+
+    def _to_residual(self, weight, x_ptr, K, P, stream):
+        """A projection whose output the residual stream adds: bf16 into r,
+        or split-K fp32 partials into part; returns the split count (0: r)."""
+        wt, n = weight
+        ns = residual_splits(n, P, self.cus)
+        if ns == 1:
+            _lib.call("dflash_gemm_bf16_tiled_prefill", x_ptr, K, wt.data_ptr(), self.r.data_ptr(),
+                      self.cfg.hidden_size, P, n, K, stream)
+            return 0
+        _lib.call("dflash_gemm_bf16_tiled_prefill_splitk", x_ptr, K, wt.data_ptr(),
+                  self.part.data_ptr(), ns, P, n, K, stream)
+        return int(self._lib.dflash_gemm_splits(K, ns))
+
+    def _add_norm(self, splits, weight, capture, P, stream):
+        """h += the branch (r, or the sum of `splits` fp32 partials), xn =
+        RMSNorm(h) * weight; capture = (pointer, row stride) also receives h."""
+        H, eps = self.cfg.hidden_size, float(self.cfg.rms_norm_eps)
+        h, xn = self.h.data_ptr(), self.xn.data_ptr()
+        r = None if splits else self.r.data_ptr()
+        part = self.part.data_ptr() if splits else None
+        if capture is not None:
+            _lib.call("dflash_add_rmsnorm_capture", h, r, part, splits, weight.data_ptr(), h,
+                      capture[0], capture[1], xn, P, H, eps, stream)
+        elif splits:
+            _lib.call("dflash_add_rmsnorm_splitk", h, part, splits, weight.data_ptr(), h, xn, P, H,
+                      eps, stream)
+        else:
+            _lib.call("dflash_add_rmsnorm", h, r, weight.data_ptr(), h, xn, P, H, eps, stream)

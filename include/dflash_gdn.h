@@ -713,6 +713,17 @@ int dflash_gemm_bf16_swiglu_tiled_prefill(const void* x, int64_t x_row_stride,
                                           const void* w_pairs_tiled, void* out,
                                           int64_t out_row_stride, int M, int N,
                                           int K, void* stream);
+/*
+ * dflash_gemm_bf16_tiled_prefill with the k-range split nsplit ways (for
+ * output shapes with too few tiles to fill the device): fp32 partial sums
+ * [dflash_gemm_splits(K, nsplit), M, N] (16-byte aligned) for
+ * dflash_add_rmsnorm_splitk / dflash_splitk_reduce, which add them in split
+ * order.
+ */
+int dflash_gemm_bf16_tiled_prefill_splitk(const void* x, int64_t x_row_stride,
+                                          const void* w_tiled, float* partials,
+                                          int nsplit, int M, int N, int K,
+                                          void* stream);
 
 /*
  * out[m, n] = bf16(sum_s partials[s, m, n]) for partials fp32 [nsplit, M, N]

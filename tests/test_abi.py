@@ -50,6 +50,7 @@ def test_header_declares_expected_entry_points():
         "dflash_gemm_bf16_tiled_residual_norm",
         "dflash_gemm_bf16_tiled_normed", "dflash_gemm_bf16_swiglu_tiled_normed",
         "dflash_gemm_bf16_tiled_prefill", "dflash_gemm_bf16_swiglu_tiled_prefill",
+        "dflash_gemm_bf16_tiled_prefill_splitk",
         "dflash_attn_prefill",
     ])
 
@@ -267,6 +268,10 @@ def test_prefill_gemm_validation(lib):
     assert f(ctypes.c_void_p(0x1008), 2560, d, d, 2560, 100, 2560, 2560, None) == -4
     assert f(d, 2564, d, d, 2560, 100, 2560, 2560, None) == -4     # x stride % 8
     assert f(d, 2560, d, ctypes.c_void_p(0x1004), 2560, 100, 2560, 2560, None) == -4
+    h = lib.dflash_gemm_bf16_tiled_prefill_splitk
+    assert h(d, 2560, d, d, 0, 100, 2560, 2560, None) == -2       # nsplit < 1
+    assert h(d, 2560, d, None, 3, 100, 2560, 2560, None) == -1
+    assert h(d, 2560, d, ctypes.c_void_p(0x1008), 3, 100, 2560, 2560, None) == -4
     g = lib.dflash_gemm_bf16_swiglu_tiled_prefill
     assert g(d, 2560, d, d, 9216, 100, 18448, 2560, None) == -2   # N % 32
     assert g(d, 2560, d, d, 9000, 100, 18432, 2560, None) == -2   # out rows shorter than N/2
