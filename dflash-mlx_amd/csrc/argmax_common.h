@@ -109,7 +109,7 @@ __device__ __forceinline__ void argmax_partial_block(
     uint64_t m = wbest[0];
 #pragma unroll
     for (int w = 1; w < kArgmaxThreads / 64; ++w) m = u64_max(m, wbest[w]);
-    if (agent_store)
+    if (agent_store)  // read by a last arriver: the protocol of device_common.h
       __hip_atomic_store(keys + (int64_t)row * splits + split, m, __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
     else

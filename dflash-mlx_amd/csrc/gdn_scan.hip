@@ -354,6 +354,10 @@ __device__ __forceinline__ void accept_finish(const ScanParams& p, int row) {
   __shared__ int32_t post[kFinMaxRows];
   const int N = p.acc_N;
   const int b = row / N;
+  // The last-arriver protocol of device_common.h: relaxed agent-scope
+  // atomics ordered by the hardware (store acknowledged before the count,
+  // loads issued after the count returns), not by happens-before edges of
+  // the HIP memory model.
   if (threadIdx.x == 0) {
     __builtin_amdgcn_s_waitcnt(0);  // this workgroup's key store has completed
     const int old = __hip_atomic_fetch_add(p.fin_count + b, 1, __ATOMIC_RELAXED,

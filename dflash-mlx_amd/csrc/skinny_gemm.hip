@@ -371,9 +371,10 @@ __global__ __launch_bounds__(KW >= 8 ? 64 * KW : kGThreads) void skinny_gemm_ker
   }
 
   if (KW == 4 && tail) {
-    // Cross-workgroup merge.  The quarters travel as agent-scope atomic
-    // stores and loads (write-through to, and read from, the point where
-    // every XCD's L2 sees the same data); the wave waits for its stores to
+    // Cross-workgroup merge by the last arriver (the protocol and the
+    // hardware ordering it relies on, which relaxed atomics do not give in
+    // the HIP memory model: device_common.h).  The quarters travel as
+    // agent-scope atomic stores and loads; the wave waits for its stores to
     // complete before it counts itself, and the last arriver issues its
     // loads only once its count has returned.  No wave waits on another.
     constexpr int kUnit = VT * MT * 4 * 64;  // floats per quarter

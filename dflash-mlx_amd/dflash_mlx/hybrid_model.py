@@ -684,8 +684,3 @@ class HybridVerifyRunner:
         for st, tp in zip(self.state, self.tape):
             out.append(torch.stack([tp[k - 1, b] if k >= 1 else st[b] for b, k in enumerate(keep)]))
         return out
-
-    def logits(self):
-        """The LM-head logits of the last full-block forward (a plain GEMM;
-        for tests)."""
-        return torch.nn.functional.linear(self.xn, self.w.lm_head).float().view(self.B, self.T, -1)

@@ -290,3 +290,13 @@ def test_attn_prefill_validation(lib):
     assert f(d, ctypes.c_void_p(0x1008), d, d, d, 5120, d, 16, 16, 4, 128, 4096, 0.09,
              None) == -4
     assert f(None, None, None, None, None, 5120, None, 0, 16, 4, 128, 4096, 0.09, None) == 0
+
+
+def test_noalloc_refuses_shapes_beyond_its_array_before_any_device_call(lib):
+    """dflash_greedy_accept_noalloc refuses key arrays beyond its 1 MiB static
+    array from the shapes alone, before touching a device (no GPU here)."""
+    d = ctypes.c_void_p(0x1000)
+    assert lib.dflash_greedy_accept_noalloc_max_bytes() == 1 << 20
+    B, N, V = 8193, 16, 4096  # 131088 rows -> 1 MiB + 128 B of keys
+    assert lib.dflash_greedy_accept_noalloc(d, 0, N * V, V, None, 0, 0, d, None, None, B, N, V,
+                                            None) == -5

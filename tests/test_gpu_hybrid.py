@@ -36,6 +36,13 @@ def _np(x):
     return x.float().cpu().numpy().astype(np.float64)
 
 
+def _logits(run):
+    """The LM-head logits of the runner's last full-block forward in fp32
+    torch (the check's reference; the runner itself only runs the fused
+    LM-head greedy accept)."""
+    return (run.xn.float() @ run.w.lm_head.float().t()).view(run.B, run.T, -1)
+
+
 def _np_weights(w: HybridWeights):
     layers = []
     for lw in w.layers:
@@ -96,7 +103,7 @@ def test_small_hybrid_step_matches_oracle(device):
     ref = ho.model_step(cfg, _np_weights(w), o_state, tokens.numpy(), cfg.rms_norm_eps)
     hid = _np(run.xn).reshape(B, T, -1)
     hid_err = np.max(np.abs(hid - ref["hidden"])) / np.max(np.abs(ref["hidden"]))
-    logits = _np(run.logits())
+    logits = _np(_logits(run))
     log_err = np.max(np.abs(logits - ref["logits"])) / np.max(np.abs(ref["logits"]))
     tape_err = np.max(np.abs(_np(run.tape[0]) - ref["tape"][0])) / np.max(np.abs(ref["tape"][0]))
     print(f"  hidden rel {hid_err:.2e}  logits rel {log_err:.2e}  tape[0] rel {tape_err:.2e}",
@@ -160,7 +167,7 @@ def test_fused_norms_agree_with_norm_launches(device):
         run.forward_accept()
         torch.cuda.synchronize()
         outs.append(dict(xn=run.xn.clone(), tape=run.tape[0].clone(), post=run.posterior.clone(),
-                         logits=run.logits(), cap=run.captured.clone()))
+                         logits=_logits(run), cap=run.captured.clone()))
     f, u = outs
     assert torch.equal(f["tape"], u["tape"])
     scale = u["xn"].float().abs().max().item()
@@ -371,7 +378,7 @@ def test_c4_width_layers_match_oracle(device, fused_norms):
         assert terr <= 2e-2
     hid = _np(run.xn).reshape(B, T, H)
     herr = np.max(np.abs(hid - ref["hidden"])) / np.max(np.abs(ref["hidden"]))
-    logits = _np(run.logits())
+    logits = _np(_logits(run))
     lerr = np.max(np.abs(logits - ref["logits"])) / np.max(np.abs(ref["logits"]))
     print(f"  final hidden rel {herr:.2e}  logits rel {lerr:.2e}", flush=True)
     assert herr <= 3e-2 and lerr <= 3e-2
@@ -384,7 +391,12 @@ def test_c4_width_layers_match_oracle(device, fused_norms):
     assert int(run.bonus.cpu()[0]) == post[0, m]
     print(f"  posterior equal to the oracle's on {int(clear.sum())} clear-margin rows of {T}",
           flush=True)
-    assert clear.sum() >= 4
+    # `clear` depends only on the oracle's fp64 logits of these seeded inputs,
+    # not on any GPU output: 6 of the 16 rows have a top-1 margin above 2 % of
+    # the logits' scale (at vocab 151 936 random-init logits crowd near the
+    # top).  Those rows are compared exactly; the floor guards against a
+    # change of inputs that would leave the exact check with nothing to check.
+    assert clear.sum() >= 6
     # on the other rows the GPU's token is a near tie of the oracle's top one
     scale = np.max(np.abs(ref["logits"]))
     chosen = np.take_along_axis(ref["logits"], post[..., None].astype(np.int64), -1)[..., 0]

@@ -109,10 +109,20 @@ def test_noalloc_in_a_graph_replays_like_eager(device):
 
 
 def test_noalloc_refuses_shapes_beyond_its_array(device):
+    """The size refusal on the device.  The buffers are real and as large as
+    the shape says (2.1 GB of logits), so if the check ever stopped
+    refusing, the call would compute into them rather than read past an
+    allocation."""
     lib = _lib.load()
     assert int(lib.dflash_greedy_accept_noalloc_max_bytes()) == 1 << 20
     B, N, V = 8193, 16, 4096  # 131088 rows -> 1 MiB + 128 B of keys
     assert int(lib.dflash_greedy_accept_workspace_bytes(B, N, V)) > 1 << 20
-    rc = lib.dflash_greedy_accept_noalloc(0x1000, _lib.DFLASH_DTYPE_F32, N * V, V, None, 0, 0,
-                                          0x1000, None, None, B, N, V, None)
+    logits = torch.zeros(B * N * V, dtype=torch.float32, device=device)
+    post = torch.full((B * N,), -7, dtype=torch.int32, device=device)
+    rc = lib.dflash_greedy_accept_noalloc(logits.data_ptr(), _lib.DFLASH_DTYPE_F32, N * V, V, None,
+                                          0, 0, post.data_ptr(), None, None, B, N, V,
+                                          _lib.stream_handle(device))
+    torch.cuda.synchronize()
     assert rc == -5
+    assert bool((post == -7).all())  # refused before any launch
+    del logits
