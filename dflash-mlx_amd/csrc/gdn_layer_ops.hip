@@ -177,8 +177,36 @@ __device__ __forceinline__ void load_tile_rows(const ProParams& p, int b, int t0
     const int s = min(t0 + r, p.T + K1 - 1);
     const uint16_t* src = s < K1 ? p.conv_state + ((int64_t)b * K1 + s) * p.C + c0
                                  : p.qkv + b * p.qkv_sb + (int64_t)(s - K1) * p.qkv_st + c0;
+    if constexpr (NC == 2) {  // one 4-byte load (c0 even; rows 4-byte aligned)
+      const uint32_t w = *reinterpret_cast<const uint32_t*>(src);
+      x[r][0] = bf16_lo(w);
+      x[r][1] = bf16_hi(w);
+    } else if constexpr (NC == 4) {  // one 8-byte load (c0 % 4 == 0; rows 8-byte aligned)
+      const uint2 w = *reinterpret_cast<const uint2*>(src);
+      x[r][0] = bf16_lo(w.x);
+      x[r][1] = bf16_hi(w.x);
+      x[r][2] = bf16_lo(w.y);
+      x[r][3] = bf16_hi(w.y);
+    } else {
 #pragma unroll
-    for (int i = 0; i < NC; ++i) x[r][i] = ldbf(src + i);
+      for (int i = 0; i < NC; ++i) x[r][i] = ldbf(src + i);
+    }
+  }
+}
+
+// NC consecutive bf16 outputs of one token in one store.
+template <int NC>
+__device__ __forceinline__ void store_run(uint16_t* dst, const float* v) {
+  if constexpr (NC == 2) {
+    *reinterpret_cast<uint32_t*>(dst) =
+        (uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16);
+  } else if constexpr (NC == 4) {
+    *reinterpret_cast<uint2*>(dst) =
+        uint2{(uint32_t)f32_to_bf16_rne(v[0]) | ((uint32_t)f32_to_bf16_rne(v[1]) << 16),
+              (uint32_t)f32_to_bf16_rne(v[2]) | ((uint32_t)f32_to_bf16_rne(v[3]) << 16)};
+  } else {
+#pragma unroll
+    for (int i = 0; i < NC; ++i) dst[i] = f32_to_bf16_rne(v[i]);
   }
 }
 
@@ -237,8 +265,10 @@ __global__ __launch_bounds__(256) void gdn_prologue_tile_kernel(const ProParams 
       for (int i = 0; i < PER; ++i) ss = fmaf(vals[i], vals[i], ss);
       ss = pro_wave_sum(ss);
       const float r = pro_head_scale(ss, p.Dk, p.eps, scale);
+      float o[PER];
 #pragma unroll
-      for (int i = 0; i < PER; ++i) act[(int64_t)t * p.C + c0 + i] = f32_to_bf16_rne(vals[i] * r);
+      for (int i = 0; i < PER; ++i) o[i] = vals[i] * r;
+      store_run<PER>(act + (int64_t)t * p.C + c0, o);
     }
   } else if (unit < n_qk + n_v) {
     const int c0 = v0 + (unit - n_qk) * 256 + lane * 4;
@@ -252,8 +282,7 @@ __global__ __launch_bounds__(256) void gdn_prologue_tile_kernel(const ProParams 
         if (t >= nt) break;
         float vals[4];
         tile_conv_silu<4, NT>(p, t, x, w, vals);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) act[(int64_t)t * p.C + c0 + i] = f32_to_bf16_rne(vals[i]);
+        store_run<4>(act + (int64_t)t * p.C + c0, vals);
       }
     } else {
       for (int t = 0; t < nt; ++t)
@@ -395,7 +424,12 @@ extern "C" int dflash_gdn_prologue(const void* qkv, int64_t qkv_batch_stride,
   p.q_scale = p.k_scale * p.k_scale;
   const int64_t units = 2LL * Hk + ceil_div(C - 2LL * Hk * Dk, 256) + 1 + ceil_div(C, 512);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (T > kPromptTokens && Dk == 128) {
+  // the tiled kernel's 4- and 8-byte row accesses: qkv, the conv window and
+  // act 8-byte aligned, row and batch strides and C multiples of 4 elements
+  const bool vec_ok =
+      !(((uintptr_t)qkv | (uintptr_t)conv_state | (uintptr_t)act) & 7) &&
+      qkv_row_stride % 4 == 0 && qkv_batch_stride % 4 == 0 && C % 4 == 0;
+  if (T > kPromptTokens && Dk == 128 && vec_ok) {
     // a prompt: token tiles, each stream row read once (same bits)
     const dim3 tgrid((unsigned)(B * ceil_div(T, kPTile)), (unsigned)ceil_div(units, 4));
     if (K == 4)
