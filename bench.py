@@ -127,6 +127,15 @@ def traffic_from_profiles(workload: str):
     return int(m.group(1)) if m else None
 
 
+def counter_from_profile(fname: str, key: str):
+    """An integer `key: value` line of a committed profiles/ summary."""
+    path = ROOT / "profiles" / fname
+    if not path.exists():
+        return None
+    m = re.search(rf"^{key}:\s*([0-9]+)", path.read_text(), re.M)
+    return int(m.group(1)) if m else None
+
+
 def mfma_from_profiles(name: str):
     """Counter-measured MFMA busy fraction and executed TFLOP/s per kernel from
     a committed rocprofv3 --pmc summary (profiles/<name>_mfma_pmc.md)."""
@@ -288,8 +297,11 @@ def measure_prefill(torch, dev, n=50):
         "mfma_counters": mfma_from_profiles("chunked_prefill_c3-prefill-8k"),
         "hbm_bytes_alg": hbm,
         "hbm_frac": round(hbm / (chunked_us / 1e6) / 1e9 / PEAK_HBM_GBPS, 4),
+        "traffic": counter_from_profile("chunked_prefill_c3-prefill-8k_traffic_pmc.md",
+                                        "traffic_bytes_per_call"),
         "note": "per call incl. Python dispatch, 50 calls after 20 untimed; two kernels "
-                "(chunk prep, chunk state)",
+                "(chunk prep, chunk state); traffic: HBM bytes per call from FETCH_SIZE / "
+                "WRITE_SIZE counters (the prep kernel's operand fragments round-trip through HBM)",
     }
 
 
