@@ -255,9 +255,12 @@ __global__ __launch_bounds__(256) void gdn_prologue_tile_kernel(const ProParams 
     float w[PER][NT];
     load_taps<PER, NT>(p, c0, w);
     const float scale = unit < p.Hk ? p.q_scale : p.k_scale;
+    // Every token of the tile is computed (the rows past the input are
+    // clamped copies) and only the stores are guarded: a loop that stops at
+    // the run-time tile length would not unroll, and the row array would be
+    // indexed at run time, out of registers.
 #pragma unroll
     for (int t = 0; t < kPTile; ++t) {
-      if (t >= nt) break;  // wave-uniform
       float vals[PER];
       tile_conv_silu<PER, NT>(p, t, x, w, vals);
       float ss = 0.f;
@@ -268,7 +271,7 @@ __global__ __launch_bounds__(256) void gdn_prologue_tile_kernel(const ProParams 
       float o[PER];
 #pragma unroll
       for (int i = 0; i < PER; ++i) o[i] = vals[i] * r;
-      store_run<PER>(act + (int64_t)t * p.C + c0, o);
+      if (t < nt) store_run<PER>(act + (int64_t)t * p.C + c0, o);
     }
   } else if (unit < n_qk + n_v) {
     const int c0 = v0 + (unit - n_qk) * 256 + lane * 4;
@@ -279,10 +282,9 @@ __global__ __launch_bounds__(256) void gdn_prologue_tile_kernel(const ProParams 
       load_taps<4, NT>(p, c0, w);
 #pragma unroll
       for (int t = 0; t < kPTile; ++t) {
-        if (t >= nt) break;
         float vals[4];
         tile_conv_silu<4, NT>(p, t, x, w, vals);
-        store_run<4>(act + (int64_t)t * p.C + c0, vals);
+        if (t < nt) store_run<4>(act + (int64_t)t * p.C + c0, vals);
       }
     } else {
       for (int t = 0; t < nt; ++t)
