@@ -593,7 +593,7 @@ def measure_prompt(torch, dev, P=4096, reps=3):
                          "chunked_gated_delta": round(chunk_ms, 3),
                          "prompt_attention": round(attn_ms, 3),
                          "other": round(prompt_ms - gemm_ms - chunk_ms - attn_ms, 3)},
-        "roofline": {"kernel": "prefill_gemm_kernel (dflash_gemm_bf16_tiled_prefill / _swiglu)",
+        "roofline": {"kernel": "prefill_gemm_wide_kernel (dflash_gemm_bf16_tiled_prefill / _swiglu / _splitk; 256 x 256 tiles)",
                      "bound": "mfma", "flops": gemm_flops,
                      "achieved": round(gemm_tflops, 1), "peak": 2500.0, "unit": "TFLOP/s",
                      "frac": round(gemm_tflops / 2500.0, 4)},

@@ -13,7 +13,14 @@
 //
 // The weight is the verify GEMMs' fragment-tiled copy (dflash_weight_tile_bf16,
 // made once at load time: [K/64 k-steps][N/16 row tiles][2 halves][64 lanes]
-// [8]), so both GEMM families share one copy and its k-slot order:
+// [8]), so both GEMM families share one copy and its k-slot order.
+//
+// Two workgroup tiles, chosen per launch: 256 weight rows x 256 activation
+// rows (8 waves, both operands staged in LDS by direct loads; the wide tile
+// below) whenever its work units give every compute unit one, else the
+// 256 x 128 tile described here (twice the units, for short prompts).  Both
+// add each output's products in the same order, so the choice never
+// changes a bit.  The 256 x 128 tile:
 //   - A workgroup (4 waves) computes 256 weight rows x 128 activation rows.
 //     Wave w owns weight rows 64w .. 64w+63 (4 row tiles) against all 128
 //     activation rows (8 column tiles): 32 accumulator tiles of
@@ -275,6 +282,236 @@ __global__ __launch_bounds__(256, 1) void prefill_gemm_kernel(const PrefillGemmP
   }
 }
 
+// ---------------------------------------------------------------------------
+// Wide tile: 256 weight rows x 256 activation rows per workgroup of 8 waves,
+// both operands staged in LDS by direct global -> LDS loads.
+//
+// Wave w (wr = w / 2, wc = w % 2) owns weight row tiles 4 wr .. 4 wr + 3
+// against activation column tiles 8 wc .. 8 wc + 7: 32 accumulator tiles,
+// 32 MFMAs per half k-step (32 k); two waves share each SIMD.  A stage is one
+// half k-step of both operands in fragment order, 32 KB: the 16 weight
+// fragments (1 KB each, straight from the tiled layout) and the 16
+// activation fragments (lane (r16, g) of fragment (c, h) holds
+// x[16c + r16][64 ks + 16 g + 8 h .. +7], the k-slots of the weight
+// fragment, gathered by each lane's own 16-byte load).  A direct load puts
+// lane l's 16 bytes at LDS base + 16 l, so one wave-wide load fills one
+// fragment and every fragment read is 64 consecutive 16-byte pieces (no
+// bank conflicts, no swizzle).  Waves 0-3 load the weight fragments, waves
+// 4-7 the activation fragments, four loads each per stage.  Three stages
+// (96 KB) rotate: stage i + 2 is loaded while stage i is multiplied; one
+// barrier per half k-step.  Per k-step the workgroup moves 64 KB for
+// 2 * 256 * 256 * 64 flops, half the bytes per flop of the 256 x 128 tile.
+//
+// Measured at the c4 projections (4096 prompt rows; TFLOP/s, this tile /
+// the 256 x 128 tile / hipBLASLt on the same box): in_proj 897 / 679 / 909,
+// q|k|v 790 / 682 / 1109, gate|up (SwiGLU) 1159 / 821 / 1047, out_proj
+// split 3 999 / 691 / 1192, o_proj 793 / 568 / 960, down 1194 / 829 / 1333;
+// the six shapes 1061 us against 1443 us and hipBLASLt's 1013 us, and the
+// sums bit for bit the 256 x 128 tile's.  Tried: 4 waves of 128 x 128 (256
+// accumulator registers a lane: the compiler shuffles them between register
+// files every step), 2 / 4 / 5 stages (1296 / 1075 / 1097 us), bands of 4 /
+// 8 / 16 weight tiles (within 2 %), fragments read a half k-step ahead into
+// a second register set (no gain), whole k-step stages with 8-row
+// activation loads (full 128-byte lines, swizzled rows; 1055 us).  Timing
+// copies with parts removed (wrong sums): no fragment reads 871 us, no
+// MFMAs 842 us, neither 846 us, neither and no activation loads 467 us,
+// neither and no weight loads 681 us: the stage loads, above all the
+// activation gather (16 rows of half lines per load), bound the kernel, and
+// a probe of the same direct loads from a resident 1 MB buffer streams
+// 55 bytes a clock per compute unit, so it is the L2 / fabric side of that
+// gather, not the load instruction.
+constexpr int kWRows = 256;      // weight rows per workgroup
+constexpr int kWCols = 256;      // activation rows per workgroup
+constexpr int kWStages = 3;      // half k-step stages in LDS
+constexpr int kWStageU4 = 2048;  // u32x4 per stage (32 KB)
+constexpr int kWGroup = 16;      // weight tiles per band of the tile walk
+
+// The 32-bit LDS address of a workgroup-shared object.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// One direct global -> LDS load of 16 bytes a lane: lane l reads
+// sbase + voff (its own byte offset) and its 16 bytes land at LDS address
+// lds + 16 l.  Written as an instruction of its own so that the compiler
+// does not see a pending LDS write and hold every later LDS read behind all
+// of the loads in flight: the waits for these loads are explicit (wait_vm).
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(lds) : "memory");
+}
+
+// Wait until at most N loads of this wave are outstanding (loads complete
+// in issue order).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Stage hs (k-step hs / 2, half hs % 2) into the LDS stage at byte address
+// `st` (weight fragments at +0, activation fragments at +16 KB).  Waves 0-3
+// load weight fragments 4w .. 4w + 3 (row tiles past the weight's last are
+// clamped to it; their sums are never stored), waves 4-7 activation
+// fragments 4(w - 4) .. +3.  off[i]: the lane's byte offset for its i-th
+// load (weight: 16 bytes a lane in lane order; activation: row 16 c + r16,
+// clamped to the last row, k-slot 16 g).  wave, rt0 and m0 are
+// wave-uniform.
+__device__ __forceinline__ void wide_load_stage(const PrefillGemmParams& p, int hs, int rt0,
+                                                int m0, int wave, const uint32_t (&off)[4],
+                                                uint32_t st) {
+  const int ks = hs >> 1, h = hs & 1;
+  if (wave < 4) {
+    const int NT = p.N >> 4;
+    const char* wb = reinterpret_cast<const char*>(p.w) + (int64_t)ks * NT * 2048 + h * 1024;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int f = 4 * wave + i;
+      dma16(wb + (int64_t)min(rt0 + f, NT - 1) * 2048, off[i], st + f * 1024);
+    }
+  } else {
+    const char* xb =
+        reinterpret_cast<const char*>(p.x) + (int64_t)m0 * p.xs * 2 + ks * 128 + h * 16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(xb, off[i], st + 16384 + (4 * (wave - 4) + i) * 1024);
+  }
+}
+
+// One half k-step of the wave's 4 x 8 accumulator tiles from the stage at
+// `st`: weight fragments 4 wr .. 4 wr + 3, activation fragments
+// 8 wc .. 8 wc + 7.
+__device__ __forceinline__ void wide_mma(const u32x4* st, int wr, int wc, int lane,
+                                         f32x4 (&acc)[4][8]) {
+  u32x4 a[4], b[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = st[(4 * wr + i) * 64 + lane];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) b[j] = st[1024 + (8 * wc + j) * 64 + lane];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[i]), as_bf16x8(b[j]),
+                                                          acc[i][j], 0, 0, 0);
+}
+
+template <bool SWIGLU>
+__global__ __launch_bounds__(512, 1) void prefill_gemm_wide_kernel(const PrefillGemmParams p) {
+  __shared__ __attribute__((aligned(16))) u32x4 stages[kWStages * kWStageU4];
+  const int u = (int)(blockIdx.x & 7) * p.per_xcd + (int)(blockIdx.x >> 3);
+  if (u >= p.total) return;
+  // work unit u = split * tiles + t: k-range `split` of output tile t
+  const int split = u / p.tiles;
+  const int t = u - split * p.tiles;
+  const int band_tiles = kWGroup * p.m_tiles;
+  const int band = t / band_tiles;
+  const int in_band = t - band * band_tiles;
+  const int gsz = min(kWGroup, p.n_tiles - band * kWGroup);
+  const int mt = in_band / gsz;
+  const int nt = band * kWGroup + (in_band - mt * gsz);
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int wr = wave >> 1, wc = wave & 1;
+  const int rt0 = (nt * kWRows) >> 4;  // the workgroup's first weight row tile
+  const int m0 = mt * kWCols;
+  const int hb = 2 * split * p.ks_per_split;  // the unit's first half k-step
+  const int nhs = 2 * min(p.ks_per_split, (p.K >> 6) - split * p.ks_per_split);
+
+  f32x4 acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  uint32_t off[4];
+  {
+    const int r16 = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = min(m0 + 16 * (4 * (wave & 3) + i) + r16, p.M - 1);
+      off[i] = wave < 4 ? (uint32_t)(lane * 16)
+                        : (uint32_t)((int64_t)(m - m0) * p.xs * 2) + 32 * g;
+    }
+  }
+  const uint32_t l0 = lds_addr(stages);
+
+  // nhs >= 2 (K >= 64).  Stages 0 and 1 before the loop.
+  wide_load_stage(p, hb, rt0, m0, wave, off, l0);
+  wide_load_stage(p, hb + 1, rt0, m0, wave, off, l0 + 32768);
+
+  // A wave whose weight row tiles all lie past the weight's last (in the last
+  // weight tile of a launch whose N is not a multiple of 256) loads its share
+  // of every stage and keeps the barriers, but multiplies nothing: its sums
+  // would never be stored.
+  const bool live = rt0 + 4 * wr < (p.N >> 4);
+
+  // Half k-step i multiplies stage slot i % 3.  Before it, this wave's loads
+  // of stage i must be done (those of stage i + 1, four, may still be in
+  // flight) and every wave's: the barrier, which also frees slot
+  // (i + 2) % 3 = (i - 1) % 3 for stage i + 2.  The barrier is the bare
+  // instruction: its waits are explicit (the stage loads by count, the
+  // fragment reads by the MFMAs that consumed them), where a workgroup
+  // fence would also wait for the loads of the later stage.
+  auto pipeline = [&](auto MMA) {
+    int slot = 0, fill = 2;  // slots of stage i and of stage i + 2
+    for (int i = 0; i < nhs; ++i) {
+      if (i + 1 < nhs) wait_vm<4>();
+      else wait_vm<0>();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (i + 2 < nhs) wide_load_stage(p, hb + i + 2, rt0, m0, wave, off, l0 + fill * 32768);
+      if (decltype(MMA)::value) wide_mma(stages + slot * kWStageU4, wr, wc, lane, acc);
+      slot = slot == 2 ? 0 : slot + 1;
+      fill = fill == 2 ? 0 : fill + 1;
+    }
+  };
+  if (live)
+    pipeline(std::true_type{});
+  else
+    pipeline(std::false_type{});
+
+  // Epilogue.  Lane (r16, g) of tile (i, j) holds out[m = m0 + 16 (8 wc + j)
+  // + r16][n = n0 + 16 i + 4 g .. +3], n0 the wave's first weight row.
+  const int n0 = nt * kWRows + wr * 64;
+  const int r16 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int m = m0 + 16 * (8 * wc + j) + r16;
+    if (m >= p.M) continue;
+    if (p.part != nullptr) {
+      float* prow = p.part + ((int64_t)split * p.M + m) * p.N;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = n0 + 16 * i;
+        if (n < p.N) *reinterpret_cast<f32x4*>(prow + n + 4 * g) = acc[i][j];
+      }
+      continue;
+    }
+    uint16_t* orow = p.out + (int64_t)m * p.os;
+    if (SWIGLU) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int n = n0 + 32 * q;  // gate rows n .. n+15, up rows n+16 .. n+31
+        if (n >= p.N) continue;
+        const f32x4 gt = acc[2 * q][j], up = acc[2 * q + 1][j];
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = gt[e] / (1.f + __expf(-gt[e])) * up[e];
+        *reinterpret_cast<u32x2*>(orow + (n >> 1) + 4 * g) = pack4(o[0], o[1], o[2], o[3]);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = n0 + 16 * i;
+        if (n >= p.N) continue;
+        const f32x4 v = acc[i][j];
+        *reinterpret_cast<u32x2*>(orow + n + 4 * g) = pack4(v[0], v[1], v[2], v[3]);
+      }
+    }
+  }
+}
+
 // nsplit == 0: bf16 out (SwiGLU with swiglu); nsplit >= 1: fp32 partial
 // sums of dflash_gemm_splits-style k-ranges into part [splits][M][N].
 int launch_prefill(const void* x, int64_t x_row_stride, const void* w_tiled, void* out,
@@ -291,6 +528,8 @@ int launch_prefill(const void* x, int64_t x_row_stride, const void* w_tiled, voi
     return DFLASH_ERR_ALIGN;
   if (nsplit == 0 ? (((uintptr_t)out & 7) || (out_row_stride % 4)) : ((uintptr_t)part & 15))
     return DFLASH_ERR_ALIGN;
+  // The wide tile's activation offsets are 32-bit: (256 rows - 1) * row stride.
+  if (x_row_stride > ((int64_t)1 << 22)) return DFLASH_ERR_SHAPE;
   PrefillGemmParams p{};
   p.x = static_cast<const uint16_t*>(x);
   p.xs = x_row_stride;
@@ -299,12 +538,17 @@ int launch_prefill(const void* x, int64_t x_row_stride, const void* w_tiled, voi
   p.os = out_row_stride;
   p.part = nsplit > 0 ? part : nullptr;
   p.M = M; p.N = N; p.K = K;
-  p.n_tiles = (int)ceil_div(N, kPRows);
-  p.m_tiles = (int)ceil_div(M, kPCols);
   const int nks = K / 64;
   const int want = nsplit > 0 ? std::min(nsplit, nks) : 1;
   p.ks_per_split = (int)ceil_div(nks, want);
   p.nsplit = (int)ceil_div(nks, p.ks_per_split);
+  // The 256 x 256 tile when its work units give every compute unit one, else
+  // the 256 x 128 tile (twice the units); both add each output's products in
+  // the same order, so the choice never changes a bit.
+  const int64_t wide_units = ceil_div(N, kWRows) * ceil_div(M, kWCols) * (int64_t)p.nsplit;
+  const bool wide = wide_units >= device_cus();
+  p.n_tiles = (int)ceil_div(N, wide ? kWRows : kPRows);
+  p.m_tiles = (int)ceil_div(M, wide ? kWCols : kPCols);
   const int64_t tiles = (int64_t)p.n_tiles * p.m_tiles;
   const int64_t total = tiles * p.nsplit;
   if (total > (int64_t)INT32_MAX / 2) return DFLASH_ERR_SHAPE;
@@ -313,10 +557,16 @@ int launch_prefill(const void* x, int64_t x_row_stride, const void* w_tiled, voi
   p.per_xcd = (int)ceil_div(total, 8);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid((unsigned)(8 * p.per_xcd));
-  if (swiglu)
+  if (wide) {
+    if (swiglu)
+      hipLaunchKernelGGL((prefill_gemm_wide_kernel<true>), grid, dim3(512), 0, s, p);
+    else
+      hipLaunchKernelGGL((prefill_gemm_wide_kernel<false>), grid, dim3(512), 0, s, p);
+  } else if (swiglu) {
     hipLaunchKernelGGL((prefill_gemm_kernel<true, kPDepth, kPSwizzle>), grid, dim3(256), 0, s, p);
-  else
+  } else {
     hipLaunchKernelGGL((prefill_gemm_kernel<false, kPDepth, kPSwizzle>), grid, dim3(256), 0, s, p);
+  }
   return to_status(hipGetLastError());
 }
 

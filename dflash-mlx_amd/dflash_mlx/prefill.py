@@ -51,19 +51,26 @@ MAX_SPLITS = 4
 
 
 def residual_splits(N: int, P: int, cus: int) -> int:
-    """K splits for a prompt-sized projection of N output columns over P rows
-    (256 x 128 output tiles): 1 when the tiles fill at least two rounds of
-    the device's compute units, else the count up to MAX_SPLITS that fills
-    the last round best (the smallest such)."""
-    tiles = -(-N // 256) * -(-P // 128)
-    if tiles >= 2 * cus:
+    """K splits for a prompt-sized projection of N output columns over P rows.
+
+    The GEMM runs 256 x 256 output tiles when their work units (tiles x
+    splits) give every compute unit one, else 256 x 128 tiles; a 256 x 128
+    unit costs about 0.7 of a 256 x 256 one (half the products at the
+    smaller tile's lower rate).  The count up to MAX_SPLITS with the least
+    time, rounds of units x cost per unit / splits, wins (the smallest on a
+    tie); 1 when the wide tiles alone fill two rounds."""
+    wide = -(-N // 256) * -(-P // 256)
+    narrow = -(-N // 256) * -(-P // 128)
+    if wide >= 2 * cus:
         return 1
-    best, fill = 1, 0.0
+    best, best_cost = 1, None
     for s in range(1, MAX_SPLITS + 1):
-        units = tiles * s
-        f = units / (-(-units // cus) * cus)
-        if f > fill + 1e-9:
-            best, fill = s, f
+        if wide * s >= cus:
+            cost = -(-(wide * s) // cus) / s
+        else:
+            cost = 0.7 * -(-(narrow * s) // cus) / s
+        if best_cost is None or cost < best_cost - 1e-9:
+            best, best_cost = s, cost
     return best
 
 

@@ -267,6 +267,7 @@ def test_prefill_gemm_validation(lib):
     assert f(None, 2560, d, d, 2560, 100, 2560, 2560, None) == -1
     assert f(ctypes.c_void_p(0x1008), 2560, d, d, 2560, 100, 2560, 2560, None) == -4
     assert f(d, 2564, d, d, 2560, 100, 2560, 2560, None) == -4     # x stride % 8
+    assert f(d, (1 << 22) + 8, d, d, 2560, 100, 2560, 2560, None) == -2  # x stride > 2^22
     assert f(d, 2560, d, ctypes.c_void_p(0x1004), 2560, 100, 2560, 2560, None) == -4
     h = lib.dflash_gemm_bf16_tiled_prefill_splitk
     assert h(d, 2560, d, d, 0, 100, 2560, 2560, None) == -2       # nsplit < 1

@@ -9,8 +9,12 @@ dflash_gemm_bf16_swiglu_tiled_prefill) over the fragment-tiled weights.
   fp32 chain per output over the k-steps in order, so at M <= 64 their sums
   are the same bits — a check that pins the k-slot order of the activation
   operand, which the fp32 bound would not catch at small K.
+* The two workgroup tiles (256 x 256 when its units fill the device, else
+  256 x 128) bit for bit against each other: a launch over M rows against
+  launches over 128-row slices of the same rows, which take the other tile.
 Shapes: every projection of the config-c4 layers at prompt lengths, M and N
-tails (M not a multiple of 128, N not a multiple of 256), K = 64.
+tails (M not a multiple of 128 or 256, N not a multiple of 256, down to a
+last weight tile of one 16-row tile), K = 64.
 """
 from __future__ import annotations
 
@@ -90,6 +94,28 @@ def test_prefill_gemm_matches_verify_gemm_bits(device, M, N, K):
               1, 16, 1, None, 0, _lib.stream_handle(device))
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("M,N,K,swiglu", [(4000, 4112, 192, False), (4096, 12352, 128, False),
+                                           (2900, 8224, 128, True), (4096, 5120, 256, False)])
+def test_prefill_gemm_wide_tile_matches_narrow_bits(device, M, N, K, swiglu):
+    """The 256 x 256 tile (chosen here: its units reach the device's compute
+    units) against the 256 x 128 tile (chosen for each 128-row slice alone):
+    each output row depends on its own activation row only, so the slices
+    must reproduce the whole launch bit for bit.  N = 4112 leaves one 16-row
+    tile in the last weight tile (three of its four weight-row waves hold no
+    rows), M = 4000 / 2900 a partial last activation tile."""
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    assert -(-N // 256) * -(-M // 256) >= cus and -(-N // 256) * 1 < cus
+    print(f"[prefill gemm] wide vs narrow tile M={M} N={N} K={K} swiglu={swiglu}", flush=True)
+    x, w = _inputs(device, M, N, K, seed=M + N + K)
+    wt = _tile(w, device)
+    whole = _prefill(device, x, wt, M, N, K, swiglu=swiglu)
+    parts = torch.cat([_prefill(device, x[r:r + 128], wt, min(128, M - r), N, K, swiglu=swiglu)
+                       for r in range(0, M, 128)])
+    assert torch.equal(whole, parts)
+    if not swiglu:
+        _check(whole, x.float() @ w.float().t())
 
 
 @pytest.mark.parametrize("M,I,K", [(300, 9216, 2560), (5, 16, 64), (129, 272, 192)])
