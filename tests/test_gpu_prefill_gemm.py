@@ -97,7 +97,8 @@ def test_prefill_gemm_matches_verify_gemm_bits(device, M, N, K):
 
 
 @pytest.mark.parametrize("M,N,K,swiglu", [(4000, 4112, 192, False), (4096, 12352, 128, False),
-                                           (2900, 8224, 128, True), (4096, 5120, 256, False)])
+                                           (2900, 8224, 128, True), (4096, 5120, 256, False),
+                                           (4096, 4096, 64, False)])
 def test_prefill_gemm_wide_tile_matches_narrow_bits(device, M, N, K, swiglu):
     """The 256 x 256 tile (chosen here: its units reach the device's compute
     units) against the 256 x 128 tile (chosen for each 128-row slice alone):
