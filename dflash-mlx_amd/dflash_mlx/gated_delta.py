@@ -136,9 +136,23 @@ def _(q, k, v, g, beta, state):
 
 def gated_delta_kernel(q, k, v, g, beta, state, mask=None):
     """Drop-in for mlx_lm's gated_delta_kernel: returns (out, final_state)
-    without a tape (the reference's forward, custom_qwen35_model.py:457-466)."""
+    without a tape (the reference's forward, custom_qwen35_model.py:457-466).
+
+    ``mask`` (bool or 0/1 [B, T], the reference's SSM mask of left-padded
+    batches, built by create_ssm_mask at custom_qwen35_model.py:968-969):
+    a masked token leaves the recurrent state unchanged and its output is
+    zero.  It runs as the same scan with g = 1 and beta = 0 at masked
+    tokens, which carries the state through bit for bit (S * 1 + k * 0)."""
     if mask is not None:
-        raise NotImplementedError("masked scans are not part of the verify path")
+        B, T = k.shape[0], k.shape[1]
+        m = torch.as_tensor(mask, device=k.device)
+        if m.dim() != 2 or tuple(m.shape) != (B, T):
+            raise ValueError(f"mask must be [B, T] = [{B}, {T}], got {tuple(m.shape)}")
+        m = m.to(torch.bool)
+        g = torch.where(m[..., None], g.to(torch.float32), 1.0)
+        beta = torch.where(m[..., None], beta.to(torch.float32), 0.0)
+        out, final, _ = _scan(q, k, v, g, beta, state, want_out=True, want_tape=False)
+        return out * m[..., None, None].to(out.dtype), final
     out, final, _ = _scan(q, k, v, g, beta, state, want_out=True, want_tape=False)
     return out, final
 

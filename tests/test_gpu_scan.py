@@ -204,3 +204,34 @@ def test_rejects_bad_inputs(device):
         gated_delta_verify(d["q"], d["k"], d["v"], d["g"], d["beta"], d["state"][..., :32])
     with pytest.raises(TypeError):
         gated_delta_verify(d["q"], d["k"], d["v"], d["g"], d["beta"], d["state"].bfloat16())
+
+
+def test_masked_scan_equals_the_compacted_sequences(device):
+    """gated_delta_kernel with the reference's SSM mask (left padding, and a
+    hole inside one sequence): a masked token leaves the state unchanged, so
+    each sequence's final state and its outputs at unmasked positions equal,
+    bit for bit, an unmasked scan of only its unmasked tokens; masked outputs
+    are zero.  Pad positions hold random, unrelated inputs."""
+    cfg = ScanConfig(name="masked", B=3, T=16, Hk=2, Hv=4, Dk=64, Dv=64, state_std=0.5)
+    x = make_scan_inputs(cfg, seed=5)
+    d = _to_dev(x, device)
+    mask = torch.ones(3, 16, dtype=torch.bool)
+    mask[0, 7:9] = False           # a hole
+    mask[1, :5] = False            # left padding
+    mask[2, :11] = False
+    out, fin = gated_delta_kernel(d["q"], d["k"], d["v"], d["g"], d["beta"], d["state"],
+                                  mask=mask.to(device))
+    torch.cuda.synchronize()
+    for b in range(3):
+        keep = mask[b].nonzero().flatten().to(device)
+        sel = {n: d[n][b:b + 1].index_select(1, keep).contiguous() for n in ("q", "k", "v", "g", "beta")}
+        o_ref, f_ref = gated_delta_kernel(sel["q"], sel["k"], sel["v"], sel["g"], sel["beta"],
+                                          d["state"][b:b + 1])
+        torch.cuda.synchronize()
+        assert torch.equal(fin[b:b + 1], f_ref), b
+        assert torch.equal(out[b:b + 1].index_select(1, keep), o_ref), b
+        drop = (~mask[b]).nonzero().flatten().to(device)
+        assert (out[b].index_select(0, drop) == 0).all(), b
+    with pytest.raises(ValueError):
+        gated_delta_kernel(d["q"], d["k"], d["v"], d["g"], d["beta"], d["state"],
+                           mask=mask[:, :8].to(device))
