@@ -336,6 +336,9 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // lds + 16 l.  Written as an instruction of its own so that the compiler
 // does not see a pending LDS write and hold every later LDS read behind all
 // of the loads in flight: the waits for these loads are explicit (wait_vm).
+// M0 (the LDS base of the load) is set inside the instruction pair; the
+// compiler treats M0 as reserved and does not use it in these kernels (the
+// generated code's only M0 writes are these), so nothing it holds is lost.
 __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1"
                :: "v"(voff), "s"(sbase), "s"(lds) : "memory");
