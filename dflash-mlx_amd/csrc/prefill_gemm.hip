@@ -315,11 +315,11 @@ __global__ __launch_bounds__(256, 1) void prefill_gemm_kernel(const PrefillGemmP
 // activation loads (full 128-byte lines, swizzled rows; 1055 us).  Timing
 // copies with parts removed (wrong sums): no fragment reads 871 us, no
 // MFMAs 842 us, neither 846 us, neither and no activation loads 467 us,
-// neither and no weight loads 681 us: the stage loads, above all the
-// activation gather (16 rows of half lines per load), bound the kernel, and
-// a probe of the same direct loads from a resident 1 MB buffer streams
-// 55 bytes a clock per compute unit, so it is the L2 / fabric side of that
-// gather, not the load instruction.
+// neither and no weight loads 681 us.  Yet the whole kernel reading a
+// fragment-tiled copy of the activations (contiguous 1 KB loads, same sums)
+// took 1131 us against 1140: the activation gather is not what bounds it;
+// the per-half-k-step rhythm (stage wait, barrier, fragment reads, 32 MFMAs
+// a wave at two waves a SIMD) is.
 constexpr int kWRows = 256;      // weight rows per workgroup
 constexpr int kWCols = 256;      // activation rows per workgroup
 constexpr int kWStages = 3;      // half k-step stages in LDS
