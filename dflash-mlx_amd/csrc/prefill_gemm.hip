@@ -208,38 +208,40 @@ __global__ __launch_bounds__(256, 1) void prefill_gemm_kernel(const PrefillGemmP
 #pragma unroll
     for (int c = 0; c < 8; ++c) acc[i][c] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  // Rings: slot s holds the operands of k-steps s, s + D, s + 2D, ...
+  // Rings: slot s holds the operands of k-steps s, s + D, s + 2D, ...  Every
+  // step issues the same loads, whatever nks is (k-steps past the unit's
+  // last re-read the last one; nothing multiplies them), so the compiler's
+  // count of loads in flight is exact at each wait.  Loads under a condition
+  // make it wait for all of them once per turn of the ring instead.
+  const int klast = kb + nks - 1;
   u32x4 a[D][8], bx[D][4];
 #pragma unroll
   for (int s = 0; s < D; ++s) {
-    if (s < nks) {
-      load_b(p, kb + s, m0, tid, bx[s]);
-      load_a(p, kb + s, rt0, lane, a[s]);
-    }
+    load_b(p, min(kb + s, klast), m0, tid, bx[s]);
+    load_a(p, min(kb + s, klast), rt0, lane, a[s]);
   }
   store_b<SWZ>(sx[0], tid, bx[0]);
-  if (D < nks) load_b(p, kb + D, m0, tid, bx[0]);
+  load_b(p, min(kb + D, klast), m0, tid, bx[0]);
   __syncthreads();
-  // k-step i = ks + s multiplies LDS buffer i % 2 with a[s]; then a[s] is
-  // refilled with step i + D, step i + 1's activations go from bx[(s+1) % D]
-  // to the other LDS buffer, and that slot is refilled with step i + 1 + D.
+  // k-step i = ks + s multiplies LDS buffer i % 2 with a[s] (when i < nks);
+  // then a[s] is refilled with step i + D, step i + 1's activations go from
+  // bx[(s+1) % D] to the other LDS buffer, and that slot is refilled with
+  // step i + 1 + D.
   auto step = [&](auto S, int ks) {
     constexpr int s = decltype(S)::value;
     constexpr int s1 = (s + 1) % D;
     const int i = ks + s;
-    mma_step<SWZ>(sx[i & 1], lane, a[s], acc);
-    if (i + D < nks) load_a(p, kb + i + D, rt0, lane, a[s]);
-    if (i + 1 < nks) {
-      store_b<SWZ>(sx[(i + 1) & 1], tid, bx[s1]);
-      if (i + 1 + D < nks) load_b(p, kb + i + 1 + D, m0, tid, bx[s1]);
-    }
+    if (s == 0 || i < nks) mma_step<SWZ>(sx[i & 1], lane, a[s], acc);
+    load_a(p, min(kb + i + D, klast), rt0, lane, a[s]);
+    store_b<SWZ>(sx[(i + 1) & 1], tid, bx[s1]);
+    load_b(p, min(kb + i + 1 + D, klast), m0, tid, bx[s1]);
     __syncthreads();
   };
   for (int ks = 0; ks < nks; ks += D) {
     step(Slot<0>{}, ks);
-    if (D > 1 && ks + 1 < nks) step(Slot<(D > 1 ? 1 : 0)>{}, ks);
-    if (D > 2 && ks + 2 < nks) step(Slot<(D > 2 ? 2 : 0)>{}, ks);
-    if (D > 3 && ks + 3 < nks) step(Slot<(D > 3 ? 3 : 0)>{}, ks);
+    if (D > 1) step(Slot<(D > 1 ? 1 : 0)>{}, ks);
+    if (D > 2) step(Slot<(D > 2 ? 2 : 0)>{}, ks);
+    if (D > 3) step(Slot<(D > 3 ? 3 : 0)>{}, ks);
   }
 
   // Epilogue.  Lane (r16, g) of tile (i, c) holds out[m = m0 + 16c + r16]

@@ -42,7 +42,8 @@ def _producer(device, x, wt, resid, M, N, K, cap_stride=None):
 
 
 @pytest.mark.parametrize("M,N,K", [(16, 2560, 4096), (16, 2560, 9216), (16, 2560, 2048),
-                                   (37, 2576, 1024), (64, 1040, 640), (1, 160, 128), (5, 96, 64)])
+                                   (37, 2576, 1024), (64, 1040, 640), (1, 160, 128), (5, 96, 64),
+                                   (16, 2560, 1024), (16, 2560, 5120), (16, 2560, 6144)])
 def test_residual_norm_producer(device, M, N, K):
     print(f"[fused norm producer] M={M} N={N} K={K}", flush=True)
     g = torch.Generator(device=device).manual_seed(M * 31 + N + K)

@@ -195,6 +195,29 @@ def test_gemm_tiled_64_rows_per_wave(device, M, N, K, nsplit, kw):
         assert ((out.float() - ref).abs() - (2 ** -8) * ref.abs()).max().item() <= 1e-3 * scale
 
 
+@pytest.mark.parametrize("M", [16, 37])
+@pytest.mark.parametrize("kw", [1, 4])
+@pytest.mark.parametrize("steps", [1, 2, 3, 4, 5, 6, 7])
+def test_gemm_tiled_every_ring_remainder(device, M, kw, steps):
+    """Each wave's k-range of 1 .. 7 k-steps: every remainder modulo the
+    load ring's depth (4 k-steps at M <= 32, 2 above), so the last turn of
+    the ring skips 0 .. 3 steps.  Against the fp32 reference."""
+    K = 64 * kw * steps
+    N = 272
+    print(f"[gemm tiled] ring remainder M={M} k_waves={kw} steps={steps}", flush=True)
+    g = torch.Generator(device=device).manual_seed(100 * M + 10 * kw + steps)
+    x = torch.randn(M, K, generator=g, device=device).bfloat16()
+    w = (0.02 * torch.randn(N, K, generator=g, device=device)).bfloat16()
+    t = _tile(device, w)
+    out = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=device)
+    _lib.call("dflash_gemm_bf16_tiled", x.data_ptr(), K, t.data_ptr(), out.data_ptr(), N, M, N, K,
+              1, 16, kw, None, 0, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    ref = _ref(x, w)
+    scale = ref.pow(2).mean().sqrt().item()
+    assert ((out.float() - ref).abs() - (2 ** -8) * ref.abs()).max().item() <= 1e-3 * scale
+
+
 @pytest.mark.parametrize("M,I,K,kw", [(16, 9216, 2560, 4), (37, 64, 128, 1)])
 def test_gemm_swiglu_tiled_bit_identical(device, M, I, K, kw):
     g = torch.Generator(device=device).manual_seed(I + M)

@@ -45,7 +45,8 @@ def _check_rows(post, logits):
 
 
 @pytest.mark.parametrize("M,H,V", [(1, 64, 1000), (16, 2560, 20011), (17, 512, 4096),
-                                   (33, 256, 3000), (64, 2560, 8192)])
+                                   (33, 256, 3000), (64, 2560, 8192), (16, 192, 2000),
+                                   (16, 320, 2000), (5, 448, 1000)])
 def test_lm_head_argmax_matches_fp64(device, M, H, V):
     hidden, weight = _inputs(M, H, V, seed=M * 7 + V)
     print(f"[lm_head M={M} H={H} V={V}]", flush=True)
@@ -109,7 +110,8 @@ def test_rejects_unsupported(device):
 
 
 @pytest.mark.parametrize("M,H,V", [(1, 64, 1008), (16, 2560, 20016), (17, 512, 4096),
-                                   (33, 256, 3008), (64, 2560, 8192)])
+                                   (33, 256, 3008), (64, 2560, 8192), (16, 192, 2000),
+                                   (16, 320, 2000), (5, 448, 1008), (16, 1216, 2000)])
 def test_tiled_head_matches_fp64(device, M, H, V):
     """The head over its fragment-tiled copy (tile_weight): same contract."""
     hidden, weight = _inputs(M, H, V, seed=M * 11 + V)
