@@ -512,15 +512,15 @@ def measure_prompt(torch, dev, P=4096, reps=3):
         gemms.append(("w_down", pre.mlp_act, I, t["w_down"], None, H, I, "residual"))
 
     def run_gemms():
-        # as the prompt pass runs them (projections into the residual stream
-        # split-K where their tiles would underfill the device)
+        # as the prompt pass runs them (split-K where their tiles would
+        # underfill the device: the residual projections' partials go to the
+        # add + norm, the bf16 ones' through their reduce)
         for _, x, xs, (wt, n), out, os_, k, kind in gemms:
             if kind == "residual":
                 pre._to_residual((wt, n), x.data_ptr(), k, P, stream)
             else:
-                _lib.call("dflash_gemm_bf16_swiglu_tiled_prefill" if kind == "swiglu" else
-                          "dflash_gemm_bf16_tiled_prefill", x.data_ptr(), xs, wt.data_ptr(),
-                          out.data_ptr(), os_, P, n, k, stream)
+                pre._bf16_proj((wt, n), x.data_ptr(), k, P, out.data_ptr(), os_,
+                               kind == "swiglu", stream)
 
     gemm_flops = sum(2 * P * n * k for _, _, _, (_, n), _, _, k, _ in gemms)
     run_gemms()

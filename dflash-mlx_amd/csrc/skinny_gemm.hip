@@ -494,6 +494,34 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* part, i
   }
 }
 
+// The gated form over partials in the w_pairs column order (32-column
+// blocks: 16 gate columns, then the 16 matching up columns): out[m][j] =
+// bf16(silu(g) * u) with g, u the split sums of column 32 (j / 16) + j % 16
+// and that column + 16.  Four outputs a thread.
+__global__ __launch_bounds__(256) void splitk_swiglu_reduce_kernel(const float* part, int nsplit,
+                                                                   int M, int N, uint16_t* out,
+                                                                   int64_t os) {
+  const int I = N / 2;
+  const int64_t nv = (int64_t)M * (I / 4);
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < nv; e += (int64_t)gridDim.x * 256) {
+    const int m = (int)(e / (I / 4));
+    const int j = (int)(e - (int64_t)m * (I / 4)) * 4;
+    const int gc = 32 * (j >> 4) + (j & 15);
+    f32x4 g = {0.f, 0.f, 0.f, 0.f}, u = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < nsplit; ++k) {
+      const float* row = part + ((int64_t)k * M + m) * N;
+      g += *reinterpret_cast<const f32x4*>(row + gc);
+      u += *reinterpret_cast<const f32x4*>(row + gc + 16);
+    }
+    float o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = g[i] / (1.f + __expf(-g[i])) * u[i];
+    *reinterpret_cast<u32x2*>(out + (int64_t)m * os + j) =
+        u32x2{(uint32_t)f32_to_bf16_rne(o[0]) | ((uint32_t)f32_to_bf16_rne(o[1]) << 16),
+              (uint32_t)f32_to_bf16_rne(o[2]) | ((uint32_t)f32_to_bf16_rne(o[3]) << 16)};
+  }
+}
+
 template <int MT, int VT, int KW, bool TILED, bool NRM = false>
 hipError_t launch_gemm(const GemmParams& p, hipStream_t s) {
   constexpr int D = MT == 1 ? 4 : (MT == 2 ? 4 : 2);
@@ -658,6 +686,22 @@ extern "C" int dflash_splitk_reduce(const float* partials, int nsplit, int M, in
   const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(nv, 256), 1024);
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3(grid), dim3(256), 0, static_cast<hipStream_t>(stream),
                      partials, nsplit, M, N, static_cast<uint16_t*>(out), out_row_stride);
+  return to_status(hipGetLastError());
+}
+
+extern "C" int dflash_splitk_swiglu_reduce(const float* partials, int nsplit, int M, int N,
+                                           void* out, int64_t out_row_stride, void* stream) {
+  if (M < 0 || N <= 0 || N % 32 != 0 || nsplit < 1) return DFLASH_ERR_SHAPE;
+  if (M == 0) return DFLASH_OK;
+  if (partials == nullptr || out == nullptr) return DFLASH_ERR_NULL;
+  if (((uintptr_t)partials & 15) || ((uintptr_t)out & 7) || (out_row_stride % 4) ||
+      out_row_stride < N / 2)
+    return DFLASH_ERR_ALIGN;
+  const int64_t nv = (int64_t)M * (N / 8);
+  const unsigned grid = (unsigned)std::min<int64_t>(ceil_div(nv, 256), 1024);
+  hipLaunchKernelGGL(splitk_swiglu_reduce_kernel, dim3(grid), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), partials, nsplit, M, N,
+                     static_cast<uint16_t*>(out), out_row_stride);
   return to_status(hipGetLastError());
 }
 

@@ -27,7 +27,10 @@ each attention layer appends P keys and attends causally (:487-540).
   runner's capture layers); a projection into the residual stream whose
   output tiles would leave most compute units idle in the last round runs
   split-K (``dflash_gemm_bf16_tiled_prefill_splitk``) and the add + norm
-  sums its fp32 partials (``dflash_add_rmsnorm_splitk``).
+  sums its fp32 partials (``dflash_add_rmsnorm_splitk``); a projection with
+  a bf16 output (the gated-delta in_proj, q|k|v, gate|up) whose tiles would
+  leave most compute units idle runs split-K too, its partials summed and
+  cast by ``dflash_splitk_reduce`` (gate|up: ``dflash_splitk_swiglu_reduce``).
 
 Before the pass the recurrent states the runner would roll back on its next
 load (tape[keep - 1] when keep >= 1) are gathered into its state buffers
@@ -72,6 +75,24 @@ def residual_splits(N: int, P: int, cus: int) -> int:
         if best_cost is None or cost < best_cost - 1e-9:
             best, best_cost = s, cost
     return best
+
+
+def prompt_splits(N: int, P: int, cus: int) -> int:
+    """K splits for a prompt-sized projection with a bf16 output, summed and
+    cast afterwards by dflash_splitk_reduce / dflash_splitk_swiglu_reduce.
+
+    One launch when the 256 x 256 tile's units give every compute unit one.
+    Otherwise each 256 x 128 tile streams its 256 weight rows on one compute
+    unit, at a rate that does not grow with the units left idle, so a launch
+    of few tiles is as long as one tile: the largest count up to MAX_SPLITS
+    whose units (tiles x splits) still fit the compute units once wins.
+    Measured on MI355X (in_proj, q|k|v and gate|up at 128-1024 prompt rows,
+    partials and reduce included) that count was the fastest or within 4 %
+    of it."""
+    if -(-N // 256) * -(-P // 256) >= cus:
+        return 1
+    tiles = -(-N // 256) * -(-P // 128)
+    return max(1, min(MAX_SPLITS, cus // tiles))
 
 
 class HybridPrefill:
@@ -151,7 +172,17 @@ class HybridPrefill:
         ws = int(self._lib.dflash_gdn_chunked_prefill_workspace_bytes(
             1, P, Hv, lc.linear_key_head_dim, Dv))
         self.chunk_ws = e(max(ws, 16), dt=torch.uint8)
-        self.part = e(MAX_SPLITS * P * H, dt=f32)
+        # fp32 partials of the split projections: the residual ones (N = H) and
+        # the bf16 ones at the split counts this prompt length plans
+        need = MAX_SPLITS * P * H
+        for d in self.w:
+            for name in ("w_in", "w_qkv", "w_gu_pairs"):
+                if name in d:
+                    n = d[name][1]
+                    ns = prompt_splits(n, P, self.cus)
+                    if ns > 1:
+                        need = max(need, int(self._lib.dflash_gemm_splits(H, ns)) * P * n)
+        self.part = e(need, dt=f32)
         self.rows_cap = P
 
     # ------------------------------------------------------------ the pass
@@ -226,8 +257,7 @@ class HybridPrefill:
             lw, tw = layers[i], self.w[i]
             if cfg.is_linear(i):
                 gw = lw["gdn"]
-                wt, n = tw["w_in"]
-                call("dflash_gemm_bf16_tiled_prefill", xn, H, wt.data_ptr(), base, rs, P, n, H, stream)
+                self._bf16_proj(tw["w_in"], xn, H, P, base, rs, False, stream)
                 a_ptr, b_ptr = base + 2 * (C + Hv * Dv + Hv), base + 2 * (C + Hv * Dv)
                 call("dflash_gdn_prologue", base, P * rs, rs, run.conv[gi].data_ptr(),
                      gw.conv_weight.data_ptr(), a_ptr, b_ptr, ab, gw.A_log.data_ptr(),
@@ -243,10 +273,8 @@ class HybridPrefill:
                 branch = self._to_residual(tw["w_out"], self.gnorm.data_ptr(), Hv * Dv, P, stream)
                 gi += 1
             else:
-                wt, n = tw["w_qkv"]
                 ap = self.aproj.data_ptr()
-                call("dflash_gemm_bf16_tiled_prefill", xn, H, wt.data_ptr(), ap, arows, P, n, H,
-                     stream)
+                self._bf16_proj(tw["w_qkv"], xn, H, P, ap, arows, False, stream)
                 call("dflash_attn_prep", ap, arows, lw["q_norm"].data_ptr(), lw["k_norm"].data_ptr(),
                      run.lens.data_ptr(), run.k_cache[ai].data_ptr(), run.vt_cache[ai].data_ptr(),
                      self.q.data_ptr(), run.overflow.data_ptr(), 1, P, Hq, Hkv, D, run.Smax,
@@ -257,9 +285,7 @@ class HybridPrefill:
                 branch = self._to_residual(tw["w_o"], self.attn_out.data_ptr(), Hq * D, P, stream)
                 ai += 1
             self._add_norm(branch, lw["ln_post"], None, P, stream)
-            wt, n = tw["w_gu_pairs"]
-            call("dflash_gemm_bf16_swiglu_tiled_prefill", xn, H, wt.data_ptr(),
-                 self.mlp_act.data_ptr(), I, P, n, H, stream)
+            self._bf16_proj(tw["w_gu_pairs"], xn, H, P, self.mlp_act.data_ptr(), I, True, stream)
             branch = self._to_residual(tw["w_down"], self.mlp_act.data_ptr(), I, P, stream)
             nw = layers[i + 1]["ln_in"] if i + 1 < L else run.w.final_norm
             j = cap_ids.get(i)
@@ -267,6 +293,26 @@ class HybridPrefill:
             self._add_norm(branch, nw, cap, P, stream)
         # every layer's final state is in its tape's slab 0
         run.keep.fill_(1)
+
+    def _bf16_proj(self, weight, x_ptr, K, P, out_ptr, out_stride, swiglu, stream):
+        """out = bf16(x . W^T) (swiglu: the gated form over the w_pairs rows,
+        N / 2 output columns) in one launch, or split-K (prompt_splits) with
+        the partials summed and cast by the reduce."""
+        wt, n = weight
+        ns = prompt_splits(n, P, self.cus)
+        used = int(self._lib.dflash_gemm_splits(K, ns)) if ns > 1 else 1
+        if used > 1 and used * P * n <= self.part.numel():
+            part = self.part.data_ptr()
+            _lib.call("dflash_gemm_bf16_tiled_prefill_splitk", x_ptr, K, wt.data_ptr(), part, ns,
+                      P, n, K, stream)
+            _lib.call("dflash_splitk_swiglu_reduce" if swiglu else "dflash_splitk_reduce", part,
+                      used, P, n, out_ptr, out_stride, stream)
+        elif swiglu:
+            _lib.call("dflash_gemm_bf16_swiglu_tiled_prefill", x_ptr, K, wt.data_ptr(), out_ptr,
+                      out_stride, P, n, K, stream)
+        else:
+            _lib.call("dflash_gemm_bf16_tiled_prefill", x_ptr, K, wt.data_ptr(), out_ptr,
+                      out_stride, P, n, K, stream)
 
     def _to_residual(self, weight, x_ptr, K, P, stream):
         """A projection whose output the residual stream adds: bf16 into r,

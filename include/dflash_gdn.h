@@ -735,6 +735,19 @@ int dflash_splitk_reduce(const float* partials, int nsplit, int M, int N,
                          void* out, int64_t out_row_stride, void* stream);
 
 /*
+ * The MLP's gating over split-K partials (mlx-lm Qwen3NextMLP, called at
+ * dflash_mlx/custom_qwen35_model.py:845; the partials of a
+ * dflash_gemm_bf16_tiled_prefill_splitk over the tiled w_pairs of
+ * dflash_gemm_bf16_swiglu): out[m, j] = bf16(silu(g) * u) with g and u the
+ * split sums (in split order) of partials columns 32 (j / 16) + j % 16 and
+ * that column + 16.  partials fp32 [nsplit, M, N] (16-byte aligned,
+ * N % 32 == 0), out bf16 [M, N/2] with row stride out_row_stride (a
+ * multiple of 4, >= N/2).
+ */
+int dflash_splitk_swiglu_reduce(const float* partials, int nsplit, int M, int N,
+                                void* out, int64_t out_row_stride, void* stream);
+
+/*
  * The MLP's gating (mlx-lm Qwen3NextMLP, called at
  * dflash_mlx/custom_qwen35_model.py:845): out = bf16(silu(gate) * up) with
  * gate_up bf16 [M, 2I] = [gate | up] (one GEMM of the stacked gate/up

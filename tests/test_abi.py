@@ -44,7 +44,8 @@ def test_header_declares_expected_entry_points():
         "dflash_add_rmsnorm", "dflash_swiglu", "dflash_attn_prep",
         "dflash_attn_verify_workspace_bytes", "dflash_attn_verify", "dflash_commit_accept",
         "dflash_add_rmsnorm_splitk", "dflash_add_rmsnorm_capture", "dflash_embed_rmsnorm", "dflash_gemm_bf16", "dflash_gemm_splits",
-        "dflash_splitk_reduce", "dflash_gemm_bf16_swiglu", "dflash_weight_tile_bytes",
+        "dflash_splitk_reduce", "dflash_splitk_swiglu_reduce", "dflash_gemm_bf16_swiglu",
+        "dflash_weight_tile_bytes",
         "dflash_weight_tile_bf16", "dflash_gemm_bf16_tiled", "dflash_gemm_bf16_swiglu_tiled",
         "dflash_gemm_tail_workspace_bytes",
         "dflash_gemm_bf16_tiled_residual_norm",
@@ -252,6 +253,23 @@ def test_gemm_tail_workspace_and_normed_validation(lib):
                      odd, tail, None) == -4
     assert sw_normed(d, 20480, d, d, 160, 1e-6, None, d, d, 9216, 16, 18432, 20480, 4,
                      aligned, tail, None) == -2
+
+
+def test_splitk_swiglu_reduce_validation(lib):
+    """The gated reduce over the w_pairs column order: N a multiple of 32, at
+    least one split, 16-byte aligned partials, output rows of at least N/2
+    columns in 8-byte pieces; M = 0 is a no-op."""
+    d = ctypes.c_void_p(0x1000)
+    f = lib.dflash_splitk_swiglu_reduce
+    assert f(d, 2, 0, 64, d, 32, None) == 0
+    assert f(d, 2, 16, 48, d, 24, None) == -2      # N % 32
+    assert f(d, 0, 16, 64, d, 32, None) == -2      # nsplit < 1
+    assert f(None, 2, 16, 64, d, 32, None) == -1
+    assert f(d, 2, 16, 64, None, 32, None) == -1
+    assert f(ctypes.c_void_p(0x1008), 2, 16, 64, d, 32, None) == -4
+    assert f(d, 2, 16, 64, ctypes.c_void_p(0x1004), 32, None) == -4
+    assert f(d, 2, 16, 64, d, 30, None) == -4      # stride % 4
+    assert f(d, 2, 16, 64, d, 28, None) == -4      # rows shorter than N/2
 
 
 def test_prefill_gemm_validation(lib):

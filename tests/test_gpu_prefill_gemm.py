@@ -142,6 +142,43 @@ def test_prefill_gemm_swiglu(device, M, I, K):
         assert torch.equal(out, ref)
 
 
+@pytest.mark.parametrize("M,N,K,ns,swiglu", [(128, 12352, 2560, 4, False), (37, 5120, 2560, 3, False),
+                                              (128, 18432, 2560, 3, True), (5, 96, 192, 2, True),
+                                              (300, 2080, 640, 4, True)])
+def test_prefill_splitk_reduce_matches_one_launch(device, M, N, K, ns, swiglu):
+    """The prompt pass's split form of a bf16 projection: split-K partials
+    summed and cast by dflash_splitk_reduce (gated: dflash_splitk_swiglu_reduce
+    over the w_pairs columns) against the one-launch GEMM: both round fp32
+    sums of the same products added in another order, so they sit within one
+    bf16 ulp (2^-7 relative) of each other (two for the gated form) plus
+    1e-4 of the output scale; the gated form also against the fp32
+    reference."""
+    print(f"[prefill gemm] split-K + reduce M={M} N={N} K={K} nsplit={ns} swiglu={swiglu}",
+          flush=True)
+    x, w = _inputs(device, M, N, K, seed=M * 5 + N + ns)
+    wt = _tile(w, device)
+    one = _prefill(device, x, wt, M, N, K, swiglu=swiglu)
+    lib = _lib.load()
+    used = int(lib.dflash_gemm_splits(K, ns))
+    part = torch.full((used, M, N), float("nan"), device=device)
+    _lib.call("dflash_gemm_bf16_tiled_prefill_splitk", x.data_ptr(), K, wt.data_ptr(),
+              part.data_ptr(), ns, M, N, K, _lib.stream_handle(device))
+    n_out = N // 2 if swiglu else N
+    ow = torch.full((M, n_out + 8), float("nan"), dtype=torch.bfloat16, device=device)
+    _lib.call("dflash_splitk_swiglu_reduce" if swiglu else "dflash_splitk_reduce", part.data_ptr(),
+              used, M, N, ow.data_ptr(), n_out + 8, _lib.stream_handle(device))
+    torch.cuda.synchronize()
+    got = ow[:, :n_out]
+    assert torch.isnan(ow[:, n_out:].float()).all()  # nothing past the row written
+    ref = one.float()
+    tol = (2 if swiglu else 1) * (2 ** -7) * ref.abs() + 1e-4 * ref.pow(2).mean().sqrt()
+    assert ((got.float() - ref).abs() <= tol).all()
+    if swiglu:
+        g_ = x.float() @ w.float().t()
+        pairs = g_.view(M, N // 32, 2, 16)
+        _check(got, (torch.nn.functional.silu(pairs[:, :, 0]) * pairs[:, :, 1]).reshape(M, N // 2))
+
+
 def test_prefill_gemm_strided_rows(device):
     """Activation and output rows with strides larger than K and N (views
     into wider buffers)."""

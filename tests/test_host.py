@@ -139,3 +139,24 @@ def test_cache_lengths_are_checked_on_the_host():
         check_cache_lengths([-1, 3], 2, 16, 4096)
     with pytest.raises(ValueError):
         check_cache_lengths([1, 2, 3], 2, 16, 4096)
+
+
+def test_prompt_splits_follow_the_measured_rule():
+    """Split counts of the prompt pass's bf16 projections on 256 compute
+    units: the largest count up to 4 whose 256 x 128 tile units still fit the
+    device once; one launch when the 256 x 256 tiles fill it.  The values at
+    the c4 widths are the counts measured fastest (in_proj N = 12352, q|k|v
+    5120, gate|up pairs 18432)."""
+    from dflash_mlx.prefill import MAX_SPLITS, prompt_splits
+
+    want = {(12352, 128): 4, (12352, 256): 2, (12352, 512): 1, (12352, 1024): 1,
+            (5120, 128): 4, (5120, 256): 4, (5120, 512): 3, (5120, 768): 2, (5120, 1024): 1,
+            (18432, 128): 3, (18432, 256): 1, (18432, 4096): 1}
+    for (N, P), s in want.items():
+        assert prompt_splits(N, P, 256) == s, (N, P)
+    for N in (16, 272, 2560, 5120, 12352, 18432):
+        for P in (1, 17, 128, 300, 1000, 4096):
+            s = prompt_splits(N, P, 256)
+            assert 1 <= s <= MAX_SPLITS
+            tiles = -(-N // 256) * -(-P // 128)
+            assert s == 1 or tiles * s <= 256
