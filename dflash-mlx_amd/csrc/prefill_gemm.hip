@@ -17,10 +17,10 @@
 //
 // Two workgroup tiles, chosen per launch: 256 weight rows x 256 activation
 // rows (8 waves, both operands staged in LDS by direct loads; the wide tile
-// below) whenever its work units give every compute unit one, else the
-// 256 x 128 tile described here (twice the units, for short prompts).  Both
-// add each output's products in the same order, so the choice never
-// changes a bit.  The 256 x 128 tile:
+// below) or the 256 x 128 tile described here (twice the units, each about
+// 0.7 of a wide unit's time), whichever takes fewer rounds of the compute
+// units at those costs.  Both add each output's products in the same order,
+// so the choice never changes a bit.  The 256 x 128 tile:
 //   - A workgroup (4 waves) computes 256 weight rows x 128 activation rows.
 //     Wave w owns weight rows 64w .. 64w+63 (4 row tiles) against all 128
 //     activation rows (8 column tiles): 32 accumulator tiles of
@@ -547,11 +547,17 @@ int launch_prefill(const void* x, int64_t x_row_stride, const void* w_tiled, voi
   const int want = nsplit > 0 ? std::min(nsplit, nks) : 1;
   p.ks_per_split = (int)ceil_div(nks, want);
   p.nsplit = (int)ceil_div(nks, p.ks_per_split);
-  // The 256 x 256 tile when its work units give every compute unit one, else
-  // the 256 x 128 tile (twice the units); both add each output's products in
-  // the same order, so the choice never changes a bit.
+  // The tile whose units take less time on the compute units: whole rounds
+  // of units, a 256 x 128 unit costing 0.7 of a 256 x 256 one (measured on
+  // MI355X at the Qwen3.5-4B projection shapes, 512-2048 prompt rows: the
+  // ratio of the two tiles' times at equal rounds was 1.35-1.43, and this
+  // rule picked the faster tile in every case measured; the wide tile on a
+  // tie).  Both add each output's products in the same order, so the
+  // choice never changes a bit.
+  const int64_t cus = std::max(device_cus(), 1);
   const int64_t wide_units = ceil_div(N, kWRows) * ceil_div(M, kWCols) * (int64_t)p.nsplit;
-  const bool wide = wide_units >= device_cus();
+  const int64_t narrow_units = ceil_div(N, kPRows) * ceil_div(M, kPCols) * (int64_t)p.nsplit;
+  const bool wide = 10 * ceil_div(wide_units, cus) <= 7 * ceil_div(narrow_units, cus);
   p.n_tiles = (int)ceil_div(N, wide ? kWRows : kPRows);
   p.m_tiles = (int)ceil_div(M, wide ? kWCols : kPCols);
   const int64_t tiles = (int64_t)p.n_tiles * p.m_tiles;

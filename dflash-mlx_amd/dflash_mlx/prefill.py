@@ -67,12 +67,12 @@ def residual_splits(N: int, P: int, cus: int, K: int) -> int:
     MAX_RESIDUAL_SPLITS (measured on MI355X for out_proj / o_proj / down at
     128-1024 prompt rows, the add + norm included: within 6 % of the fastest
     count, up to 3x faster than one launch).
-    Past that the GEMM runs 256 x 256 output tiles when their work units
-    give every compute unit one, else 256 x 128 tiles; a 256 x 128 unit
-    costs about 0.7 of a 256 x 256 one (half the products at the smaller
-    tile's lower rate).  The count up to MAX_SPLITS with the least time,
-    rounds of units x cost per unit / splits, wins (the smallest on a tie);
-    1 when the wide tiles alone fill two rounds."""
+    Past that the count up to MAX_SPLITS with the least time wins (the
+    smallest on a tie), 1 when the wide tiles alone fill two rounds: the
+    GEMM runs 256 x 256 or 256 x 128 output tiles, whichever takes fewer
+    whole rounds of the compute units with a 256 x 128 unit costing 0.7 of a
+    256 x 256 one (half the products at the smaller tile's lower rate), and
+    a split's time is that cost / splits."""
     wide = -(-N // 256) * -(-P // 256)
     narrow = -(-N // 256) * -(-P // 128)
     if 2 * narrow <= cus:
@@ -81,10 +81,7 @@ def residual_splits(N: int, P: int, cus: int, K: int) -> int:
         return 1
     best, best_cost = 1, None
     for s in range(1, MAX_SPLITS + 1):
-        if wide * s >= cus:
-            cost = -(-(wide * s) // cus) / s
-        else:
-            cost = 0.7 * -(-(narrow * s) // cus) / s
+        cost = min(-(-(wide * s) // cus), 0.7 * -(-(narrow * s) // cus)) / s
         if best_cost is None or cost < best_cost - 1e-9:
             best, best_cost = s, cost
     return best

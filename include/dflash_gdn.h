@@ -703,9 +703,9 @@ int dflash_gemm_bf16_swiglu_tiled_normed(const void* h, int64_t h_row_stride,
  * dflash_gemm_bf16_swiglu (N % 32 == 0) and writes out[M, N/2] =
  * bf16(silu(x . G^T) * (x . U^T)).  x: 16-byte aligned, row stride a
  * multiple of 8 elements (>= K, <= 2^22); out: 8-byte aligned, row stride a
- * multiple of 4 (>= N, or N/2).  Workgroups own 256 x 256 output tiles when
- * those give every compute unit one, else 256 x 128; the sums are the same
- * bits either way.
+ * multiple of 4 (>= N, or N/2).  Workgroups own 256 x 256 or 256 x 128
+ * output tiles, whichever takes fewer rounds of the compute units (a
+ * 256 x 128 tile counted at 0.7); the sums are the same bits either way.
  */
 int dflash_gemm_bf16_tiled_prefill(const void* x, int64_t x_row_stride,
                                    const void* w_tiled, void* out,
