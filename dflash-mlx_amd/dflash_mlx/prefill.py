@@ -53,6 +53,11 @@ from .gdn_layer import QK_NORM_EPS
 MAX_SPLITS = 4
 # Residual projections of short prompts split further (see residual_splits).
 MAX_RESIDUAL_SPLITS = 16
+# The split model's rates (MI355X, measured): one compute unit's MFMA rate
+# on a 256 x 256 prompt GEMM tile (about 1 PFLOP/s over 256 units), and the
+# rate at which split partials are written and read back.
+UNIT_FLOPS = 4.0e12
+PARTIAL_BYTES_PER_S = 5.0e12
 
 
 def residual_splits(N: int, P: int, cus: int, K: int) -> int:
@@ -67,21 +72,30 @@ def residual_splits(N: int, P: int, cus: int, K: int) -> int:
     MAX_RESIDUAL_SPLITS (measured on MI355X for out_proj / o_proj / down at
     128-1024 prompt rows, the add + norm included: within 6 % of the fastest
     count, up to 3x faster than one launch).
-    Past that the count up to MAX_SPLITS with the least time wins (the
-    smallest on a tie), 1 when the wide tiles alone fill two rounds: the
-    GEMM runs 256 x 256 or 256 x 128 output tiles, whichever takes fewer
+    Past that the count up to MAX_SPLITS with the least estimated time wins
+    (the smallest on a tie), 1 when the wide tiles alone fill two rounds.
+    The GEMM runs 256 x 256 or 256 x 128 output tiles, whichever takes fewer
     whole rounds of the compute units with a 256 x 128 unit costing 0.7 of a
-    256 x 256 one (half the products at the smaller tile's lower rate), and
-    a split's time is that cost / splits."""
+    256 x 256 one (half the products at the smaller tile's lower rate); a
+    256 x 256 unit over all K takes 2 * 256 * 256 * K / UNIT_FLOPS and a
+    split's unit 1/s of that; the partials add 8 * s * P * N bytes (written
+    by the GEMM, read by the add + norm) at PARTIAL_BYTES_PER_S against
+    4 * P * N for one launch's bf16 output.  Measured on MI355X (GEMM + add +
+    norm at 2048 and 4096 prompt rows) this picked the fastest count for
+    every projection: 3 at 2048 rows, and at 4096 rows 3 for down, 1 for
+    o_proj (75 against 86 us split 3 ways), a tie for out_proj."""
     wide = -(-N // 256) * -(-P // 256)
     narrow = -(-N // 256) * -(-P // 128)
     if 2 * narrow <= cus:
         return max(1, min(cus // narrow, (K // 64) // 8, MAX_RESIDUAL_SPLITS))
     if wide >= 2 * cus:
         return 1
+    unit_us = 2 * 256 * 256 * K / UNIT_FLOPS * 1e6
     best, best_cost = 1, None
     for s in range(1, MAX_SPLITS + 1):
-        cost = min(-(-(wide * s) // cus), 0.7 * -(-(narrow * s) // cus)) / s
+        rounds = min(-(-(wide * s) // cus), 0.7 * -(-(narrow * s) // cus))
+        traffic = (8 * s if s > 1 else 4) * P * N / PARTIAL_BYTES_PER_S * 1e6
+        cost = rounds * unit_us / s + traffic
         if best_cost is None or cost < best_cost - 1e-9:
             best, best_cost = s, cost
     return best
