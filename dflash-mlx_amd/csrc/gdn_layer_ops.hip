@@ -367,6 +367,53 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const NormParams p) 
     p.y[(int64_t)row * p.D + i * 64 + lane] = f32_to_bf16_rne(xv[i] * r * wv[i] * pro_silu(zv[i]));
 }
 
+// The same norm with 16-byte accesses, for prompt-sized launches whose rows
+// and gates start 16-byte aligned: L = D / 8 lanes a row (lane j of a row holds channels
+// 8j .. 8j+7 of x, z and the weight), 64 / L rows a wavefront, 4 wavefronts
+// a workgroup.  One load instruction moves 1 KB instead of 128 B, which is
+// what bounds the norm over a prompt's thousands of rows.
+template <int L>
+__global__ __launch_bounds__(256) void gated_rmsnorm_vec_kernel(const NormParams p) {
+  constexpr int RW = 64 / L;
+  const int lane = threadIdx.x & 63;
+  const int j = lane % L;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RW + lane / L;
+  const bool live = row0 < p.rows;
+  const int row = live ? row0 : p.rows - 1;  // idle row slots redo the last row, unstored
+  const int h = row % p.H;
+  const int bt = row / p.H;
+  const int t = bt % p.T;
+  const int b = bt / p.T;
+  const uint16_t* x = p.x + (int64_t)row * p.D + 8 * j;
+  const uint16_t* z = p.z + b * p.z_sb + (int64_t)t * p.z_st + (int64_t)h * p.z_sh + 8 * j;
+  const u32x4 xr = *reinterpret_cast<const u32x4*>(x);
+  const u32x4 zr = *reinterpret_cast<const u32x4*>(z);
+  const u32x4 wr = *reinterpret_cast<const u32x4*>(p.w + 8 * j);
+  float xv[8], zv[8], wv[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    xv[2 * i] = bf16_bits_to_f32(xr[i] & 0xffffu);
+    xv[2 * i + 1] = bf16_bits_to_f32(xr[i] >> 16);
+    zv[2 * i] = bf16_bits_to_f32(zr[i] & 0xffffu);
+    zv[2 * i + 1] = bf16_bits_to_f32(zr[i] >> 16);
+    wv[2 * i] = bf16_bits_to_f32(wr[i] & 0xffffu);
+    wv[2 * i + 1] = bf16_bits_to_f32(wr[i] >> 16);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ss = fmaf(xv[i], xv[i], ss);
+#pragma unroll
+  for (int o = L / 2; o >= 1; o >>= 1) ss += __shfl_xor(ss, o, 64);  // the row's L lanes
+  const float r = rsqrtf(ss / (float)p.D + p.eps);
+  u32x4 out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    out[i] = (uint32_t)f32_to_bf16_rne(xv[2 * i] * r * wv[2 * i] * pro_silu(zv[2 * i])) |
+             ((uint32_t)f32_to_bf16_rne(xv[2 * i + 1] * r * wv[2 * i + 1] *
+                                        pro_silu(zv[2 * i + 1])) << 16);
+  if (live) *reinterpret_cast<u32x4*>(p.y + (int64_t)row * p.D + 8 * j) = out;
+}
+
 }  // namespace
 }  // namespace dflash
 
@@ -475,8 +522,26 @@ extern "C" int dflash_gdn_gated_rmsnorm(const void* x, const void* z, const int6
   p.D = D;
   p.rows = B * T * H;
   p.eps = eps;
-  const dim3 grid((unsigned)ceil_div(p.rows, 4));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // 16-byte accesses over a prompt's rows when every row and gate start
+  // allows them (D % 64 == 0 already makes the row a multiple of 8
+  // channels).  At verify sizes (hundreds of rows) the one-wave-a-row form
+  // is faster: it spreads the same rows over 4x-8x the workgroups, and
+  // latency, not instructions, bounds it there.
+  const bool vec = p.rows >= 4096 &&
+                   ((((uintptr_t)x | (uintptr_t)z | (uintptr_t)weight | (uintptr_t)y) & 15) == 0) &&
+                   p.z_sb % 8 == 0 && p.z_st % 8 == 0 && p.z_sh % 8 == 0;
+  if (vec) {
+    const int L = D / 8;  // 8, 16, 24 or 32 lanes a row
+    if (L == 8 || L == 16 || L == 32) {
+      const dim3 vgrid((unsigned)ceil_div(p.rows, 4 * (64 / L)));
+      if (L == 8) hipLaunchKernelGGL(gated_rmsnorm_vec_kernel<8>, vgrid, dim3(256), 0, s, p);
+      else if (L == 16) hipLaunchKernelGGL(gated_rmsnorm_vec_kernel<16>, vgrid, dim3(256), 0, s, p);
+      else hipLaunchKernelGGL(gated_rmsnorm_vec_kernel<32>, vgrid, dim3(256), 0, s, p);
+      return to_status(hipGetLastError());
+    }
+  }
+  const dim3 grid((unsigned)ceil_div(p.rows, 4));
   switch (D / 64) {
     case 1: hipLaunchKernelGGL(gated_rmsnorm_kernel<1>, grid, dim3(256), 0, s, p); break;
     case 2: hipLaunchKernelGGL(gated_rmsnorm_kernel<2>, grid, dim3(256), 0, s, p); break;

@@ -88,17 +88,23 @@ def test_prologue_matches_oracle(oracle, device, cfg, B, T):
     np.testing.assert_array_equal(new_conv.float().cpu().numpy(), rst)
 
 
-@pytest.mark.parametrize("B,T,H,D", [(2, 16, 32, 128), (1, 3, 5, 64), (1, 16, 7, 192), (2, 1, 3, 256)])
-def test_gated_rmsnorm_matches_oracle(oracle, device, B, T, H, D):
+@pytest.mark.parametrize("zoff", [0, 1])
+@pytest.mark.parametrize("B,T,H,D", [(2, 16, 32, 128), (1, 3, 5, 64), (1, 16, 7, 192), (2, 1, 3, 256),
+                                     (1, 161, 32, 128), (1, 129, 40, 64), (2, 33, 64, 256),
+                                     (1, 100, 41, 192)])
+def test_gated_rmsnorm_matches_oracle(oracle, device, B, T, H, D, zoff):
     """Every compiled channel count (D / 64 = 1..4), rows not a multiple of the
-    4 per workgroup, the gate as a strided view of a wider projection row."""
+    rows per workgroup, the gate as a strided view of a wider projection row.
+    Launches of 4096 rows or more with zoff = 0 (16-byte aligned rows and
+    gates) take the 16-byte form (D = 64, 128, 256), the rest and zoff = 1
+    (the gate one element off) the one-wave-a-row form."""
     gen = torch.Generator().manual_seed(7 + D)
-    print(f"[gated_rmsnorm B={B} T={T} H={H} D={D}]", flush=True)
+    print(f"[gated_rmsnorm B={B} T={T} H={H} D={D} zoff={zoff}]", flush=True)
     x = torch.randn(B, T, H, D, generator=gen).bfloat16()
     zfull = torch.randn(B, T, H * D + 64, generator=gen).bfloat16()
-    z = zfull[..., :H * D].unflatten(-1, (H, D))       # strided view, as out of a projection
+    z = zfull[..., zoff:zoff + H * D].unflatten(-1, (H, D))  # strided view, as out of a projection
     wgt = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16()
-    y = gated_rmsnorm(x.to(device), zfull.to(device)[..., :H * D].unflatten(-1, (H, D)),
+    y = gated_rmsnorm(x.to(device), zfull.to(device)[..., zoff:zoff + H * D].unflatten(-1, (H, D)),
                       wgt.to(device), 1e-6)
     torch.cuda.synchronize()
     ref = oracle.gated_rmsnorm(x.float().numpy(), z.float().numpy(), wgt.float().numpy(), 1e-6)
