@@ -189,6 +189,7 @@ struct AttnPrepParams {
   uint16_t* q_out;     // [B, T, Hq, D]
   int32_t* overflow;   // [B] or null: set to 1 when a block position falls outside [0, Smax)
   int B, T, Hq, Hkv, Smax, rot;
+  int skip_v;          // value heads left to attn_prep_vt_kernel
   double log2_base;
   float eps;
 };
@@ -218,6 +219,7 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const AttnPrepParams p) 
   const uint16_t* row = p.proj + (int64_t)bt * p.row_stride;
   const int d0 = 2 * lane;
   if (slot >= p.Hq + p.Hkv) {  // value head: V^T cache column
+    if (p.skip_v) return;
     const int h = slot - p.Hq - p.Hkv;
     const uint32_t vv = *reinterpret_cast<const uint32_t*>(row + p.Hq * 2 * kHD + p.Hkv * kHD + h * kHD + d0);
     if (in_cache) {
@@ -265,6 +267,46 @@ __global__ __launch_bounds__(256) void attn_prep_kernel(const AttnPrepParams p) 
   } else if (in_cache) {
     *reinterpret_cast<uint32_t*>(p.k_cache + (((int64_t)b * p.Hkv + h) * p.Smax + pos) * kHD + d0) =
         packed;
+  }
+}
+
+// The value heads of a long input (a prompt pass) into the transposed cache:
+// workgroup (block of kVtTile tokens, value head h, sequence b).  Per token
+// the value row is one 256-byte run of proj, but in vt_cache each of its 128
+// features lands in another row (Smax positions apart), so one wave a token
+// scatters 2-byte stores.  Here the block's rows go to LDS (16 bytes a
+// thread) and each feature's kVtTile positions are then stored by
+// consecutive lanes: one 128-byte run a store.  Positions outside
+// [0, Smax) are not written (attn_prep_kernel's query head 0 records them
+// in the overflow word).  The values are copied bit for bit.
+constexpr int kVtTile = 64;
+
+__global__ __launch_bounds__(256) void attn_prep_vt_kernel(const AttnPrepParams p) {
+  __shared__ uint32_t sv[kVtTile][kHD / 2 + 1];  // a row of 128 bf16, 4 bytes of pad
+  const int t0 = blockIdx.x * kVtTile, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int nt = min(kVtTile, p.T - t0);
+  // piece e: token e / 16, features 8 (e % 16) .. +7
+#pragma unroll
+  for (int i = 0; i < kVtTile * kHD / 8 / 256; ++i) {
+    const int e = tid + 256 * i;
+    const int tk = e >> 4, c = e & 15;
+    if (tk < nt) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(
+          p.proj + ((int64_t)b * p.T + t0 + tk) * p.row_stride + p.Hq * 2 * kHD + p.Hkv * kHD +
+          h * kHD + 8 * c);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) sv[tk][4 * c + w] = v[w];
+    }
+  }
+  __syncthreads();
+  const int lane = tid & 63, wave = tid >> 6;
+  const int pos = p.lens[b] + t0 + lane;
+  if (lane >= nt || pos < 0 || pos >= p.Smax) return;
+  uint16_t* col = p.vt_cache + ((int64_t)b * p.Hkv + h) * kHD * p.Smax + pos;
+  for (int d = wave; d < kHD; d += 4) {
+    const uint32_t pair = sv[lane][d >> 1];
+    col[(int64_t)d * p.Smax] = (uint16_t)((d & 1) ? (pair >> 16) : pair);
   }
 }
 
@@ -795,8 +837,17 @@ extern "C" int dflash_attn_prep(const void* proj, int64_t proj_row_stride, const
   p.B = B; p.T = T; p.Hq = Hq; p.Hkv = Hkv; p.Smax = Smax; p.rot = rot_dims;
   p.log2_base = log2((double)rope_base);
   p.eps = eps;
-  const dim3 grid((unsigned)(B * T), (unsigned)ceil_div(Hq + 2 * Hkv, 4));
-  hipLaunchKernelGGL(attn_prep_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream), p);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // Long inputs with 16-byte aligned value rows: the value heads through
+  // attn_prep_vt_kernel's tiles instead of a wave a token.
+  p.skip_v = T >= kVtTile && ((uintptr_t)proj & 15) == 0 && proj_row_stride % 8 == 0;
+  const int slots = p.skip_v ? Hq + Hkv : Hq + 2 * Hkv;
+  const dim3 grid((unsigned)(B * T), (unsigned)ceil_div(slots, 4));
+  hipLaunchKernelGGL(attn_prep_kernel, grid, dim3(256), 0, s, p);
+  if (p.skip_v) {
+    const dim3 vgrid((unsigned)ceil_div(T, kVtTile), (unsigned)Hkv, (unsigned)B);
+    hipLaunchKernelGGL(attn_prep_vt_kernel, vgrid, dim3(256), 0, s, p);
+  }
   return to_status(hipGetLastError());
 }
 

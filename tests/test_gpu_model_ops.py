@@ -96,8 +96,12 @@ def _attn_prep(device, B, T, lens, Smax, seed):
     return q, kc, vtc, ref, proj
 
 
-@pytest.mark.parametrize("B,T,lens", [(1, 16, [4096]), (2, 16, [0, 1000]), (3, 5, [7, 63, 64])])
+@pytest.mark.parametrize("B,T,lens", [(1, 16, [4096]), (2, 16, [0, 1000]), (3, 5, [7, 63, 64]),
+                                    (1, 200, [37]), (2, 130, [0, 4001]), (1, 64, [3000])])
 def test_attn_prep_norm_rope_and_cache_append(device, B, T, lens):
+    """q / k normed and rotated, V copied into the transposed cache at
+    lens[b] + t, nothing else written; T >= 64 takes the value heads through
+    64-token tiles (a last partial tile, odd start positions)."""
     Smax = 4160
     print(f"[attn_prep] B={B} T={T} lens={lens}", flush=True)
     q, kc, vtc, (q_ref, k_ref, v_ref, _), _ = _attn_prep(device, B, T, lens, Smax, seed=B * 7 + T)
