@@ -90,7 +90,8 @@ constexpr bool kPSwizzle = DFLASH_PREFILL_SWIZZLE;  // swizzled activation tile 
 struct PrefillGemmParams {
   const uint16_t* x;  // [M][xs]
   int64_t xs;
-  const uint16_t* w;  // fragment-tiled [K/64][N/16][2][64][8]
+  const uint16_t* w;  // fragment-tiled [K/64][nt_w][2][64][8], at the launch's first row tile
+  int nt_w;           // row tiles per k-step of the weight (its full row count / 16)
   uint16_t* out;      // [M][os]
   int64_t os;
   float* part;        // split-K: fp32 partial sums [nsplit][M][N] (out unused)
@@ -115,7 +116,7 @@ __device__ __forceinline__ void load_a(const PrefillGemmParams& p, int ks, int r
   for (int i = 0; i < 4; ++i) {
     const int rt = min(rt0 + i, NT - 1);
     const u32x4* src = reinterpret_cast<const u32x4*>(
-        p.w + (((int64_t)ks * NT + rt) * 2) * 512 + lane * 8);
+        p.w + (((int64_t)ks * p.nt_w + rt) * 2) * 512 + lane * 8);
     a[2 * i] = __builtin_nontemporal_load(src);
     a[2 * i + 1] = __builtin_nontemporal_load(src + 64);
   }
@@ -367,7 +368,7 @@ __device__ __forceinline__ void wide_load_stage(const PrefillGemmParams& p, int 
   const int ks = hs >> 1, h = hs & 1;
   if (wave < 4) {
     const int NT = p.N >> 4;
-    const char* wb = reinterpret_cast<const char*>(p.w) + (int64_t)ks * NT * 2048 + h * 1024;
+    const char* wb = reinterpret_cast<const char*>(p.w) + (int64_t)ks * p.nt_w * 2048 + h * 1024;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int f = 4 * wave + i;
@@ -517,12 +518,16 @@ __global__ __launch_bounds__(512, 1) void prefill_gemm_wide_kernel(const Prefill
   }
 }
 
-// nsplit == 0: bf16 out (SwiGLU with swiglu); nsplit >= 1: fp32 partial
-// sums of dflash_gemm_splits-style k-ranges into part [splits][M][N].
-int launch_prefill(const void* x, int64_t x_row_stride, const void* w_tiled, void* out,
-                   int64_t out_row_stride, float* part, int nsplit, int M, int N, int K,
-                   bool swiglu, void* stream) {
-  if (M < 0 || N <= 0 || K <= 0 || K % 64 != 0 || N % (swiglu ? 32 : 16) != 0 || nsplit < 0)
+// Rows row0 .. row0+N-1 of a tiled weight of w_rows rows.  nsplit == 0:
+// bf16 out (SwiGLU with swiglu); nsplit >= 1: fp32 partial sums of
+// dflash_gemm_splits-style k-ranges into part [splits][M][N].
+int launch_prefill(const void* x, int64_t x_row_stride, const void* w_tiled, int w_rows, int row0,
+                   void* out, int64_t out_row_stride, float* part, int nsplit, int M, int N,
+                   int K, bool swiglu, void* stream) {
+  const int rows_unit = swiglu ? 32 : 16;
+  if (M < 0 || N <= 0 || K <= 0 || K % 64 != 0 || N % rows_unit != 0 || nsplit < 0)
+    return DFLASH_ERR_SHAPE;
+  if (row0 < 0 || row0 % rows_unit != 0 || w_rows % 16 != 0 || (int64_t)row0 + N > w_rows)
     return DFLASH_ERR_SHAPE;
   if (x_row_stride < K || (nsplit == 0 && out_row_stride < (swiglu ? N / 2 : N)))
     return DFLASH_ERR_SHAPE;
@@ -538,7 +543,9 @@ int launch_prefill(const void* x, int64_t x_row_stride, const void* w_tiled, voi
   PrefillGemmParams p{};
   p.x = static_cast<const uint16_t*>(x);
   p.xs = x_row_stride;
-  p.w = static_cast<const uint16_t*>(w_tiled);
+  // the first row tile of the range; k-steps stay w_rows / 16 tiles apart
+  p.w = static_cast<const uint16_t*>(w_tiled) + (int64_t)(row0 / 16) * 1024;
+  p.nt_w = w_rows / 16;
   p.out = static_cast<uint16_t*>(out);
   p.os = out_row_stride;
   p.part = nsplit > 0 ? part : nullptr;
@@ -588,16 +595,16 @@ extern "C" int dflash_gemm_bf16_tiled_prefill(const void* x, int64_t x_row_strid
                                               const void* w_tiled, void* out,
                                               int64_t out_row_stride, int M, int N, int K,
                                               void* stream) {
-  return dflash::launch_prefill(x, x_row_stride, w_tiled, out, out_row_stride, nullptr, 0, M, N,
-                                K, false, stream);
+  return dflash::launch_prefill(x, x_row_stride, w_tiled, N, 0, out, out_row_stride, nullptr, 0,
+                                M, N, K, false, stream);
 }
 
 extern "C" int dflash_gemm_bf16_swiglu_tiled_prefill(const void* x, int64_t x_row_stride,
                                                      const void* w_pairs_tiled, void* out,
                                                      int64_t out_row_stride, int M, int N, int K,
                                                      void* stream) {
-  return dflash::launch_prefill(x, x_row_stride, w_pairs_tiled, out, out_row_stride, nullptr, 0,
-                                M, N, K, true, stream);
+  return dflash::launch_prefill(x, x_row_stride, w_pairs_tiled, N, 0, out, out_row_stride,
+                                nullptr, 0, M, N, K, true, stream);
 }
 
 extern "C" int dflash_gemm_bf16_tiled_prefill_splitk(const void* x, int64_t x_row_stride,
@@ -605,6 +612,16 @@ extern "C" int dflash_gemm_bf16_tiled_prefill_splitk(const void* x, int64_t x_ro
                                                      int nsplit, int M, int N, int K,
                                                      void* stream) {
   if (nsplit < 1) return DFLASH_ERR_SHAPE;
-  return dflash::launch_prefill(x, x_row_stride, w_tiled, nullptr, 0, partials, nsplit, M, N, K,
-                                false, stream);
+  return dflash::launch_prefill(x, x_row_stride, w_tiled, N, 0, nullptr, 0, partials, nsplit, M,
+                                N, K, false, stream);
+}
+
+extern "C" int dflash_gemm_bf16_tiled_prefill_rows(const void* x, int64_t x_row_stride,
+                                                   const void* w_tiled, int w_rows, int row0,
+                                                   void* out, int64_t out_row_stride,
+                                                   float* partials, int nsplit, int M, int N,
+                                                   int K, int swiglu, void* stream) {
+  if (nsplit < 0 || (nsplit > 0 && swiglu)) return DFLASH_ERR_SHAPE;
+  return dflash::launch_prefill(x, x_row_stride, w_tiled, w_rows, row0, out, out_row_stride,
+                                partials, nsplit, M, N, K, swiglu != 0, stream);
 }

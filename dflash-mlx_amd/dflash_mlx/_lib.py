@@ -88,6 +88,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "dflash_gemm_bf16_tiled_prefill": (_I, [_VP, _I64, _VP, _VP, _I64, _I, _I, _I, _VP]),
     "dflash_gemm_bf16_swiglu_tiled_prefill": (_I, [_VP, _I64, _VP, _VP, _I64, _I, _I, _I, _VP]),
     "dflash_gemm_bf16_tiled_prefill_splitk": (_I, [_VP, _I64, _VP, _VP, _I, _I, _I, _I, _VP]),
+    "dflash_gemm_bf16_tiled_prefill_rows": (
+        _I, [_VP, _I64, _VP, _I, _I, _VP, _I64, _VP, _I, _I, _I, _I, _I, _VP]),
     "dflash_splitk_reduce": (_I, [_VP, _I, _I, _I, _VP, _I64, _VP]),
     "dflash_splitk_swiglu_reduce": (_I, [_VP, _I, _I, _I, _VP, _I64, _VP]),
     "dflash_swiglu": (_I, [_VP, _VP, _I, _I, _VP]),

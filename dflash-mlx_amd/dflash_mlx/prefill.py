@@ -119,6 +119,37 @@ def prompt_splits(N: int, P: int, cus: int) -> int:
     return max(1, min(MAX_SPLITS, cus // tiles))
 
 
+MAX_TAIL_SPLITS = 16
+
+
+def tail_split(N: int, P: int, cus: int, K: int) -> tuple[int, int] | None:
+    """(rows of the main launch, k-splits of the rest) for a bf16 prompt
+    projection whose 256 x 256 units end in a mostly empty round, else None.
+
+    U units of 256 x 256 on the compute units run as U // cus whole rounds
+    and a last one of U % cus; when that last round is at most half full the
+    GEMM runs as two launches (dflash_gemm_bf16_tiled_prefill_rows): the
+    weight rows of the whole rounds as usual, and the last n-tiles' rows
+    split-K into enough units to fill one round of 1/s of the time (at least
+    4 k-steps of 64 a split, at most MAX_TAIL_SPLITS), their partials summed
+    and cast by the reduce.  None where the kernel would take the 256 x 128
+    tile (see dflash_gemm_bf16_tiled_prefill) or nothing is gained."""
+    n_tiles, m_tiles = -(-N // 256), -(-P // 256)
+    wide = n_tiles * m_tiles
+    narrow = n_tiles * -(-P // 128)
+    if 10 * -(-wide // cus) > 7 * -(-narrow // cus):
+        return None
+    rounds, last = divmod(wide, cus)
+    if rounds < 1 or last == 0 or 2 * last > cus:
+        return None
+    n_tail = -(-last // m_tiles)
+    rows_main = (n_tiles - n_tail) * 256
+    if rows_main <= 0 or rows_main >= N:
+        return None
+    s = min(MAX_TAIL_SPLITS, cus // (n_tail * m_tiles), (K // 64) // 4)
+    return (rows_main, s) if s >= 2 else None
+
+
 class HybridPrefill:
     """Prompt pass over the caches of ``runner`` (B = 1)."""
 
@@ -206,6 +237,11 @@ class HybridPrefill:
                     ns = residual_splits(n, P, self.cus, K)
                 else:
                     ns = prompt_splits(n, P, self.cus)
+                    tail = tail_split(n, P, self.cus, K) if ns == 1 else None
+                    if tail is not None:
+                        rows_main, ts = tail
+                        need = max(need, int(self._lib.dflash_gemm_splits(K, ts)) * P
+                                   * (n - rows_main))
                 if ns > 1:
                     need = max(need, int(self._lib.dflash_gemm_splits(K, ns)) * P * n)
         self.part = e(max(need, 4), dt=f32)
@@ -322,18 +358,35 @@ class HybridPrefill:
 
     def _bf16_proj(self, weight, x_ptr, K, P, out_ptr, out_stride, swiglu, stream):
         """out = bf16(x . W^T) (swiglu: the gated form over the w_pairs rows,
-        N / 2 output columns) in one launch, or split-K (prompt_splits) with
-        the partials summed and cast by the reduce."""
+        N / 2 output columns) in one launch; or split-K (prompt_splits) with
+        the partials summed and cast by the reduce; or the rows of the whole
+        rounds in one launch and the last n-tiles' rows split-K (tail_split)."""
         wt, n = weight
         ns = prompt_splits(n, P, self.cus)
         used = int(self._lib.dflash_gemm_splits(K, ns)) if ns > 1 else 1
+        tail = tail_split(n, P, self.cus, K) if ns == 1 else None
+        reduce = "dflash_splitk_swiglu_reduce" if swiglu else "dflash_splitk_reduce"
         if used > 1 and used * P * n <= self.part.numel():
             part = self.part.data_ptr()
             _lib.call("dflash_gemm_bf16_tiled_prefill_splitk", x_ptr, K, wt.data_ptr(), part, ns,
                       P, n, K, stream)
-            _lib.call("dflash_splitk_swiglu_reduce" if swiglu else "dflash_splitk_reduce", part,
-                      used, P, n, out_ptr, out_stride, stream)
-        elif swiglu:
+            _lib.call(reduce, part, used, P, n, out_ptr, out_stride, stream)
+            return
+        if tail is not None:
+            rows_main, ts = tail
+            n_tail = n - rows_main
+            tused = int(self._lib.dflash_gemm_splits(K, ts))
+            if tused > 1 and tused * P * n_tail <= self.part.numel():
+                part = self.part.data_ptr()
+                _lib.call("dflash_gemm_bf16_tiled_prefill_rows", x_ptr, K, wt.data_ptr(), n, 0,
+                          out_ptr, out_stride, None, 0, P, rows_main, K, int(swiglu), stream)
+                _lib.call("dflash_gemm_bf16_tiled_prefill_rows", x_ptr, K, wt.data_ptr(), n,
+                          rows_main, None, 0, part, ts, P, n_tail, K, 0, stream)
+                out_col = rows_main // 2 if swiglu else rows_main
+                _lib.call(reduce, part, tused, P, n_tail, out_ptr + 2 * out_col, out_stride,
+                          stream)
+                return
+        if swiglu:
             _lib.call("dflash_gemm_bf16_swiglu_tiled_prefill", x_ptr, K, wt.data_ptr(), out_ptr,
                       out_stride, P, n, K, stream)
         else:

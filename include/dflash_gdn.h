@@ -728,6 +728,24 @@ int dflash_gemm_bf16_tiled_prefill_splitk(const void* x, int64_t x_row_stride,
                                           void* stream);
 
 /*
+ * The prompt-sized GEMMs over rows row0 .. row0+N-1 of a tiled weight of
+ * w_rows rows (the same projections of custom_qwen35_model.py:726-736 as
+ * above; a launch over part of a projection, so that a projection's last
+ * output tiles can run split-K apart from the rest): nsplit == 0 writes
+ * bf16 out[M, N] (swiglu != 0: the gated out[M, N/2] of a w_pairs weight),
+ * nsplit >= 1 writes fp32 partials [dflash_gemm_splits(K, nsplit), M, N]
+ * (swiglu must be 0; dflash_splitk_swiglu_reduce gates a w_pairs range).
+ * Each output's sums are the bits of the whole-weight launch.  Needs
+ * w_rows % 16 == 0, row0 and N multiples of 16 (32 with swiglu),
+ * row0 + N <= w_rows; otherwise as dflash_gemm_bf16_tiled_prefill(_splitk).
+ */
+int dflash_gemm_bf16_tiled_prefill_rows(const void* x, int64_t x_row_stride,
+                                        const void* w_tiled, int w_rows, int row0,
+                                        void* out, int64_t out_row_stride,
+                                        float* partials, int nsplit, int M, int N,
+                                        int K, int swiglu, void* stream);
+
+/*
  * out[m, n] = bf16(sum_s partials[s, m, n]) for partials fp32 [nsplit, M, N]
  * (N % 4 == 0), out bf16 with row stride out_row_stride.
  */

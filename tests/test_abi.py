@@ -51,7 +51,7 @@ def test_header_declares_expected_entry_points():
         "dflash_gemm_bf16_tiled_residual_norm",
         "dflash_gemm_bf16_tiled_normed", "dflash_gemm_bf16_swiglu_tiled_normed",
         "dflash_gemm_bf16_tiled_prefill", "dflash_gemm_bf16_swiglu_tiled_prefill",
-        "dflash_gemm_bf16_tiled_prefill_splitk",
+        "dflash_gemm_bf16_tiled_prefill_splitk", "dflash_gemm_bf16_tiled_prefill_rows",
         "dflash_attn_prefill",
     ])
 
@@ -295,6 +295,23 @@ def test_prefill_gemm_validation(lib):
     assert g(d, 2560, d, d, 9216, 100, 18448, 2560, None) == -2   # N % 32
     assert g(d, 2560, d, d, 9000, 100, 18432, 2560, None) == -2   # out rows shorter than N/2
     assert g(d, 2560, d, d, 9218, 100, 18432, 2560, None) == -4   # out stride % 4
+
+
+def test_prefill_gemm_rows_validation(lib):
+    """A row range of a tiled weight: row0 and N whole 16-row tiles (32 with
+    the gated form), inside the weight; partials and the gated form are
+    exclusive; otherwise the whole-weight checks."""
+    d = ctypes.c_void_p(0x1000)
+    f = lib.dflash_gemm_bf16_tiled_prefill_rows
+    assert f(d, 2560, d, 4096, 256, d, 256, None, 0, 0, 256, 2560, 0, None) == 0     # M = 0
+    assert f(d, 2560, d, 4096, 8, d, 256, None, 0, 100, 256, 2560, 0, None) == -2    # row0 % 16
+    assert f(d, 2560, d, 4096, 16, d, 128, None, 0, 100, 256, 2560, 1, None) == -2   # row0 % 32
+    assert f(d, 2560, d, 4096, 3968, d, 256, None, 0, 100, 256, 2560, 0, None) == -2  # past w_rows
+    assert f(d, 2560, d, 4100, 0, d, 256, None, 0, 100, 256, 2560, 0, None) == -2    # w_rows % 16
+    assert f(d, 2560, d, 4096, -16, d, 256, None, 0, 100, 256, 2560, 0, None) == -2  # row0 < 0
+    assert f(d, 2560, d, 4096, 0, None, 0, d, 2, 100, 256, 2560, 1, None) == -2     # partials + gated
+    assert f(d, 2560, d, 4096, 0, None, 0, None, 2, 100, 256, 2560, 0, None) == -1
+    assert f(d, 2560, d, 4096, 0, d, 200, None, 0, 100, 256, 2560, 0, None) == -2    # out rows < N
 
 
 def test_attn_prefill_validation(lib):

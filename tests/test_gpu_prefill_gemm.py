@@ -179,6 +179,57 @@ def test_prefill_splitk_reduce_matches_one_launch(device, M, N, K, ns, swiglu):
         _check(got, (torch.nn.functional.silu(pairs[:, :, 0]) * pairs[:, :, 1]).reshape(M, N // 2))
 
 
+@pytest.mark.parametrize("M,N,K,row0,rows,swiglu,ns", [
+    (300, 4112, 192, 256, 3856, False, 0), (300, 4112, 192, 4096, 16, False, 3),
+    (129, 2080, 640, 0, 1024, True, 0), (129, 2080, 640, 1024, 1056, False, 4),
+    (1000, 12352, 256, 12288, 64, False, 4)])
+def test_prefill_gemm_row_range(device, M, N, K, row0, rows, swiglu, ns):
+    """dflash_gemm_bf16_tiled_prefill_rows over rows row0 .. row0+rows-1 of a
+    tiled weight: bf16 (or gated) outputs bit for bit the same columns of the
+    whole-weight launch; split-K partials summing to those columns' fp32
+    reference, and through the reduce (the gated one for a w_pairs range)
+    within one bf16 ulp of the whole launch's columns."""
+    print(f"[prefill gemm] rows {row0}..{row0 + rows} of {N} M={M} K={K} swiglu={swiglu} "
+          f"nsplit={ns}", flush=True)
+    x, w = _inputs(device, M, N, K, seed=M + row0 + rows)
+    wt = _tile(w, device)
+    gated = swiglu or (ns > 0 and row0 % 32 == 0 and rows % 32 == 0 and N % 32 == 0)
+    whole = _prefill(device, x, wt, M, N, K, swiglu=swiglu)
+    st = _lib.stream_handle(device)
+    if ns == 0:
+        n_out = rows // 2 if swiglu else rows
+        got = torch.full((M, n_out), float("nan"), dtype=torch.bfloat16, device=device)
+        _lib.call("dflash_gemm_bf16_tiled_prefill_rows", x.data_ptr(), K, wt.data_ptr(), N, row0,
+                  got.data_ptr(), n_out, None, 0, M, rows, K, int(swiglu), st)
+        torch.cuda.synchronize()
+        c0 = row0 // 2 if swiglu else row0
+        assert torch.equal(got, whole[:, c0:c0 + n_out])
+        return
+    used = int(_lib.load().dflash_gemm_splits(K, ns))
+    part = torch.full((used, M, rows), float("nan"), device=device)
+    _lib.call("dflash_gemm_bf16_tiled_prefill_rows", x.data_ptr(), K, wt.data_ptr(), N, row0,
+              None, 0, part.data_ptr(), ns, M, rows, K, 0, st)
+    torch.cuda.synchronize()
+    ref = x.float() @ w[row0:row0 + rows].float().t()
+    scale = ref.pow(2).mean().sqrt().item()
+    assert torch.isfinite(part).all()
+    assert (part.sum(0) - ref).abs().max().item() <= 1e-4 * scale + 1e-5
+    red = torch.full((M, rows), float("nan"), dtype=torch.bfloat16, device=device)
+    _lib.call("dflash_splitk_reduce", part.data_ptr(), used, M, rows, red.data_ptr(), rows, st)
+    torch.cuda.synchronize()
+    one = whole[:, row0:row0 + rows].float()
+    assert ((red.float() - one).abs() <= (2 ** -7) * one.abs() + 1e-4 * scale).all()
+    if gated:  # the same range of a w_pairs weight through the gated reduce
+        gw = _prefill(device, x, wt, M, N, K, swiglu=True)
+        gr = torch.full((M, rows // 2), float("nan"), dtype=torch.bfloat16, device=device)
+        _lib.call("dflash_splitk_swiglu_reduce", part.data_ptr(), used, M, rows, gr.data_ptr(),
+                  rows // 2, st)
+        torch.cuda.synchronize()
+        g1 = gw[:, row0 // 2:(row0 + rows) // 2].float()
+        gs = g1.pow(2).mean().sqrt().item()
+        assert ((gr.float() - g1).abs() <= 2 * (2 ** -7) * g1.abs() + 1e-4 * gs).all()
+
+
 def test_prefill_gemm_strided_rows(device):
     """Activation and output rows with strides larger than K and N (views
     into wider buffers)."""
