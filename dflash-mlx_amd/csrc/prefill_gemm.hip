@@ -286,43 +286,63 @@ __global__ __launch_bounds__(256, 1) void prefill_gemm_kernel(const PrefillGemmP
 }
 
 // ---------------------------------------------------------------------------
-// Wide tile: 256 weight rows x 256 activation rows per workgroup of 8 waves,
-// both operands staged in LDS by direct global -> LDS loads.
+// Wide tile: 256 weight rows x 256 activation rows per workgroup of 12 waves
+// (8 that multiply, 4 that load), both operands staged in LDS by direct
+// global -> LDS loads.
 //
-// Wave w (wr = w / 2, wc = w % 2) owns weight row tiles 4 wr .. 4 wr + 3
-// against activation column tiles 8 wc .. 8 wc + 7: 32 accumulator tiles,
-// 32 MFMAs per half k-step (32 k); two waves share each SIMD.  A stage is one
-// half k-step of both operands in fragment order, 32 KB: the 16 weight
-// fragments (1 KB each, straight from the tiled layout) and the 16
-// activation fragments (lane (r16, g) of fragment (c, h) holds
+// Compute wave w < 8 (wr = w / 2, wc = w % 2) owns weight row tiles
+// 4 wr .. 4 wr + 3 against activation column tiles 8 wc .. 8 wc + 7: 32
+// accumulator tiles, 32 MFMAs per half k-step (32 k), and issues no global
+// load.  A stage is one half k-step of both operands in fragment order,
+// 32 KB: the 16 weight fragments (1 KB each, straight from the tiled layout)
+// and the 16 activation fragments (lane (r16, g) of fragment (c, h) holds
 // x[16c + r16][64 ks + 16 g + 8 h .. +7], the k-slots of the weight
 // fragment, gathered by each lane's own 16-byte load).  A direct load puts
 // lane l's 16 bytes at LDS base + 16 l, so one wave-wide load fills one
 // fragment and every fragment read is 64 consecutive 16-byte pieces (no
-// bank conflicts, no swizzle).  Waves 0-3 load the weight fragments, waves
-// 4-7 the activation fragments, four loads each per stage.  Three stages
-// (96 KB) rotate: stage i + 2 is loaded while stage i is multiplied; one
-// barrier per half k-step.  Per k-step the workgroup moves 64 KB for
-// 2 * 256 * 256 * 64 flops, half the bytes per flop of the 256 x 128 tile.
+// bank conflicts, no swizzle).  Loader waves 8-9 load the weight fragments,
+// 10-11 the activation fragments, eight loads each per stage, and do
+// nothing else.  Three stages (96 KB) rotate: stage i + 2 is loaded while
+// stage i is multiplied; one barrier per half k-step, which all 12 waves
+// keep.  Per k-step the workgroup moves 64 KB for 2 * 256 * 256 * 64 flops,
+// half the bytes per flop of the 256 x 128 tile.
 //
-// Measured at the c4 projections (4096 prompt rows; TFLOP/s, this tile /
-// the 256 x 128 tile / hipBLASLt on the same box): in_proj 897 / 679 / 909,
-// q|k|v 790 / 682 / 1109, gate|up (SwiGLU) 1159 / 821 / 1047, out_proj
-// split 3 999 / 691 / 1192, o_proj 793 / 568 / 960, down 1194 / 829 / 1333;
-// the six shapes 1061 us against 1443 us and hipBLASLt's 1013 us, and the
-// sums bit for bit the 256 x 128 tile's.  Tried: 4 waves of 128 x 128 (256
+// Why loader waves: timing copies at gate|up (N 18432, K 2560, 8192 prompt
+// rows; wrong sums) took 307 us with the loads alone, 395 us with the
+// fragment reads and MFMAs alone, and 652-700 us with both in the same
+// waves — almost no overlap, however deep the stage ring (four stages, the
+// same) and even with no fragment reads at all (643 us).  Waves that issue
+// loads and MFMAs both lose MFMA issue time to their loads; with the loads
+// in waves of their own the same sums take 606-641 us (MFMA busy 51 % ->
+// higher; hipBLASLt on the same box 650-690 us).  Two loader waves of 16
+// loads each measured 1-2 % slower than four, wave priorities (either way)
+// changed nothing, whole k-step stages with two slots were slower (674 us).
+//
+// The first form of this tile (8 waves, each loading its share of every
+// stage and multiplying), at the c4 projections (4096 prompt rows; TFLOP/s,
+// that form / the 256 x 128 tile / hipBLASLt on the same box): in_proj
+// 897 / 679 / 909, q|k|v 790 / 682 / 1109, gate|up (SwiGLU) 1159 / 821 /
+// 1047, out_proj split 3 999 / 691 / 1192, o_proj 793 / 568 / 960, down
+// 1194 / 829 / 1333; the six shapes 1061 us against 1443 us and hipBLASLt's
+// 1013 us, and the sums bit for bit the 256 x 128 tile's (as they are with
+// the loader waves).  Tried on that form: 4 waves of 128 x 128 (256
 // accumulator registers a lane: the compiler shuffles them between register
-// files every step), 2 / 4 / 5 stages (1296 / 1075 / 1097 us), bands of 4 /
-// 8 / 16 weight tiles (within 2 %), fragments read a half k-step ahead into
-// a second register set (no gain), whole k-step stages with 8-row
-// activation loads (full 128-byte lines, swizzled rows; 1055 us).  Timing
-// copies with parts removed (wrong sums): no fragment reads 871 us, no
-// MFMAs 842 us, neither 846 us, neither and no activation loads 467 us,
-// neither and no weight loads 681 us.  Yet the whole kernel reading a
-// fragment-tiled copy of the activations (contiguous 1 KB loads, same sums)
-// took 1131 us against 1140: the activation gather is not what bounds it;
-// the per-half-k-step rhythm (stage wait, barrier, fragment reads, 32 MFMAs
-// a wave at two waves a SIMD) is.
+// files every step; with the accumulators held in AGPRs by the MFMA's own
+// operand constraint, one wave a SIMD, 830 us against 712 at gate|up, 8192
+// rows), 2 / 4 / 5 stages (1296 / 1075 / 1097 us), bands of 4 / 8 / 16
+// weight tiles (within 2 %), fragments read a half k-step ahead into a
+// second register set (no gain), whole k-step stages with 8-row activation
+// loads (full 128-byte lines, swizzled rows; 1055 us), the loads spread
+// between groups of 8 MFMAs (9 % slower), half the fragment reads (wrong
+// sums; 2 % faster: the LDS read bandwidth is not what bounds it), and a
+// fragment-tiled copy of the activations (contiguous 1 KB loads, same
+// sums: the loads alone 474 -> 307 us at gate|up, 8192 rows, the kernel
+// unchanged; with the loader waves the same copy measured 3-5 % faster,
+// so the gather costs that much).  Clocks under load (GRBM_GUI_ACTIVE over
+// the dispatch, and rocm-smi during 400 back-to-back calls): that form ran
+// at 1.6-2.2 GHz with the matrix cores busy 51 % of the cycles, hipBLASLt
+// at 1.4-1.8 GHz with them busy 80-86 %: both are held below the 2.4 GHz
+// peak clock by the power drawn, so the busy fraction is what to raise.
 constexpr int kWRows = 256;      // weight rows per workgroup
 constexpr int kWCols = 256;      // activation rows per workgroup
 constexpr int kWStages = 3;      // half k-step stages in LDS
@@ -355,53 +375,59 @@ __device__ __forceinline__ void wait_vm() {
 }
 
 // Stage hs (k-step hs / 2, half hs % 2) into the LDS stage at byte address
-// `st` (weight fragments at +0, activation fragments at +16 KB).  Waves 0-3
-// load weight fragments 4w .. 4w + 3 (row tiles past the weight's last are
-// clamped to it; their sums are never stored), waves 4-7 activation
-// fragments 4(w - 4) .. +3.  off[i]: the lane's byte offset for its i-th
-// load (weight: 16 bytes a lane in lane order; activation: row 16 c + r16,
-// clamped to the last row, k-slot 16 g).  wave, rt0 and m0 are
-// wave-uniform.
+// `st` (weight fragments at +0, activation fragments at +16 KB), by loader
+// wave l (0-3): loaders 0-1 load weight fragments 8l .. 8l + 7 (row tiles
+// past the weight's last are clamped to it; their sums are never stored),
+// loaders 2-3 activation fragments 8(l - 2) .. +7.  off[i]: the lane's byte
+// offset for its i-th load (weight: 16 bytes a lane in lane order;
+// activation: row 16 c + r16, clamped to the last row, k-slot 16 g).  l,
+// rt0 and m0 are wave-uniform.
 __device__ __forceinline__ void wide_load_stage(const PrefillGemmParams& p, int hs, int rt0,
-                                                int m0, int wave, const uint32_t (&off)[4],
+                                                int m0, int l, const uint32_t (&off)[8],
                                                 uint32_t st) {
   const int ks = hs >> 1, h = hs & 1;
-  if (wave < 4) {
+  if (l < 2) {
     const int NT = p.N >> 4;
     const char* wb = reinterpret_cast<const char*>(p.w) + (int64_t)ks * p.nt_w * 2048 + h * 1024;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int f = 4 * wave + i;
+    for (int i = 0; i < 8; ++i) {
+      const int f = 8 * l + i;
       dma16(wb + (int64_t)min(rt0 + f, NT - 1) * 2048, off[i], st + f * 1024);
     }
   } else {
     const char* xb =
         reinterpret_cast<const char*>(p.x) + (int64_t)m0 * p.xs * 2 + ks * 128 + h * 16;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(xb, off[i], st + 16384 + (4 * (wave - 4) + i) * 1024);
+    for (int i = 0; i < 8; ++i) dma16(xb, off[i], st + 16384 + (8 * (l - 2) + i) * 1024);
   }
 }
 
 // One half k-step of the wave's 4 x 8 accumulator tiles from the stage at
 // `st`: weight fragments 4 wr .. 4 wr + 3, activation fragments
-// 8 wc .. 8 wc + 7.
+// 8 wc .. 8 wc + 7, the activation fragments in two halves of four (so a
+// compute wave fits three waves a SIMD: 165 registers).
 __device__ __forceinline__ void wide_mma(const u32x4* st, int wr, int wc, int lane,
                                          f32x4 (&acc)[4][8]) {
-  u32x4 a[4], b[8];
+  u32x4 a[4], b[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) a[i] = st[(4 * wr + i) * 64 + lane];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) b[j] = st[1024 + (8 * wc + j) * 64 + lane];
+  for (int jh = 0; jh < 2; ++jh) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 4; ++j) b[j] = st[1024 + (8 * wc + 4 * jh + j) * 64 + lane];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[i]), as_bf16x8(b[j]),
-                                                          acc[i][j], 0, 0, 0);
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        acc[i][4 * jh + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            as_bf16x8(a[i]), as_bf16x8(b[j]), acc[i][4 * jh + j], 0, 0, 0);
+  }
 }
 
+constexpr int kWThreads = 768;  // 8 compute waves + 4 loader waves
+
 template <bool SWIGLU>
-__global__ __launch_bounds__(512, 1) void prefill_gemm_wide_kernel(const PrefillGemmParams p) {
+__global__ __launch_bounds__(kWThreads, 1) void prefill_gemm_wide_kernel(const PrefillGemmParams p) {
   __shared__ __attribute__((aligned(16))) u32x4 stages[kWStages * kWStageU4];
   const int u = (int)(blockIdx.x & 7) * p.per_xcd + (int)(blockIdx.x >> 3);
   if (u >= p.total) return;
@@ -423,53 +449,64 @@ __global__ __launch_bounds__(512, 1) void prefill_gemm_wide_kernel(const Prefill
   const int hb = 2 * split * p.ks_per_split;  // the unit's first half k-step
   const int nhs = 2 * min(p.ks_per_split, (p.K >> 6) - split * p.ks_per_split);
 
+  const uint32_t l0 = lds_addr(stages);
+
+  // Half k-step i multiplies stage slot i % 3.  Before it, each loader's
+  // loads of stage i must be done (those of stage i + 1 may still be in
+  // flight) and every wave must have passed the barrier, which also frees
+  // slot (i + 2) % 3 = (i - 1) % 3 for stage i + 2: a compute wave reaches
+  // it only after the MFMAs that consumed its reads of that slot.  The
+  // barrier is the bare instruction: its waits are explicit (the stage loads
+  // by count, the fragment reads by the MFMAs that consumed them), where a
+  // workgroup fence would also wait for the loads of the later stage.  Every
+  // wave runs nhs barriers; the loaders then exit and the compute waves store
+  // their sums (no barrier after the loop).
+  if (wave >= 8) {
+    const int l = wave - 8;
+    uint32_t off[8];
+    {
+      const int r16 = lane & 15, g = lane >> 4;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int m = min(m0 + 16 * (8 * (l & 1) + i) + r16, p.M - 1);
+        off[i] = l < 2 ? (uint32_t)(lane * 16)
+                       : (uint32_t)((int64_t)(m - m0) * p.xs * 2) + 32 * g;
+      }
+    }
+    // nhs >= 2 (K >= 64).  Stages 0 and 1 before the loop.
+    wide_load_stage(p, hb, rt0, m0, l, off, l0);
+    wide_load_stage(p, hb + 1, rt0, m0, l, off, l0 + 32768);
+    int fill = 2;  // the slot of stage i + 2
+    for (int i = 0; i < nhs; ++i) {
+      if (i + 1 < nhs) wait_vm<8>();
+      else wait_vm<0>();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (i + 2 < nhs) wide_load_stage(p, hb + i + 2, rt0, m0, l, off, l0 + fill * 32768);
+      fill = fill == 2 ? 0 : fill + 1;
+    }
+    return;
+  }
+
   f32x4 acc[4][8];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  uint32_t off[4];
-  {
-    const int r16 = lane & 15, g = lane >> 4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = min(m0 + 16 * (4 * (wave & 3) + i) + r16, p.M - 1);
-      off[i] = wave < 4 ? (uint32_t)(lane * 16)
-                        : (uint32_t)((int64_t)(m - m0) * p.xs * 2) + 32 * g;
-    }
-  }
-  const uint32_t l0 = lds_addr(stages);
-
-  // nhs >= 2 (K >= 64).  Stages 0 and 1 before the loop.
-  wide_load_stage(p, hb, rt0, m0, wave, off, l0);
-  wide_load_stage(p, hb + 1, rt0, m0, wave, off, l0 + 32768);
-
-  // A wave whose weight row tiles all lie past the weight's last (in the last
-  // weight tile of a launch whose N is not a multiple of 256) loads its share
-  // of every stage and keeps the barriers, but multiplies nothing: its sums
-  // would never be stored.
+  // A compute wave whose weight row tiles all lie past the weight's last (in
+  // the last weight tile of a launch whose N is not a multiple of 256) keeps
+  // the barriers but multiplies nothing: its sums would never be stored.
   const bool live = rt0 + 4 * wr < (p.N >> 4);
-
-  // Half k-step i multiplies stage slot i % 3.  Before it, this wave's loads
-  // of stage i must be done (those of stage i + 1, four, may still be in
-  // flight) and every wave's: the barrier, which also frees slot
-  // (i + 2) % 3 = (i - 1) % 3 for stage i + 2.  The barrier is the bare
-  // instruction: its waits are explicit (the stage loads by count, the
-  // fragment reads by the MFMAs that consumed them), where a workgroup
-  // fence would also wait for the loads of the later stage.
   auto pipeline = [&](auto MMA) {
-    int slot = 0, fill = 2;  // slots of stage i and of stage i + 2
+    int slot = 0;  // the slot of stage i
     for (int i = 0; i < nhs; ++i) {
-      if (i + 1 < nhs) wait_vm<4>();
-      else wait_vm<0>();
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (i + 2 < nhs) wide_load_stage(p, hb + i + 2, rt0, m0, wave, off, l0 + fill * 32768);
       if (decltype(MMA)::value) wide_mma(stages + slot * kWStageU4, wr, wc, lane, acc);
       slot = slot == 2 ? 0 : slot + 1;
-      fill = fill == 2 ? 0 : fill + 1;
     }
   };
   if (live)
@@ -577,9 +614,9 @@ int launch_prefill(const void* x, int64_t x_row_stride, const void* w_tiled, int
   const dim3 grid((unsigned)(8 * p.per_xcd));
   if (wide) {
     if (swiglu)
-      hipLaunchKernelGGL((prefill_gemm_wide_kernel<true>), grid, dim3(512), 0, s, p);
+      hipLaunchKernelGGL((prefill_gemm_wide_kernel<true>), grid, dim3(kWThreads), 0, s, p);
     else
-      hipLaunchKernelGGL((prefill_gemm_wide_kernel<false>), grid, dim3(512), 0, s, p);
+      hipLaunchKernelGGL((prefill_gemm_wide_kernel<false>), grid, dim3(kWThreads), 0, s, p);
   } else if (swiglu) {
     hipLaunchKernelGGL((prefill_gemm_kernel<true, kPDepth, kPSwizzle>), grid, dim3(256), 0, s, p);
   } else {
