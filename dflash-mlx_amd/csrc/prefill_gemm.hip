@@ -293,19 +293,30 @@ __global__ __launch_bounds__(256, 1) void prefill_gemm_kernel(const PrefillGemmP
 // Compute wave w < 8 (wr = w / 2, wc = w % 2) owns weight row tiles
 // 4 wr .. 4 wr + 3 against activation column tiles 8 wc .. 8 wc + 7: 32
 // accumulator tiles, 32 MFMAs per half k-step (32 k), and issues no global
-// load.  A stage is one half k-step of both operands in fragment order,
-// 32 KB: the 16 weight fragments (1 KB each, straight from the tiled layout)
-// and the 16 activation fragments (lane (r16, g) of fragment (c, h) holds
-// x[16c + r16][64 ks + 16 g + 8 h .. +7], the k-slots of the weight
-// fragment, gathered by each lane's own 16-byte load).  A direct load puts
-// lane l's 16 bytes at LDS base + 16 l, so one wave-wide load fills one
-// fragment and every fragment read is 64 consecutive 16-byte pieces (no
-// bank conflicts, no swizzle).  Loader waves 8-9 load the weight fragments,
-// 10-11 the activation fragments, eight loads each per stage, and do
-// nothing else.  Three stages (96 KB) rotate: stage i + 2 is loaded while
-// stage i is multiplied; one barrier per half k-step, which all 12 waves
-// keep.  Per k-step the workgroup moves 64 KB for 2 * 256 * 256 * 64 flops,
-// half the bytes per flop of the 256 x 128 tile.
+// load.  Its fragments: the weight's straight from the tiled layout (lane
+// (r16, g) of fragment (tile, h) holds W[16 tile + r16][64 ks + 16 g + 8 h ..
+// +7]) and the activations' with the same k-slots, x[16 c + r16][64 ks +
+// 16 g + 8 h .. +7].
+//   - Weight stages: one half k-step's 16 fragments (16 KB), loaded by
+//     loader waves 8-9 (eight 1 KB loads each, straight from the tiled
+//     layout); three slots rotate, stage i + 2 loaded while stage i is
+//     multiplied.
+//   - Activation stages: one whole k-step of the 256 rows (32 KB, 128 bytes
+//     a row), loaded by loader waves 10-11 in chunks of 128 rows: each load
+//     takes 8 whole rows (8 lanes a row, 1 KB of whole 128-byte lines) where
+//     a load in fragment order would take 16 rows of half lines (the k-slots
+//     of half h are every other 16 bytes of the row); measured that way in
+//     the prompt pass's own launch order (c4 shapes, 4096 rows, 32 layers)
+//     the GEMMs took 25.9 ms against 23.9 ms now.  In LDS a 1 KB block holds
+//     8 rows, 16-byte piece c of row r at slot 8 r + (c ^ r): the DMA puts
+//     lane l's 16 bytes at slot l, so lane l loads piece (l % 8) ^ (l / 8) of
+//     row l / 8, still 128 contiguous bytes a row; a compute wave's fragment
+//     read (8 consecutive lanes = 8 rows of one piece) then touches 8
+//     different 16-byte bank groups.  Three slots (96 KB): k-step v's two
+//     chunks are issued 4 and 3 half k-steps before v is first multiplied.
+//   - One barrier per half k-step, which all 12 waves keep; LDS 144 KB.
+//     Per k-step the workgroup moves 64 KB for 2 * 256 * 256 * 64 flops,
+//     half the bytes per flop of the 256 x 128 tile.
 //
 // Why loader waves: timing copies at gate|up (N 18432, K 2560, 8192 prompt
 // rows; wrong sums) took 307 us with the loads alone, 395 us with the
@@ -313,41 +324,45 @@ __global__ __launch_bounds__(256, 1) void prefill_gemm_kernel(const PrefillGemmP
 // waves — almost no overlap, however deep the stage ring (four stages, the
 // same) and even with no fragment reads at all (643 us).  Waves that issue
 // loads and MFMAs both lose MFMA issue time to their loads; with the loads
-// in waves of their own the same sums take 606-641 us (MFMA busy 51 % ->
-// higher; hipBLASLt on the same box 650-690 us).  Two loader waves of 16
-// loads each measured 1-2 % slower than four, wave priorities (either way)
-// changed nothing, whole k-step stages with two slots were slower (674 us).
+// in waves of their own the same sums took 606-641 us (hipBLASLt on the
+// same box 650-690 us).  Two loader waves of 16 loads each measured 1-2 %
+// slower than four, wave priorities (either way) changed nothing, whole
+// k-step stages for both operands in two slots were slower (674 us).
+// Isolated back-to-back launches favour the loader waves by 8-17 %; in the
+// prompt pass's launch order (different weights every launch) by ~1 %, and
+// there the activation loads' whole lines are what gained (above): the
+// GEMMs run at a power-held clock (zeroed activations ran the same
+// launches 6 % faster), so fewer cache requests per byte pay.
 //
 // The first form of this tile (8 waves, each loading its share of every
-// stage and multiplying), at the c4 projections (4096 prompt rows; TFLOP/s,
-// that form / the 256 x 128 tile / hipBLASLt on the same box): in_proj
-// 897 / 679 / 909, q|k|v 790 / 682 / 1109, gate|up (SwiGLU) 1159 / 821 /
-// 1047, out_proj split 3 999 / 691 / 1192, o_proj 793 / 568 / 960, down
-// 1194 / 829 / 1333; the six shapes 1061 us against 1443 us and hipBLASLt's
-// 1013 us, and the sums bit for bit the 256 x 128 tile's (as they are with
-// the loader waves).  Tried on that form: 4 waves of 128 x 128 (256
-// accumulator registers a lane: the compiler shuffles them between register
-// files every step; with the accumulators held in AGPRs by the MFMA's own
-// operand constraint, one wave a SIMD, 830 us against 712 at gate|up, 8192
-// rows), 2 / 4 / 5 stages (1296 / 1075 / 1097 us), bands of 4 / 8 / 16
-// weight tiles (within 2 %), fragments read a half k-step ahead into a
-// second register set (no gain), whole k-step stages with 8-row activation
-// loads (full 128-byte lines, swizzled rows; 1055 us), the loads spread
-// between groups of 8 MFMAs (9 % slower), half the fragment reads (wrong
-// sums; 2 % faster: the LDS read bandwidth is not what bounds it), and a
-// fragment-tiled copy of the activations (contiguous 1 KB loads, same
-// sums: the loads alone 474 -> 307 us at gate|up, 8192 rows, the kernel
-// unchanged; with the loader waves the same copy measured 3-5 % faster,
-// so the gather costs that much).  Clocks under load (GRBM_GUI_ACTIVE over
-// the dispatch, and rocm-smi during 400 back-to-back calls): that form ran
-// at 1.6-2.2 GHz with the matrix cores busy 51 % of the cycles, hipBLASLt
-// at 1.4-1.8 GHz with them busy 80-86 %: both are held below the 2.4 GHz
-// peak clock by the power drawn, so the busy fraction is what to raise.
-constexpr int kWRows = 256;      // weight rows per workgroup
-constexpr int kWCols = 256;      // activation rows per workgroup
-constexpr int kWStages = 3;      // half k-step stages in LDS
-constexpr int kWStageU4 = 2048;  // u32x4 per stage (32 KB)
-constexpr int kWGroup = 16;      // weight tiles per band of the tile walk
+// stage and multiplying; activation fragments gathered 16 rows of half
+// lines a load), at the c4 projections (4096 prompt rows; TFLOP/s, that
+// form / the 256 x 128 tile / hipBLASLt on the same box): in_proj 897 / 679
+// / 909, q|k|v 790 / 682 / 1109, gate|up (SwiGLU) 1159 / 821 / 1047, out_proj
+// split 3 999 / 691 / 1192, o_proj 793 / 568 / 960, down 1194 / 829 / 1333;
+// the six shapes 1061 us against 1443 us and hipBLASLt's 1013 us, and the
+// sums bit for bit the 256 x 128 tile's (as they are now).  Tried on that
+// form: 4 waves of 128 x 128 (256 accumulator registers a lane: the
+// compiler shuffles them between register files every step; with the
+// accumulators held in AGPRs by the MFMA's own operand constraint, one wave
+// a SIMD, 830 us against 712 at gate|up, 8192 rows), 2 / 4 / 5 stages
+// (1296 / 1075 / 1097 us), bands of 4 / 8 / 16 weight tiles (within 2 %),
+// fragments read a half k-step ahead into a second register set (no gain),
+// the loads spread between groups of 8 MFMAs (9 % slower), half the
+// fragment reads (wrong sums; 2 % faster: the LDS read bandwidth is not
+// what bounds it).  Clocks under load (GRBM_GUI_ACTIVE over the dispatch,
+// and rocm-smi during 400 back-to-back calls): that form ran at 1.6-2.2 GHz
+// with the matrix cores busy 51 % of the cycles, hipBLASLt at 1.4-1.8 GHz
+// with them busy 80-86 %: both are held below the 2.4 GHz peak clock by the
+// power drawn.
+constexpr int kWRows = 256;                  // weight rows per workgroup
+constexpr int kWCols = 256;                  // activation rows per workgroup
+constexpr int kWGroup = 16;                  // weight tiles per band of the tile walk
+constexpr int kWThreads = 768;               // 8 compute waves + 4 loader waves
+constexpr int kWWeightSlot = 16384;          // bytes: a half k-step's 16 weight fragments
+constexpr int kWActSlot = 32768;             // bytes: a k-step of 256 activation rows
+constexpr int kWActBase = 3 * kWWeightSlot;  // the activation slots follow the weight slots
+constexpr int kWLdsU4 = (kWActBase + 3 * kWActSlot) / 16;  // 144 KB
 
 // The 32-bit LDS address of a workgroup-shared object.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -374,47 +389,45 @@ __device__ __forceinline__ void wait_vm() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Stage hs (k-step hs / 2, half hs % 2) into the LDS stage at byte address
-// `st` (weight fragments at +0, activation fragments at +16 KB), by loader
-// wave l (0-3): loaders 0-1 load weight fragments 8l .. 8l + 7 (row tiles
+// Wait until at most n activation chunks (8 loads each) of this wave are
+// outstanding; n <= 3.
+__device__ __forceinline__ void wait_chunks(int n) {
+  if (n <= 0) wait_vm<0>();
+  else if (n == 1) wait_vm<8>();
+  else if (n == 2) wait_vm<16>();
+  else wait_vm<24>();
+}
+
+// Weight stage hs (k-step hs / 2, half hs % 2) into the slot at LDS byte
+// address `st`, by weight loader l (0-1): fragments 8l .. 8l + 7 (row tiles
 // past the weight's last are clamped to it; their sums are never stored),
-// loaders 2-3 activation fragments 8(l - 2) .. +7.  off[i]: the lane's byte
-// offset for its i-th load (weight: 16 bytes a lane in lane order;
-// activation: row 16 c + r16, clamped to the last row, k-slot 16 g).  l,
-// rt0 and m0 are wave-uniform.
-__device__ __forceinline__ void wide_load_stage(const PrefillGemmParams& p, int hs, int rt0,
-                                                int m0, int l, const uint32_t (&off)[8],
-                                                uint32_t st) {
+// 16 bytes a lane in lane order.  l and rt0 are wave-uniform.
+__device__ __forceinline__ void wide_load_weights(const PrefillGemmParams& p, int hs, int rt0,
+                                                  int l, uint32_t voff, uint32_t st) {
   const int ks = hs >> 1, h = hs & 1;
-  if (l < 2) {
-    const int NT = p.N >> 4;
-    const char* wb = reinterpret_cast<const char*>(p.w) + (int64_t)ks * p.nt_w * 2048 + h * 1024;
+  const int NT = p.N >> 4;
+  const char* wb = reinterpret_cast<const char*>(p.w) + (int64_t)ks * p.nt_w * 2048 + h * 1024;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int f = 8 * l + i;
-      dma16(wb + (int64_t)min(rt0 + f, NT - 1) * 2048, off[i], st + f * 1024);
-    }
-  } else {
-    const char* xb =
-        reinterpret_cast<const char*>(p.x) + (int64_t)m0 * p.xs * 2 + ks * 128 + h * 16;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) dma16(xb, off[i], st + 16384 + (8 * (l - 2) + i) * 1024);
+  for (int i = 0; i < 8; ++i) {
+    const int f = 8 * l + i;
+    dma16(wb + (int64_t)min(rt0 + f, NT - 1) * 2048, voff, st + f * 1024);
   }
 }
 
-// One half k-step of the wave's 4 x 8 accumulator tiles from the stage at
-// `st`: weight fragments 4 wr .. 4 wr + 3, activation fragments
-// 8 wc .. 8 wc + 7, the activation fragments in two halves of four (so a
-// compute wave fits three waves a SIMD: 165 registers).
-__device__ __forceinline__ void wide_mma(const u32x4* st, int wr, int wc, int lane,
-                                         f32x4 (&acc)[4][8]) {
+// One half k-step of the wave's 4 x 8 accumulator tiles: weight fragments
+// 4 wr .. 4 wr + 3 from the weight slot `wst`, activation column tiles
+// 8 wc .. 8 wc + 7 from the activation slot `ast` (tile c's rows are blocks
+// 2c and 2c + 1; boff = the lane's slot for this half, see the kernel), in
+// two halves of four (so a compute wave fits three waves a SIMD).
+__device__ __forceinline__ void wide_mma(const u32x4* wst, const u32x4* ast, int wr, int wc,
+                                         int lane, int boff, f32x4 (&acc)[4][8]) {
   u32x4 a[4], b[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) a[i] = st[(4 * wr + i) * 64 + lane];
+  for (int i = 0; i < 4; ++i) a[i] = wst[(4 * wr + i) * 64 + lane];
 #pragma unroll
   for (int jh = 0; jh < 2; ++jh) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) b[j] = st[1024 + (8 * wc + 4 * jh + j) * 64 + lane];
+    for (int j = 0; j < 4; ++j) b[j] = ast[boff + 2 * (8 * wc + 4 * jh + j) * 64];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -424,11 +437,9 @@ __device__ __forceinline__ void wide_mma(const u32x4* st, int wr, int wc, int la
   }
 }
 
-constexpr int kWThreads = 768;  // 8 compute waves + 4 loader waves
-
 template <bool SWIGLU>
 __global__ __launch_bounds__(kWThreads, 1) void prefill_gemm_wide_kernel(const PrefillGemmParams p) {
-  __shared__ __attribute__((aligned(16))) u32x4 stages[kWStages * kWStageU4];
+  __shared__ __attribute__((aligned(16))) u32x4 lds[kWLdsU4];
   const int u = (int)(blockIdx.x & 7) * p.per_xcd + (int)(blockIdx.x >> 3);
   if (u >= p.total) return;
   // work unit u = split * tiles + t: k-range `split` of output tile t
@@ -446,36 +457,68 @@ __global__ __launch_bounds__(kWThreads, 1) void prefill_gemm_wide_kernel(const P
   const int wr = wave >> 1, wc = wave & 1;
   const int rt0 = (nt * kWRows) >> 4;  // the workgroup's first weight row tile
   const int m0 = mt * kWCols;
-  const int hb = 2 * split * p.ks_per_split;  // the unit's first half k-step
-  const int nhs = 2 * min(p.ks_per_split, (p.K >> 6) - split * p.ks_per_split);
+  const int ks0 = split * p.ks_per_split;  // the unit's first k-step
+  const int hb = 2 * ks0;                  // ... and half k-step
+  const int nhs = 2 * min(p.ks_per_split, (p.K >> 6) - ks0);
+  const uint32_t l0 = lds_addr(lds);
 
-  const uint32_t l0 = lds_addr(stages);
-
-  // Half k-step i multiplies stage slot i % 3.  Before it, each loader's
-  // loads of stage i must be done (those of stage i + 1 may still be in
-  // flight) and every wave must have passed the barrier, which also frees
-  // slot (i + 2) % 3 = (i - 1) % 3 for stage i + 2: a compute wave reaches
-  // it only after the MFMAs that consumed its reads of that slot.  The
-  // barrier is the bare instruction: its waits are explicit (the stage loads
-  // by count, the fragment reads by the MFMAs that consumed them), where a
-  // workgroup fence would also wait for the loads of the later stage.  Every
-  // wave runs nhs barriers; the loaders then exit and the compute waves store
-  // their sums (no barrier after the loop).
-  if (wave >= 8) {
-    const int l = wave - 8;
-    uint32_t off[8];
-    {
-      const int r16 = lane & 15, g = lane >> 4;
+  // Half k-step i multiplies weight slot i % 3 and activation slot
+  // (i / 2) % 3.  Before it each loader's loads of what it needs must be
+  // done and every wave must have passed the barrier, which also frees the
+  // slots read at half k-step i - 1 for what the loaders issue next (a
+  // compute wave reaches the barrier only after the MFMAs that consumed its
+  // reads).  The barrier is the bare instruction: its waits are explicit
+  // (the loads by count, the fragment reads by the MFMAs that consumed
+  // them), where a workgroup fence would also wait for the later loads.
+  // Every wave runs nhs barriers; the loaders then exit and the compute
+  // waves store their sums (no barrier after the loop).
+  if (wave >= 10) {
+    // Activation loader a: chunk j = 2 v + r (the unit's k-step v, rows
+    // 128 r .. 128 r + 127) into activation slot v % 3, blocks 16 r + 8 a ..
+    // +7 of 8 rows each.  Lane l loads piece (l % 8) ^ (l / 8) of the block's
+    // row l / 8 (rows past the last clamped to it; their sums are never
+    // stored).  Chunk j is issued at half k-step j - 4: its slot last held
+    // k-step v - 3, multiplied up to half k-step 2v - 5.
+    const int a = wave - 10;
+    const int piece = (lane & 7) ^ (lane >> 3);
+    uint32_t off0[8], off1[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int m = min(m0 + 16 * (8 * (l & 1) + i) + r16, p.M - 1);
-        off[i] = l < 2 ? (uint32_t)(lane * 16)
-                       : (uint32_t)((int64_t)(m - m0) * p.xs * 2) + 32 * g;
-      }
+    for (int q = 0; q < 8; ++q) {
+      const int row = m0 + 8 * (8 * a + q) + (lane >> 3);
+      off0[q] = (uint32_t)((int64_t)(min(row, p.M - 1) - m0) * p.xs * 2) + 16 * piece;
+      off1[q] = (uint32_t)((int64_t)(min(row + 128, p.M - 1) - m0) * p.xs * 2) + 16 * piece;
     }
-    // nhs >= 2 (K >= 64).  Stages 0 and 1 before the loop.
-    wide_load_stage(p, hb, rt0, m0, l, off, l0);
-    wide_load_stage(p, hb + 1, rt0, m0, l, off, l0 + 32768);
+    const char* xb = reinterpret_cast<const char*>(p.x) + (int64_t)m0 * p.xs * 2;
+    auto chunk = [&](int j) {
+      const int v = j >> 1;
+      const char* src = xb + (int64_t)(ks0 + v) * 128;
+      const uint32_t dst = l0 + kWActBase + (v % 3) * kWActSlot + (16 * (j & 1) + 8 * a) * 1024;
+      if (j & 1) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dma16(src, off1[q], dst + q * 1024);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) dma16(src, off0[q], dst + q * 1024);
+      }
+    };
+    for (int j = 0; j < 4 && j < nhs; ++j) chunk(j);
+    for (int i = 0; i < nhs; ++i) {
+      // chunks issued: min(i + 4, nhs); k-step i / 2 needs chunks < 2 (i / 2) + 2
+      wait_chunks(min(i + 4, nhs) - (2 * (i >> 1) + 2));
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      if (i + 4 < nhs) chunk(i + 4);
+    }
+    return;
+  }
+  if (wave >= 8) {
+    // Weight loader l: its half of weight stage i + 2 after barrier i.
+    // nhs >= 2 (K >= 64): stages 0 and 1 before the loop.
+    const int l = wave - 8;
+    const uint32_t voff = (uint32_t)(lane * 16);
+    wide_load_weights(p, hb, rt0, l, voff, l0);
+    wide_load_weights(p, hb + 1, rt0, l, voff, l0 + kWWeightSlot);
     int fill = 2;  // the slot of stage i + 2
     for (int i = 0; i < nhs; ++i) {
       if (i + 1 < nhs) wait_vm<8>();
@@ -483,7 +526,7 @@ __global__ __launch_bounds__(kWThreads, 1) void prefill_gemm_wide_kernel(const P
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (i + 2 < nhs) wide_load_stage(p, hb + i + 2, rt0, m0, l, off, l0 + fill * 32768);
+      if (i + 2 < nhs) wide_load_weights(p, hb + i + 2, rt0, l, voff, l0 + fill * kWWeightSlot);
       fill = fill == 2 ? 0 : fill + 1;
     }
     return;
@@ -499,14 +542,22 @@ __global__ __launch_bounds__(kWThreads, 1) void prefill_gemm_wide_kernel(const P
   // the last weight tile of a launch whose N is not a multiple of 256) keeps
   // the barriers but multiplies nothing: its sums would never be stored.
   const bool live = rt0 + 4 * wr < (p.N >> 4);
+  // Lane (r16, g) of an activation fragment of half h is piece 2g + h of the
+  // tile's row r16: block r16 / 8 of the tile, slot 8 rr + ((2g + h) ^ rr)
+  // with rr = r16 % 8 (in u32x4 units).
+  const int r16 = lane & 15, g = lane >> 4, rr = r16 & 7;
+  const int boff0 = (r16 >> 3) * 64 + 8 * rr + ((2 * g) ^ rr);
+  const int boff1 = (r16 >> 3) * 64 + 8 * rr + ((2 * g + 1) ^ rr);
   auto pipeline = [&](auto MMA) {
-    int slot = 0;  // the slot of stage i
+    int ws = 0;  // the weight slot of stage i
     for (int i = 0; i < nhs; ++i) {
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      if (decltype(MMA)::value) wide_mma(stages + slot * kWStageU4, wr, wc, lane, acc);
-      slot = slot == 2 ? 0 : slot + 1;
+      const u32x4* ast = lds + (kWActBase + ((i >> 1) % 3) * kWActSlot) / 16;
+      if (decltype(MMA)::value)
+        wide_mma(lds + ws * (kWWeightSlot / 16), ast, wr, wc, lane, (i & 1) ? boff1 : boff0, acc);
+      ws = ws == 2 ? 0 : ws + 1;
     }
   };
   if (live)
@@ -517,7 +568,6 @@ __global__ __launch_bounds__(kWThreads, 1) void prefill_gemm_wide_kernel(const P
   // Epilogue.  Lane (r16, g) of tile (i, j) holds out[m = m0 + 16 (8 wc + j)
   // + r16][n = n0 + 16 i + 4 g .. +3], n0 the wave's first weight row.
   const int n0 = nt * kWRows + wr * 64;
-  const int r16 = lane & 15, g = lane >> 4;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int m = m0 + 16 * (8 * wc + j) + r16;

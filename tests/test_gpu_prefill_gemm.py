@@ -230,11 +230,14 @@ def test_prefill_gemm_row_range(device, M, N, K, row0, rows, swiglu, ns):
         assert ((gr.float() - g1).abs() <= 2 * (2 ** -7) * g1.abs() + 1e-4 * gs).all()
 
 
-def test_prefill_gemm_strided_rows(device):
+@pytest.mark.parametrize("M,N,K", [(200, 528, 320), (2100, 8224, 320)])
+def test_prefill_gemm_strided_rows(device, M, N, K):
     """Activation and output rows with strides larger than K and N (views
-    into wider buffers)."""
-    M, N, K = 200, 528, 320
-    x, w = _inputs(device, M, N, K, seed=11)
+    into wider buffers), on the 256 x 128 tile (200 rows) and the 256 x 256
+    tile (2100 rows: 297 units), whose activation loads take whole rows at
+    the row stride."""
+    print(f"[prefill gemm] strided rows M={M} N={N} K={K}", flush=True)
+    x, w = _inputs(device, M, N, K, seed=11 + M)
     xw = torch.zeros(M, K + 64, dtype=torch.bfloat16, device=device)
     xw[:, 8:8 + K] = x
     xv = xw[:, 8:8 + K]
