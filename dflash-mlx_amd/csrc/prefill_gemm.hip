@@ -350,7 +350,9 @@ __global__ __launch_bounds__(256, 1) void prefill_gemm_kernel(const PrefillGemmP
 // fragments read a half k-step ahead into a second register set (no gain),
 // the loads spread between groups of 8 MFMAs (9 % slower), half the
 // fragment reads (wrong sums; 2 % faster: the LDS read bandwidth is not
-// what bounds it).  Clocks under load (GRBM_GUI_ACTIVE over the dispatch,
+// what bounds it); on the 12-wave form, 32 x 32 x 16 MFMAs over the same
+// bytes (half the operand register reads a flop; a timing copy) ran the
+// prompt pass's launch order 6 % slower.  Clocks under load (GRBM_GUI_ACTIVE over the dispatch,
 // and rocm-smi during 400 back-to-back calls): that form ran at 1.6-2.2 GHz
 // with the matrix cores busy 51 % of the cycles, hipBLASLt at 1.4-1.8 GHz
 // with them busy 80-86 %: both are held below the 2.4 GHz peak clock by the
