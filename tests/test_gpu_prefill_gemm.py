@@ -119,6 +119,25 @@ def test_prefill_gemm_wide_tile_matches_narrow_bits(device, M, N, K, swiglu):
         _check(whole, x.float() @ w.float().t())
 
 
+def test_prefill_gemm_wide_tile_one_short_block(device):
+    """The 256 x 256 tile over fewer than 256 rows (200: its units take one
+    round where the 256 x 128 tile's take two), so the activation loaders
+    clamp rows 200-255 of the block: bit for bit the 128-row slices (the
+    other tile) and within one bf16 rounding of fp32."""
+    M, N, K = 200, 65536, 128
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    wide, narrow = -(-N // 256), -(-N // 256) * 2
+    assert 10 * -(-wide // cus) <= 7 * -(-narrow // cus)
+    print(f"[prefill gemm] wide tile, one short block M={M} N={N} K={K}", flush=True)
+    x, w = _inputs(device, M, N, K, seed=7)
+    wt = _tile(w, device)
+    whole = _prefill(device, x, wt, M, N, K)
+    parts = torch.cat([_prefill(device, x[r:r + 128], wt, min(128, M - r), N, K)
+                       for r in range(0, M, 128)])
+    assert torch.equal(whole, parts)
+    _check(whole, x.float() @ w.float().t())
+
+
 @pytest.mark.parametrize("M,I,K", [(300, 9216, 2560), (5, 16, 64), (129, 272, 192)])
 def test_prefill_gemm_swiglu(device, M, I, K):
     """Gated form over the w_pairs layout (32-row blocks: 16 gate rows, then
@@ -251,7 +270,8 @@ def test_prefill_gemm_strided_rows(device, M, N, K):
     assert torch.isnan(ow[:, :4].float()).all() and torch.isnan(ow[:, 4 + N:].float()).all()
 
 
-@pytest.mark.parametrize("M,N,K,ns", [(4096, 2560, 2048, 3), (300, 272, 640, 4), (17, 16, 64, 2)])
+@pytest.mark.parametrize("M,N,K,ns", [(4096, 2560, 2048, 3), (300, 272, 640, 4), (17, 16, 64, 2),
+                                      (4096, 2560, 192, 3), (4000, 2560, 384, 2)])
 def test_prefill_gemm_splitk(device, M, N, K, ns):
     """Split-K partial sums: dflash_gemm_splits(K, ns) slots, every one
     written, summing to the fp32 reference within 1e-4 of its scale."""
